@@ -1,0 +1,175 @@
+/* psgdk: MI355X (gfx950) kernels for the PSGD-Kron preconditioner update + gradient apply.
+ *
+ * C ABI. Every pointer argument named as device memory is a device address (HIP), every array of pointers
+ * (`const T* const* X`, one entry per problem of a grouped call) is a HOST array of `nb` device addresses. All
+ * matrices are row-major with the given leading dimension (elements). Outputs are caller-allocated. Work is enqueued
+ * on `stream` (NULL = the default stream); no call synchronizes the host, allocates device memory or frees caller
+ * memory. Calls that need scratch memory take (ws, ws_bytes): with ws == NULL they only store the required size in
+ * *ws_bytes and return PSGDK_OK; otherwise *ws_bytes must be at least that size.
+ * Return value: PSGDK_OK or an error code; psgdk_last_error() describes the last error of the calling thread.
+ *
+ * Precision: prec = PSGDK_PREC_F32 multiplies fp32 inputs on the fp32 MFMA path; PSGDK_PREC_BF16 rounds the inputs
+ * of every contraction to bfloat16 (round to nearest even) and multiplies on the bf16 MFMA path. Accumulation and
+ * all outputs are fp32 in both cases. Operand storage dtypes (PSGDK_F32 / PSGDK_BF16) are independent of prec.
+ *
+ * Each entry point names the reference interface (dlyr3/psgd_pro, file:line) whose role it takes.
+ */
+#ifndef PSGDK_H
+#define PSGDK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
+
+#define PSGDK_VERSION 1
+#define PSGDK_MAXB 16 /* problems per grouped call */
+#define PSGDK_NLB_K 32 /* rows of the random start of the norm lower bounds */
+
+enum { PSGDK_OK = 0, PSGDK_EINVAL = 1, PSGDK_ESHAPE = 2, PSGDK_EHIP = 3, PSGDK_EWORKSPACE = 4 };
+enum { PSGDK_F32 = 0, PSGDK_BF16 = 1 };
+enum { PSGDK_PREC_F32 = 0, PSGDK_PREC_BF16 = 1 };
+enum { PSGDK_OUT_UPPER = 0, PSGDK_OUT_MIRROR = 1, PSGDK_OUT_PACKED = 2 };
+enum { PSGDK_FACTOR_NONE = 0, PSGDK_FACTOR_DIAG = 1, PSGDK_FACTOR_DENSE = 2 };
+
+/* Message of the calling thread's last error ("" if none). */
+const char* psgdk_last_error(void);
+/* PSGDK_VERSION of the library. */
+int psgdk_version(void);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Level 1: the kernels behind the reference's custom ops (kernels/ops.py:24-116).
+ * ------------------------------------------------------------------------------------------------------------ */
+
+/* C = A A^T (trans = 0, A is n x k) or A^T A (trans = 1, A is k x n), computing only the upper-triangle tiles.
+ * out_mode PSGDK_OUT_UPPER writes the upper triangle (the strict lower triangle of C is not touched),
+ * PSGDK_OUT_MIRROR the full symmetric matrix, PSGDK_OUT_PACKED the row-major packed upper triangle
+ * (n(n+1)/2 values, row i at i n - i(i-1)/2; ldc ignored).
+ * Replaces cublasSsyrk (kernels/blas.cpp:21-33, psgd::syrk_cublas kernels/ops.py:55-63) and the Triton SYRKs
+ * psgd::syrk / syrk2 / syrk2p (kernels/ops.py:66-109, kernels/k2.py:17-39,48-85,106-137). */
+int psgdk_syrk(int prec, int trans, int out_mode, int64_t n, int64_t k, int a_dtype, int nb,
+               const void* const* A, int64_t lda, float* const* C, int64_t ldc, psgdk_stream_t stream);
+
+/* Symmetric matmul reading S (n x n) from its upper triangle only (the strict lower triangle is never read):
+ * side 0: C (n x p) = S B with B n x p;  side 1: C (p x n) = B S with B p x n.
+ * sign +1: S symmetric; -1: S skew-symmetric (diagonal taken as 0); 0: S upper-triangular (TRMM, see below).
+ * Replaces cublasSsymm side-right / side-left (kernels/blas.cpp:36-65; psgd::symm, psgd::symm_right
+ * kernels/ops.py:45-52,90-97). */
+int psgdk_symm(int prec, int side, int sign, int64_t n, int64_t p, int b_dtype, int nb, const float* const* S,
+               int64_t lds, const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream);
+
+/* C (n x p) = triu(Q) B: Q's strict lower triangle is neither read nor multiplied (k loop starts at the tile's
+ * first row). No reference counterpart beyond the triangle-reading SYMM above; the literal triangular product of
+ * the microbenchmark specification. */
+int psgdk_trmm(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
+               const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream);
+
+/* C (m x n) = alpha op(A) op(B) + beta C, op(X) = X (trans = 0) or X^T (trans = 1); A is m x k (or k x m),
+ * B is k x n (or n x k). The dense contractions of the reference's hot path that have no custom kernel there
+ * (R @ Q and R @ RQ in procrustes_step2, psgd_pro.py:89-90; term1 @ q, psgd_pro.py:135; the exprP chain,
+ * psgd_pro.py:112,123). */
+int psgdk_gemm(int prec, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, int a_dtype,
+               int b_dtype, int nb, const void* const* A, int64_t lda, const void* const* B, int64_t ldb, float beta,
+               float* const* C, int64_t ldc, psgdk_stream_t stream);
+
+/* Squared row norms rn2 (n) and max |A_ij| (*amax, one float per problem) of the symmetric (sign +1) or
+ * skew-symmetric (sign -1) matrix held in the upper triangle of A (n x n, fp32).
+ * Replaces psgd::tri_rownorm2 (kernels/ops.py:34-42, kernels/k1.cu:84-181,297-307). */
+int psgdk_tri_rownorm2(int64_t n, int sign, int nb, const float* const* A, int64_t lda, float* const* rn2,
+                       float* const* amax, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* W (32 x n) = V A_sym, V 32 x n contiguous fp32, A_sym read from the upper triangle of A (sign as above).
+ * Replaces psgd::tri_vmm (kernels/ops.py:24-31, kernels/k1.cu:189-268,282-294). */
+int psgdk_tri_vmm(int64_t n, int sign, int nb, const float* const* V, const float* const* A, int64_t lda,
+                  float* const* W, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* Norm lower bound of the SPD (sign +1) or skew-symmetric (sign -1) matrix held in the upper triangle of A, with
+ * the random start V (32 x n) passed in; out[b] (device, one float) receives the bound. Computed entirely on the
+ * device (no host synchronization).
+ * Replaces norm_lower_bound_spd / _skh (psgd_pro.py:19-65, psgd_pro_fast.py:32-51) and nlb_tri
+ * (kernels/ops.py:124-136, kernels/k1.py:19-33). */
+int psgdk_norm_lower_bound(int64_t n, int sign, int nb, const float* const* A, int64_t lda, const float* const* V,
+                           float* const* out, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* Full symmetric n x n matrix from its row-major packed upper triangle.
+ * Replaces psgd::unpack (kernels/ops.py:112-116, kernels/k2.py:88-103). */
+int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int64_t ldc, psgdk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Level 2: the optimizer step over a group of same-shape parameters. A parameter is viewed as an m x n gradient
+ * (a vector as 1 x n, a scalar as 1 x 1) with one factor kind per dimension.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+typedef struct psgdk_kron2d {
+  int32_t nb;                /* parameters in the group, 1..PSGDK_MAXB */
+  int32_t prec;              /* PSGDK_PREC_* of the contractions */
+  int64_t m, n;              /* gradient shape (row-major, contiguous) */
+  int32_t kind[2];           /* PSGDK_FACTOR_* of dimension 0 (rows) and 1 (columns) */
+  int32_t g_dtype;           /* storage dtype of G */
+  int32_t p_dtype;           /* storage dtype of the parameters (apply) */
+  const void* G[PSGDK_MAXB]; /* gradient (or momentum) m x n */
+  float* Q[2][PSGDK_MAXB];   /* dense: d x d; diagonal: d values; none: unused */
+  float* P[2][PSGDK_MAXB];   /* Q^T Q (dense: full symmetric, or upper triangle with tri bit 1) or q * q */
+  float* L[2][PSGDK_MAXB];   /* one float each: the factor's Lipschitz smoothness EMA */
+} psgdk_kron2d_t;
+
+typedef struct psgdk_update_opts {
+  float lr;       /* lr_preconditioner */
+  float betaL;
+  float damping;
+  float grad_eps; /* eps of the damping scale (torch.finfo(gradient dtype).eps in the reference) */
+  int32_t tri;    /* bit 0: term1 kept as its upper triangle; bit 1: P kept as its upper triangle */
+  int32_t r2;     /* reserved: 0 (procrustes_step2 form) */
+} psgdk_update_opts_t;
+
+typedef struct psgdk_apply_opts {
+  float lr_params;
+  float max_avg_amp;     /* grad_clip_max_amps[0] */
+  float max_element_amp; /* grad_clip_max_amps[1] */
+  int32_t tri;           /* bit 1: P kept as its upper triangle */
+} psgdk_apply_opts_t;
+
+/* One preconditioner update of every parameter in the group: update_2d (psgd_pro_fast.py:168-192), i.e.
+ * update_precond_kron_whiten_q0p5eq1p5 (psgd_pro.py:114-137) with P = Q^T Q cached: Pg = P1 (G + (damping +
+ * grad_eps |G|) noise) P2; per factor: term1 (SYRK or sums of squares), norm lower bound, L EMA, Q update,
+ * Procrustes rotation (psgd_pro.py:71-94); then P refresh. Draws are passed in: noise[b] is m x n N(0,1); V[b]
+ * holds, per dense factor in dimension order, two 32 x d blocks (the SPD bound's start, then the skew bound's).
+ * The balancing coin (psgd_pro.py:138-139) is the caller's (psgdk_kron2d_balance). */
+int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+                        const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* Precondition, clip and update: pre = P1 G P2 (apply_2d, psgd_pro_fast.py:156-161 = precond_grad_kron,
+ * psgd_pro.py:107-112), clip to RMS <= max_avg_amp and |.| <= max_element_amp, param -= lr_params * clipped
+ * (psgd_pro.py:371-381). pre_out[b] / clipped_out[b] (m x n fp32, optional: NULL array or NULL entries) receive
+ * the unclipped and clipped gradients. */
+int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params,
+                       float* const* pre_out, float* const* clipped_out, void* ws, size_t* ws_bytes,
+                       psgdk_stream_t stream);
+
+/* P = Q^T Q (dense) or q * q (diagonal) for the factors selected by factor_mask (bit f = factor f):
+ * gram_2d (psgd_pro_fast.py:164-165,191-192,447-449). tri bit 1: P written as its upper triangle. */
+int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, psgdk_stream_t stream);
+
+/* Balance the factors of the parameters whose flag is set (host array of nb ints): q_f *= gmean / max|q_f|,
+ * gmean = (prod_f max|q_f|)^(1/order) over the group's non-NONE factors, then refresh their P
+ * (balance_kron_precond, psgd_pro.py:96-105; psgd_pro_fast.py:390-397). */
+int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri, void* ws, size_t* ws_bytes,
+                         psgdk_stream_t stream);
+
+/* m = beta m + (1 - beta) g for nb tensors of numel elements (psgd_pro.py:340-341). */
+int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const* mom, const void* const* g,
+                   psgdk_stream_t stream);
+
+/* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
+ * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B. Checks the compiler builtins' lane layout. */
+int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PSGDK_H */

@@ -1,0 +1,135 @@
+"""ctypes binding of libpsgdk.so (include/psgdk.h).
+
+The library is loaded after torch, so that it binds to the HIP runtime torch already loaded (same soname) and works
+on torch's streams and allocations. There is no fallback: when the library is missing, `lib()` raises.
+"""
+import ctypes as C
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("PSGDK_LIB", os.path.join(_HERE, "libpsgdk.so"))
+
+MAXB = 16
+NLB_K = 32
+OK, EINVAL, ESHAPE, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
+F32, BF16 = 0, 1
+PREC_F32, PREC_BF16 = 0, 1
+OUT_UPPER, OUT_MIRROR, OUT_PACKED = 0, 1, 2
+FACTOR_NONE, FACTOR_DIAG, FACTOR_DENSE = 0, 1, 2
+
+_vp = C.c_void_p
+_vpa = C.POINTER(C.c_void_p)  # host array of device pointers
+_i64 = C.c_int64
+_i32 = C.c_int
+_f = C.c_float
+_szp = C.POINTER(C.c_size_t)
+
+
+class Kron2d(C.Structure):
+    _fields_ = [("nb", C.c_int32), ("prec", C.c_int32), ("m", C.c_int64), ("n", C.c_int64),
+                ("kind", C.c_int32 * 2), ("g_dtype", C.c_int32), ("p_dtype", C.c_int32),
+                ("G", C.c_void_p * MAXB), ("Q", (C.c_void_p * MAXB) * 2), ("P", (C.c_void_p * MAXB) * 2),
+                ("L", (C.c_void_p * MAXB) * 2)]
+
+
+class UpdateOpts(C.Structure):
+    _fields_ = [("lr", C.c_float), ("betaL", C.c_float), ("damping", C.c_float), ("grad_eps", C.c_float),
+                ("tri", C.c_int32), ("r2", C.c_int32)]
+
+
+class ApplyOpts(C.Structure):
+    _fields_ = [("lr_params", C.c_float), ("max_avg_amp", C.c_float), ("max_element_amp", C.c_float),
+                ("tri", C.c_int32)]
+
+
+_SIGS = {
+    "psgdk_last_error": (C.c_char_p, []),
+    "psgdk_version": (_i32, []),
+    "psgdk_syrk": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vp]),
+    "psgdk_symm": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vpa, _i64, _vp]),
+    "psgdk_trmm": (_i32, [_i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vpa, _i64, _vp]),
+    "psgdk_gemm": (_i32, [_i32, _i32, _i32, _i64, _i64, _i64, _f, _i32, _i32, _i32, _vpa, _i64, _vpa, _i64, _f,
+                          _vpa, _i64, _vp]),
+    "psgdk_tri_rownorm2": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_tri_vmm": (_i32, [_i64, _i32, _i32, _vpa, _vpa, _i64, _vpa, _vp, _szp, _vp]),
+    "psgdk_norm_lower_bound": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_unpack": (_i32, [_i64, _i32, _vpa, _vpa, _i64, _vp]),
+    "psgdk_kron2d_update": (_i32, [C.POINTER(Kron2d), C.POINTER(UpdateOpts), _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_kron2d_apply": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_kron2d_refresh_p": (_i32, [C.POINTER(Kron2d), _i32, _i32, _vp]),
+    "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
+    "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),
+    "psgdk_debug_mfma": (_i32, [_i32, _vp, _vp, _vp, _vp]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+_lib = None
+
+
+def lib():
+    """The loaded library with typed entry points; raises when it is missing (build it with
+    `python -m psgd_pro_amd.build`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"psgd_pro_amd: {LIB_PATH} not found; build it with `python -m psgd_pro_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        msg = lib().psgdk_last_error().decode()
+        raise RuntimeError(f"psgdk error {rc}: {msg}")
+
+
+def ptrs(seq):
+    """Host array of device addresses for a list of tensors (or ints / None)."""
+    arr = (C.c_void_p * max(1, len(seq)))()
+    for i, t in enumerate(seq):
+        arr[i] = None if t is None else (t if isinstance(t, int) else t.data_ptr())
+    return arr
+
+
+def stream_of(t=None):
+    """The raw handle of torch's current stream on t's device."""
+    dev = t.device if t is not None else None
+    return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def dtype_code(dt):
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {dt}: float32 or bfloat16")
+
+
+class Workspace:
+    """A device byte buffer reused across calls, grown on demand (torch's caching allocator owns it)."""
+
+    def __init__(self):
+        self.buf = None
+
+    def get(self, nbytes, device):
+        nbytes = max(int(nbytes), 256)
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        return self.buf
+
+
+def call_ws(fn, *args, ws, device, stream):
+    """Calls an entry point that takes (..., ws, ws_bytes, stream): queries the size, then runs."""
+    sz = C.c_size_t(0)
+    check(fn(*args, None, C.byref(sz), stream))
+    buf = ws.get(sz.value, device)
+    sz2 = C.c_size_t(buf.numel())
+    check(fn(*args, C.c_void_p(buf.data_ptr()), C.byref(sz2), stream))

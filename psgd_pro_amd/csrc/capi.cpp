@@ -1,0 +1,832 @@
+// The C ABI (include/psgdk.h): argument validation, workspace layout and the sequencing of the grouped kernel
+// launches of each stage. Host code only; every launch goes to the caller's stream, nothing synchronizes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/psgdk.h"
+#include "elem.h"
+#include "gemm.h"
+#include "nlb.h"
+
+namespace psgdk {
+hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
+hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
+}  // namespace psgdk
+
+using namespace psgdk;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(PSGDK_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return PSGDK_OK;
+}
+
+#define PSGDK_TRY(expr)          \
+  do {                           \
+    const int _rc = (expr);      \
+    if (_rc != PSGDK_OK) return _rc; \
+  } while (0)
+#define PSGDK_HIP(expr, what) PSGDK_TRY(hip_check((expr), what))
+
+// Bump allocator over the caller's workspace; with base == nullptr it only measures.
+struct Ws {
+  char* base;
+  size_t off = 0;
+  explicit Ws(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+size_t esize(int dt) { return dt == PSGDK_BF16 ? 2 : 4; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <typename P>
+bool vec_ok(P const* ptrs, int nb, int64_t ld, int dt) {
+  if ((ld * (int64_t)esize(dt)) % 16 != 0) return false;
+  for (int b = 0; b < nb; ++b)
+    if (!aligned16(ptrs[b])) return false;
+  return true;
+}
+
+int check_nb(int nb) {
+  if (nb < 1 || nb > MAXB) return fail(PSGDK_EINVAL, "nb = %d: must be in 1..%d", nb, MAXB);
+  return PSGDK_OK;
+}
+int check_prec(int prec) {
+  if (prec != PSGDK_PREC_F32 && prec != PSGDK_PREC_BF16) return fail(PSGDK_EINVAL, "prec = %d", prec);
+  return PSGDK_OK;
+}
+int check_dt(int dt, const char* name) {
+  if (dt != PSGDK_F32 && dt != PSGDK_BF16) return fail(PSGDK_EINVAL, "%s dtype = %d", name, dt);
+  return PSGDK_OK;
+}
+template <typename P>
+int check_ptrs(P const* ptrs, int nb, const char* name) {
+  if (!ptrs) return fail(PSGDK_EINVAL, "%s: null pointer array", name);
+  for (int b = 0; b < nb; ++b)
+    if (!ptrs[b]) return fail(PSGDK_EINVAL, "%s[%d]: null device pointer", name, b);
+  return PSGDK_OK;
+}
+int check_dims(int64_t v, const char* name) {
+  if (v < 1 || v > (int64_t)1 << 30) return fail(PSGDK_ESHAPE, "%s = %lld out of range", name, (long long)v);
+  return PSGDK_OK;
+}
+
+void gemm_init(GemmArgs& a) {
+  std::memset(&a, 0, sizeof a);
+  a.alpha = 1.f;
+  a.splitk = 1;
+}
+
+// Operand description for the GEMM launcher.
+struct Opnd {
+  int mode = KC, sign = 1, dt = PSGDK_F32;
+  int64_t ld = 0;
+  const void* p[MAXB] = {};
+};
+
+struct EpiSpec {
+  int epi = EPI_STORE;
+  float alpha = 1.f, beta = 0.f;
+  int64_t ldx = 0;
+  const float* X1[MAXB] = {};
+  const float* X2[MAXB] = {};
+  const float* s[MAXB] = {};
+  float* part[MAXB] = {};
+};
+
+int gemm_cfg(int64_t M) { return M <= 32 ? 1 : 0; }
+int gemm_tiles(int64_t M, int64_t N, int tri) {
+  const int cfg = gemm_cfg(M);
+  const int64_t tm = cfg ? (M + 31) / 32 : (M + 127) / 128, tn = (N + 127) / 128;
+  return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
+}
+
+int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, const Opnd& B, float* const* C,
+             int64_t ldc, const EpiSpec& e, int tri, int out_mode, int kbeg_tri, int splitk, int64_t kchunk,
+             hipStream_t st) {
+  GemmArgs a;
+  gemm_init(a);
+  a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.amode = A.mode; a.asign = A.sign; a.lda = A.ld;
+  a.bmode = B.mode; a.bsign = B.sign; a.ldb = B.ld;
+  a.ldc = ldc; a.ldx = e.ldx;
+  a.alpha = e.alpha; a.beta = e.beta; a.epi = e.epi;
+  a.tri = tri; a.out_mode = out_mode; a.kbeg_tri = kbeg_tri;
+  a.splitk = splitk; a.kchunk = (int)(splitk > 1 ? kchunk : K);
+  a.avec = vec_ok(A.p, nb, A.ld, A.dt);
+  a.bvec = vec_ok(B.p, nb, B.ld, B.dt);
+  a.nb = nb;
+  for (int b = 0; b < nb; ++b) {
+    a.A[b] = A.p[b]; a.B[b] = B.p[b]; a.C[b] = C[b];
+    a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
+  }
+  return hip_check(gemm_launch(a, prec, A.dt, B.dt, gemm_cfg(M), st), "gemm launch");
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Norm lower bound pipeline (see nlb.hip). full = the matrix is stored in full (read by contiguous loads);
+// otherwise only its upper triangle is read.
+struct NlbWs {
+  float *vb0[MAXB], *vb1[MAXB], *part[MAXB], *ss0[MAXB], *ss1[MAXB];
+  float *rpart[MAXB], *cpart[MAXB], *tmax[MAXB], *dmax[MAXB], *rn2[MAXB], *scal[MAXB];
+  int splits;
+  int64_t kchunk;
+};
+
+void nlb_plan(int64_t n, int nb, int& splits, int64_t& kchunk) {
+  const int tiles = (int)((n + 127) / 128);
+  int s = (512 + tiles * nb - 1) / (tiles * nb);
+  const int maxs = (int)std::max<int64_t>(1, (n + 63) / 64);
+  s = std::max(1, std::min(s, maxs));
+  kchunk = ((n + s - 1) / s + 63) / 64 * 64;
+  splits = (int)((n + kchunk - 1) / kchunk);
+}
+
+void nlb_take(Ws& w, int64_t n, int nb, NlbWs& o) {
+  nlb_plan(n, nb, o.splits, o.kchunk);
+  const int64_t T = (n + 63) / 64, nbk = T, ntri = T * (T + 1) / 2;
+  for (int b = 0; b < nb; ++b) {
+    o.vb0[b] = w.take<float>(NLB_K * n);
+    o.vb1[b] = w.take<float>(NLB_K * n);
+    o.part[b] = w.take<float>((size_t)o.splits * NLB_K * n);
+    o.ss0[b] = w.take<float>(NLB_K * nbk);
+    o.ss1[b] = w.take<float>(NLB_K * nbk);
+    o.rpart[b] = w.take<float>((size_t)T * T * 64);
+    o.cpart[b] = w.take<float>((size_t)T * 64);
+    o.tmax[b] = w.take<float>(ntri);
+    o.dmax[b] = w.take<float>(ntri);
+    o.rn2[b] = w.take<float>(n);
+    o.scal[b] = w.take<float>(NLB_NSCAL);
+  }
+}
+
+NlbArgs nlb_args(int64_t n, int sign, int nb, const float* const* A, int64_t lda, const NlbWs& w) {
+  NlbArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.n = (int)n; a.T = (int)((n + 63) / 64); a.sign = sign; a.splits = w.splits; a.lda = lda;
+  for (int b = 0; b < nb; ++b) {
+    a.A[b] = A[b];
+    a.rpart[b] = w.rpart[b]; a.cpart[b] = w.cpart[b]; a.tmax[b] = w.tmax[b]; a.dmax[b] = w.dmax[b];
+    a.rn2[b] = w.rn2[b]; a.scal[b] = w.scal[b]; a.part[b] = w.part[b];
+  }
+  return a;
+}
+
+// One V A_sym product into the split partials.
+int nlb_vmm(int64_t n, int sign, int nb, const float* const* A, int64_t lda, bool full, float* const* Vin,
+            const NlbWs& w, hipStream_t st) {
+  Opnd oa, ob;
+  oa.mode = KC; oa.ld = n;
+  for (int b = 0; b < nb; ++b) { oa.p[b] = Vin[b]; ob.p[b] = A[b]; }
+  ob.ld = lda;
+  if (full) { ob.mode = MC; } else { ob.mode = SYM; ob.sign = sign; }
+  EpiSpec e;
+  float* C[MAXB];
+  for (int b = 0; b < nb; ++b) C[b] = w.part[b];
+  return run_gemm(PSGDK_PREC_F32, nb, NLB_K, n, n, oa, ob, C, n, e, 0, 0, 0, w.splits, w.kchunk, st);
+}
+
+int run_nlb(int64_t n, int sign, int nb, const float* const* A, int64_t lda, bool full, const float* const* V,
+            const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
+  NlbArgs a = nlb_args(n, sign, nb, A, lda, w);
+  PSGDK_HIP(nlb_rownorm_launch(a, st), "tri_rownorm");
+  for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
+  PSGDK_HIP(nlb_init_launch(a, st), "nlb_init");
+  float* const* vb[2] = {w.vb0, w.vb1};
+  float* const* ss[2] = {w.ss0, w.ss1};
+  // V1 = V0 A / nf; V2 = (V1/|V1|) A / nf; V3 = V2 A / nf; V4 = (V3/|V3|) A / nf
+  int cur = 0;
+  for (int it = 0; it < 4; ++it) {
+    PSGDK_TRY(nlb_vmm(n, sign, nb, A, lda, full, vb[cur], w, st));
+    const int normalize = it & 1;
+    for (int b = 0; b < nb; ++b) {
+      a.Vout[b] = vb[cur ^ 1][b];
+      a.ssin[b] = ss[0][b];
+      a.ssout[b] = ss[normalize][b];
+    }
+    PSGDK_HIP(nlb_reduce_launch(a, normalize, st), "nlb_reduce");
+    cur ^= 1;
+  }
+  for (int b = 0; b < nb; ++b) a.ssin[b] = ss[1][b];
+  PSGDK_HIP(nlb_final_launch(a, fin, st), "nlb_final");
+  return PSGDK_OK;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Kron 2-D group helpers
+
+int check_group(const psgdk_kron2d_t* g) {
+  if (!g) return fail(PSGDK_EINVAL, "null group");
+  PSGDK_TRY(check_nb(g->nb));
+  PSGDK_TRY(check_prec(g->prec));
+  PSGDK_TRY(check_dims(g->m, "m"));
+  PSGDK_TRY(check_dims(g->n, "n"));
+  PSGDK_TRY(check_dt(g->g_dtype, "G"));
+  PSGDK_TRY(check_dt(g->p_dtype, "param"));
+  const int64_t d[2] = {g->m, g->n};
+  for (int f = 0; f < 2; ++f) {
+    const int k = g->kind[f];
+    if (k != PSGDK_FACTOR_NONE && k != PSGDK_FACTOR_DIAG && k != PSGDK_FACTOR_DENSE)
+      return fail(PSGDK_EINVAL, "kind[%d] = %d", f, k);
+    if (k == PSGDK_FACTOR_NONE && d[f] != 1) return fail(PSGDK_ESHAPE, "factor %d is NONE but its size is %lld", f, (long long)d[f]);
+    if (k != PSGDK_FACTOR_NONE) {
+      PSGDK_TRY(check_ptrs(g->Q[f], g->nb, "Q"));
+      PSGDK_TRY(check_ptrs(g->P[f], g->nb, "P"));
+      PSGDK_TRY(check_ptrs(g->L[f], g->nb, "L"));
+    }
+  }
+  PSGDK_TRY(check_ptrs(g->G, g->nb, "G"));
+  return PSGDK_OK;
+}
+
+int64_t dense_max(const psgdk_kron2d_t* g) {
+  int64_t d = 0;
+  if (g->kind[0] == PSGDK_FACTOR_DENSE) d = std::max(d, g->m);
+  if (g->kind[1] == PSGDK_FACTOR_DENSE) d = std::max(d, g->n);
+  return d;
+}
+
+// out = P1 X P2 over the factor kinds (dense: GEMM with P; diagonal: scaling by q * q; none: identity).
+// tmp: m x n scratch. With part non-null, sum-of-squares partials of out are written there and their count to
+// *npart.
+int precondition(const psgdk_kron2d_t* g, const void* const* X, int xdt, float* const* tmp, float* const* out,
+                 float* const* part, int ptri, int* npart, hipStream_t st) {
+  const int nb = g->nb, k0 = g->kind[0], k1 = g->kind[1];
+  const int64_t m = g->m, n = g->n;
+  *npart = 0;
+  const void* cur[MAXB];
+  int curdt = xdt;
+  for (int b = 0; b < nb; ++b) cur[b] = X[b];
+  bool sumsq_done = false;
+  float* const* dst1 = k1 != PSGDK_FACTOR_NONE ? tmp : out;
+  // rows: P1 X
+  if (k0 == PSGDK_FACTOR_DENSE) {
+    Opnd A, B;
+    if (ptri & 2) { A.mode = SYM; A.sign = 1; } else { A.mode = KC; }
+    A.ld = m;
+    B.mode = MC; B.ld = n; B.dt = curdt;
+    for (int b = 0; b < nb; ++b) { A.p[b] = g->P[0][b]; B.p[b] = cur[b]; }
+    EpiSpec e;
+    if (k1 == PSGDK_FACTOR_NONE && part) {
+      e.epi = EPI_SUMSQ;
+      for (int b = 0; b < nb; ++b) e.part[b] = part[b];
+      sumsq_done = true;
+      *npart = gemm_tiles(m, n, 0);
+    }
+    PSGDK_TRY(run_gemm(g->prec, nb, m, n, m, A, B, dst1, n, e, 0, 0, 0, 1, 0, st));
+    curdt = PSGDK_F32;
+    for (int b = 0; b < nb; ++b) cur[b] = dst1[b];
+  } else if (k0 == PSGDK_FACTOR_DIAG || k1 == PSGDK_FACTOR_NONE) {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = curdt;
+    for (int b = 0; b < nb; ++b) {
+      a.in[b] = cur[b];
+      a.in2[b] = k0 == PSGDK_FACTOR_DIAG ? g->P[0][b] : nullptr;
+      a.out[b] = dst1[b];
+    }
+    PSGDK_HIP(diag_scale_launch(a, st), "diag_scale rows");
+    curdt = PSGDK_F32;
+    for (int b = 0; b < nb; ++b) cur[b] = dst1[b];
+  }
+  // columns: (.) P2
+  if (k1 == PSGDK_FACTOR_DENSE) {
+    Opnd A, B;
+    A.mode = KC; A.ld = n; A.dt = curdt;
+    if (ptri & 2) { B.mode = SYM; B.sign = 1; } else { B.mode = KC; }
+    B.ld = n;
+    for (int b = 0; b < nb; ++b) { A.p[b] = cur[b]; B.p[b] = g->P[1][b]; }
+    EpiSpec e;
+    if (part) {
+      e.epi = EPI_SUMSQ;
+      for (int b = 0; b < nb; ++b) e.part[b] = part[b];
+      sumsq_done = true;
+      *npart = gemm_tiles(m, n, 0);
+    }
+    PSGDK_TRY(run_gemm(g->prec, nb, m, n, n, A, B, out, n, e, 0, 0, 0, 1, 0, st));
+  } else if (k1 == PSGDK_FACTOR_DIAG) {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = curdt;
+    for (int b = 0; b < nb; ++b) { a.in[b] = cur[b]; a.in3[b] = g->P[1][b]; a.out[b] = out[b]; }
+    PSGDK_HIP(diag_scale_launch(a, st), "diag_scale cols");
+  }
+  if (part && !sumsq_done) {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n;
+    a.i0 = (int)std::min<int64_t>(256, std::max<int64_t>(1, (m * n + 2047) / 2048));
+    for (int b = 0; b < nb; ++b) { a.in[b] = out[b]; a.out[b] = part[b]; }
+    PSGDK_HIP(sumsq_launch(a, st), "sumsq");
+    *npart = a.i0;
+  }
+  return PSGDK_OK;
+}
+
+int refresh_p_dense(const psgdk_kron2d_t* g, int f, int tri, const int* sel, int nsel, hipStream_t st) {
+  const int64_t d = f == 0 ? g->m : g->n;
+  Opnd A;
+  A.mode = MC; A.ld = d;
+  float* C[MAXB];
+  for (int i = 0; i < nsel; ++i) { A.p[i] = g->Q[f][sel[i]]; C[i] = g->P[f][sel[i]]; }
+  EpiSpec e;
+  return run_gemm(g->prec, nsel, d, d, d, A, A, C, d, e, 1, (tri & 2) ? PSGDK_OUT_UPPER : PSGDK_OUT_MIRROR, 0, 1, 0, st);
+}
+
+int refresh_p_diag(const psgdk_kron2d_t* g, int f, const int* sel, int nsel, hipStream_t st) {
+  const int64_t d = f == 0 ? g->m : g->n;
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nsel; a.m = 1; a.n = d; a.dt = PSGDK_F32;
+  for (int i = 0; i < nsel; ++i) { a.in[i] = g->Q[f][sel[i]]; a.in3[i] = g->Q[f][sel[i]]; a.out[i] = g->P[f][sel[i]]; }
+  return hip_check(diag_scale_launch(a, st), "diag P refresh");
+}
+
+}  // namespace
+
+// ==============================================================================================================
+extern "C" {
+
+const char* psgdk_last_error(void) { return g_err.c_str(); }
+int psgdk_version(void) { return PSGDK_VERSION; }
+
+int psgdk_syrk(int prec, int trans, int out_mode, int64_t n, int64_t k, int a_dtype, int nb, const void* const* A,
+               int64_t lda, float* const* C, int64_t ldc, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_dt(a_dtype, "A"));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_dims(k, "k"));
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(C, nb, "C"));
+  if (out_mode < 0 || out_mode > 2) return fail(PSGDK_EINVAL, "out_mode = %d", out_mode);
+  if (lda < (trans ? n : k)) return fail(PSGDK_ESHAPE, "lda = %lld too small", (long long)lda);
+  if (out_mode != PSGDK_OUT_PACKED && ldc < n) return fail(PSGDK_ESHAPE, "ldc = %lld < n", (long long)ldc);
+  Opnd a;
+  a.mode = trans ? MC : KC; a.ld = lda; a.dt = a_dtype;
+  for (int b = 0; b < nb; ++b) a.p[b] = A[b];
+  EpiSpec e;
+  return run_gemm(prec, nb, n, n, k, a, a, C, out_mode == PSGDK_OUT_PACKED ? n : ldc, e, 1, out_mode, 0, 1, 0,
+                  (hipStream_t)stream);
+}
+
+int psgdk_symm(int prec, int side, int sign, int64_t n, int64_t p, int b_dtype, int nb, const float* const* S,
+               int64_t lds, const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_dt(b_dtype, "B"));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_dims(p, "p"));
+  PSGDK_TRY(check_ptrs(S, nb, "S"));
+  PSGDK_TRY(check_ptrs(B, nb, "B"));
+  PSGDK_TRY(check_ptrs(C, nb, "C"));
+  if (sign < -1 || sign > 1) return fail(PSGDK_EINVAL, "sign = %d", sign);
+  if (lds < n) return fail(PSGDK_ESHAPE, "lds < n");
+  Opnd os, ob;
+  os.mode = SYM; os.sign = sign; os.ld = lds;
+  for (int b = 0; b < nb; ++b) { os.p[b] = S[b]; ob.p[b] = B[b]; }
+  ob.dt = b_dtype; ob.ld = ldb;
+  EpiSpec e;
+  if (side == 0) {  // C (n x p) = S B: A = S, B operand rows p read B[k][j] (mn-contiguous)
+    if (ldb < p || ldc < p) return fail(PSGDK_ESHAPE, "ldb/ldc < p");
+    ob.mode = MC;
+    return run_gemm(prec, nb, n, p, n, os, ob, C, ldc, e, 0, 0, sign == 0, 1, 0, (hipStream_t)stream);
+  }
+  if (side != 1) return fail(PSGDK_EINVAL, "side = %d", side);
+  if (sign == 0) return fail(PSGDK_EINVAL, "side 1 with sign 0 (right TRMM) is not provided");
+  // C (p x n) = B S: A = B (k-contiguous rows), B operand X[j][k] = S[k][j] = sign * S_sym[j][k]
+  if (ldb < n || ldc < n) return fail(PSGDK_ESHAPE, "ldb/ldc < n");
+  ob.mode = KC;
+  e.alpha = (float)sign;
+  return run_gemm(prec, nb, p, n, n, ob, os, C, ldc, e, 0, 0, 0, 1, 0, (hipStream_t)stream);
+}
+
+int psgdk_trmm(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
+               const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream) {
+  return psgdk_symm(prec, 0, 0, n, p, b_dtype, nb, Q, ldq, B, ldb, C, ldc, stream);
+}
+
+int psgdk_gemm(int prec, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, int a_dtype,
+               int b_dtype, int nb, const void* const* A, int64_t lda, const void* const* B, int64_t ldb, float beta,
+               float* const* C, int64_t ldc, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_dt(a_dtype, "A"));
+  PSGDK_TRY(check_dt(b_dtype, "B"));
+  PSGDK_TRY(check_dims(m, "m"));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_dims(k, "k"));
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(B, nb, "B"));
+  PSGDK_TRY(check_ptrs(C, nb, "C"));
+  if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldc < n) return fail(PSGDK_ESHAPE, "leading dimension too small");
+  Opnd oa, ob;
+  oa.mode = trans_a ? MC : KC; oa.ld = lda; oa.dt = a_dtype;
+  ob.mode = trans_b ? KC : MC; ob.ld = ldb; ob.dt = b_dtype;
+  for (int b = 0; b < nb; ++b) { oa.p[b] = A[b]; ob.p[b] = B[b]; }
+  EpiSpec e;
+  e.alpha = alpha; e.beta = beta;
+  return run_gemm(prec, nb, m, n, k, oa, ob, C, ldc, e, 0, 0, 0, 1, 0, (hipStream_t)stream);
+}
+
+int psgdk_tri_rownorm2(int64_t n, int sign, int nb, const float* const* A, int64_t lda, float* const* rn2,
+                       float* const* amax, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(n, "n"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  Ws w(ws);
+  NlbWs nw;
+  nlb_take(w, n, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(rn2, nb, "rn2"));
+  PSGDK_TRY(check_ptrs(amax, nb, "amax"));
+  if (sign != 1 && sign != -1) return fail(PSGDK_EINVAL, "sign = %d", sign);
+  if (lda < n) return fail(PSGDK_ESHAPE, "lda < n");
+  NlbArgs a = nlb_args(n, sign, nb, A, lda, nw);
+  for (int b = 0; b < nb; ++b) { a.rn2[b] = rn2[b]; a.amax_out[b] = amax[b]; a.Vin[b] = nullptr; }
+  hipStream_t st = (hipStream_t)stream;
+  PSGDK_HIP(nlb_rownorm_launch(a, st), "tri_rownorm");
+  PSGDK_HIP(nlb_init_launch(a, st), "rownorm reduce");
+  return PSGDK_OK;
+}
+
+int psgdk_tri_vmm(int64_t n, int sign, int nb, const float* const* V, const float* const* A, int64_t lda,
+                  float* const* W, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(n, "n"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  int splits;
+  int64_t kchunk;
+  nlb_plan(n, nb, splits, kchunk);
+  Ws w(ws);
+  float* part[MAXB];
+  for (int b = 0; b < nb; ++b) part[b] = w.take<float>((size_t)splits * NLB_K * n);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(W, nb, "W"));
+  if (sign != 1 && sign != -1) return fail(PSGDK_EINVAL, "sign = %d", sign);
+  if (lda < n) return fail(PSGDK_ESHAPE, "lda < n");
+  hipStream_t st = (hipStream_t)stream;
+  Opnd oa, ob;
+  oa.mode = KC; oa.ld = n;
+  ob.mode = SYM; ob.sign = sign; ob.ld = lda;
+  for (int b = 0; b < nb; ++b) { oa.p[b] = V[b]; ob.p[b] = A[b]; }
+  EpiSpec e;
+  e.alpha = (float)sign;  // X[j][k] = A_sym[k][j] = sign * A_sym[j][k]
+  PSGDK_TRY(run_gemm(PSGDK_PREC_F32, nb, NLB_K, n, n, oa, ob, part, n, e, 0, 0, 0, splits, kchunk, st));
+  EwArgs s;
+  std::memset(&s, 0, sizeof s);
+  s.nb = nb; s.m = NLB_K; s.n = n; s.i0 = splits;
+  for (int b = 0; b < nb; ++b) { s.in2[b] = part[b]; s.out[b] = W[b]; }
+  return hip_check(splitk_sum_launch(s, st), "split-k sum");
+}
+
+int psgdk_norm_lower_bound(int64_t n, int sign, int nb, const float* const* A, int64_t lda, const float* const* V,
+                           float* const* out, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(n, "n"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  Ws w(ws);
+  NlbWs nw;
+  nlb_take(w, n, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  PSGDK_TRY(check_ptrs(out, nb, "out"));
+  if (sign != 1 && sign != -1) return fail(PSGDK_EINVAL, "sign = %d", sign);
+  if (lda < n) return fail(PSGDK_ESHAPE, "lda < n");
+  hipStream_t st = (hipStream_t)stream;
+  NlbFinal fin;
+  std::memset(&fin, 0, sizeof fin);
+  fin.mode = NLB_FINAL_NONE;
+  PSGDK_TRY(run_nlb(n, sign, nb, A, lda, false, V, fin, nw, st));
+  for (int b = 0; b < nb; ++b)
+    PSGDK_HIP(hipMemcpyAsync(out[b], nw.scal[b] + NLB_BOUND, sizeof(float), hipMemcpyDeviceToDevice, st), "copy bound");
+  return PSGDK_OK;
+}
+
+int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int64_t ldc, psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_ptrs(Pk, nb, "Pk"));
+  PSGDK_TRY(check_ptrs(C, nb, "C"));
+  if (ldc < n) return fail(PSGDK_ESHAPE, "ldc < n");
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.n = n; a.ld = ldc;
+  for (int b = 0; b < nb; ++b) { a.in2[b] = Pk[b]; a.out[b] = C[b]; }
+  return hip_check(unpack_launch(a, (hipStream_t)stream), "unpack");
+}
+
+// ------------------------------------------------------------------------------------------------------------
+int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+                        const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_group(g));
+  if (!o) return fail(PSGDK_EINVAL, "null options");
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  if (o->r2) return fail(PSGDK_EINVAL, "r2 is not provided by this version");
+  const int nb = g->nb;
+  const int64_t m = g->m, n = g->n, mn = m * n, dmx = dense_max(g);
+  const int64_t dims[2] = {m, n};
+  Ws w(ws);
+  float *X[MAXB], *Y[MAXB], *Pg[MAXB], *T1[MAXB], *Qn[MAXB], *R[MAXB], *RQ[MAXB];
+  float *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *dterm[MAXB];
+  const int tp = dmx ? gemm_tiles(dmx, dmx, 0) : 1;
+  for (int b = 0; b < nb; ++b) {
+    X[b] = w.take<float>(mn);
+    Y[b] = w.take<float>(mn);
+    Pg[b] = w.take<float>(mn);
+    T1[b] = w.take<float>(dmx * dmx);
+    Qn[b] = w.take<float>(dmx * dmx);
+    R[b] = w.take<float>(dmx * dmx);
+    RQ[b] = w.take<float>(dmx * dmx);
+    coef[b] = w.take<float>(4);
+    rs[b] = w.take<float>(4);
+    pc[b] = w.take<float>(4);
+    tpart[b] = w.take<float>(2 * (size_t)tp);
+    dterm[b] = w.take<float>(std::max(m, n));
+  }
+  NlbWs nw;
+  if (dmx) nlb_take(w, dmx, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(noise, nb, "noise"));
+  if (dmx) PSGDK_TRY(check_ptrs(V, nb, "V"));
+  hipStream_t st = (hipStream_t)stream;
+
+  // X = G + (damping + eps |G|) N   (psgd_pro.py:121-123)
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = o->damping; a.f1 = o->grad_eps;
+    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[b]; a.out[b] = X[b]; }
+    PSGDK_HIP(noise_launch(a, st), "noise");
+  }
+  // Pg = P1 X P2
+  int np = 0;
+  {
+    const void* Xc[MAXB];
+    for (int b = 0; b < nb; ++b) Xc[b] = X[b];
+    PSGDK_TRY(precondition(g, Xc, PSGDK_F32, Y, Pg, nullptr, o->tri, &np, st));
+  }
+  const float term_numel = (float)mn;
+  int64_t voff = 0;
+  for (int f = 0; f < 2; ++f) {
+    const int kind = g->kind[f];
+    const int64_t d = dims[f], other = dims[1 - f];
+    const float term2 = term_numel / (float)d;
+    if (kind == PSGDK_FACTOR_DIAG) {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = m; a.n = n; a.i0 = f;
+      for (int b = 0; b < nb; ++b) { a.in[b] = Pg[b]; a.out[b] = dterm[b]; }
+      PSGDK_HIP(diag_term1_launch(a, st), "diag term1");
+      EwArgs u;
+      std::memset(&u, 0, sizeof u);
+      u.nb = nb; u.m = d; u.f0 = o->lr; u.f1 = o->betaL; u.f2 = term2;
+      for (int b = 0; b < nb; ++b) { u.in2[b] = dterm[b]; u.out[b] = g->Q[f][b]; u.out2[b] = g->P[f][b]; u.sc[b] = g->L[f][b]; }
+      PSGDK_HIP(diag_update_launch(u, st), "diag update");
+      continue;
+    }
+    if (kind != PSGDK_FACTOR_DENSE) continue;
+    const int term_tri = o->tri & 1;
+    // term1 = Pg Pg^T (f = 0) or Pg^T Pg (f = 1)   (psgd_pro.py:125)
+    {
+      Opnd a;
+      a.mode = f == 0 ? KC : MC; a.ld = n;
+      for (int b = 0; b < nb; ++b) a.p[b] = Pg[b];
+      EpiSpec e;
+      PSGDK_TRY(run_gemm(g->prec, nb, d, d, other, a, a, T1, d, e, 1,
+                         term_tri ? PSGDK_OUT_UPPER : PSGDK_OUT_MIRROR, 0, 1, 0, st));
+    }
+    // ell = nlb(term1) + term2; L = max(beta L + (1 - beta) ell, ell)   (psgd_pro.py:132-134)
+    const float* Vs[MAXB];
+    const float* Vk[MAXB];
+    for (int b = 0; b < nb; ++b) { Vs[b] = V[b] + voff; Vk[b] = V[b] + voff + NLB_K * d; }
+    voff += 2 * NLB_K * d;
+    {
+      NlbFinal fin;
+      std::memset(&fin, 0, sizeof fin);
+      fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL; fin.term2 = term2;
+      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; }
+      const float* T1c[MAXB];
+      for (int b = 0; b < nb; ++b) T1c[b] = T1[b];
+      PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, !term_tri, Vs, fin, nw, st));
+    }
+    // Qn = Q - lr/L (term1 Q - term2 Q)   (psgd_pro.py:135)
+    {
+      Opnd a, bq;
+      if (term_tri) { a.mode = SYM; a.sign = 1; } else { a.mode = KC; }
+      a.ld = d;
+      bq.mode = MC; bq.ld = d;
+      EpiSpec e;
+      e.epi = EPI_FACTOR; e.ldx = d;
+      for (int b = 0; b < nb; ++b) { a.p[b] = T1[b]; bq.p[b] = g->Q[f][b]; e.X1[b] = g->Q[f][b]; e.s[b] = coef[b]; }
+      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, Qn, d, e, 0, 0, 0, 1, 0, st));
+    }
+    // Procrustes step on Qn (psgd_pro.py:71-94): R = Qn^T - Qn, R /= nlb_skh(R) + sn, RQ = R Qn, RRQ = R RQ,
+    // a from the traces, Q = Qn + a (RQ + a/2 RRQ)
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
+      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out[b] = R[b]; }
+      PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
+    }
+    {
+      NlbFinal fin;
+      std::memset(&fin, 0, sizeof fin);
+      fin.mode = NLB_FINAL_SCALE;
+      for (int b = 0; b < nb; ++b) fin.coef[b] = rs[b];
+      const float* Rc[MAXB];
+      for (int b = 0; b < nb; ++b) Rc[b] = R[b];
+      PSGDK_TRY(run_nlb(d, -1, nb, Rc, d, true, Vk, fin, nw, st));
+    }
+    {
+      Opnd a, bq;
+      a.mode = KC; a.ld = d;
+      bq.mode = MC; bq.ld = d;
+      EpiSpec e;
+      e.epi = EPI_RQ; e.ldx = d;
+      for (int b = 0; b < nb; ++b) { a.p[b] = R[b]; bq.p[b] = Qn[b]; e.X1[b] = R[b]; e.s[b] = rs[b]; e.part[b] = tpart[b]; }
+      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, RQ, d, e, 0, 0, 0, 1, 0, st));
+    }
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.i0 = gemm_tiles(d, d, 0); a.f0 = 0.125f;
+      for (int b = 0; b < nb; ++b) { a.in2[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
+      PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
+    }
+    {
+      Opnd a, bq;
+      a.mode = KC; a.ld = d;
+      bq.mode = MC; bq.ld = d;
+      EpiSpec e;
+      e.epi = EPI_PROC; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        a.p[b] = R[b]; bq.p[b] = RQ[b]; e.X1[b] = Qn[b]; e.X2[b] = RQ[b]; e.s[b] = pc[b];
+      }
+      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, g->Q[f], d, e, 0, 0, 0, 1, 0, st));
+    }
+  }
+  // P refresh (psgd_pro_fast.py:191-192)
+  int sel[MAXB];
+  for (int b = 0; b < nb; ++b) sel[b] = b;
+  for (int f = 0; f < 2; ++f)
+    if (g->kind[f] == PSGDK_FACTOR_DENSE) PSGDK_TRY(refresh_p_dense(g, f, o->tri, sel, nb, st));
+  return PSGDK_OK;
+}
+
+int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params,
+                       float* const* pre_out, float* const* clipped_out, void* ws, size_t* ws_bytes,
+                       psgdk_stream_t stream) {
+  PSGDK_TRY(check_group(g));
+  if (!o) return fail(PSGDK_EINVAL, "null options");
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  const int nb = g->nb;
+  const int64_t m = g->m, n = g->n, mn = m * n;
+  Ws w(ws);
+  float *tmp[MAXB], *pre[MAXB], *part[MAXB];
+  const int np_max = std::max(gemm_tiles(m, n, 0), 256);
+  for (int b = 0; b < nb; ++b) {
+    tmp[b] = w.take<float>(mn);
+    pre[b] = w.take<float>(mn);
+    part[b] = w.take<float>(2 * (size_t)np_max);
+  }
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(params, nb, "params"));
+  hipStream_t st = (hipStream_t)stream;
+  for (int b = 0; b < nb; ++b)
+    if (pre_out && pre_out[b]) pre[b] = pre_out[b];
+  int np = 0;
+  PSGDK_TRY(precondition(g, g->G, g->g_dtype, tmp, pre, part, o->tri, &np, st));
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.m = m; a.n = n; a.dt = g->p_dtype; a.i0 = np;
+  a.f0 = o->max_avg_amp; a.f1 = o->max_element_amp; a.f2 = o->lr_params;
+  for (int b = 0; b < nb; ++b) {
+    a.in[b] = params[b]; a.in2[b] = pre[b]; a.in3[b] = part[b];
+    a.out2[b] = clipped_out ? clipped_out[b] : nullptr;
+  }
+  return hip_check(clip_update_launch(a, st), "clip + update");
+}
+
+int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, psgdk_stream_t stream) {
+  PSGDK_TRY(check_group(g));
+  int sel[MAXB];
+  for (int b = 0; b < g->nb; ++b) sel[b] = b;
+  for (int f = 0; f < 2; ++f) {
+    if (!(factor_mask & (1 << f))) continue;
+    if (g->kind[f] == PSGDK_FACTOR_DENSE) PSGDK_TRY(refresh_p_dense(g, f, tri, sel, g->nb, (hipStream_t)stream));
+    else if (g->kind[f] == PSGDK_FACTOR_DIAG) PSGDK_TRY(refresh_p_diag(g, f, sel, g->nb, (hipStream_t)stream));
+  }
+  return PSGDK_OK;
+}
+
+int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri, void* ws, size_t* ws_bytes,
+                         psgdk_stream_t stream) {
+  PSGDK_TRY(check_group(g));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  constexpr int PB = 64;  // partial maxima per factor
+  Ws w(ws);
+  float *part[MAXB], *sc[MAXB];
+  for (int b = 0; b < g->nb; ++b) { part[b] = w.take<float>(2 * PB); sc[b] = w.take<float>(4); }
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  if (!flags) return fail(PSGDK_EINVAL, "null flags");
+  int fac[2], order = 0;
+  for (int f = 0; f < 2; ++f)
+    if (g->kind[f] != PSGDK_FACTOR_NONE) fac[order++] = f;
+  if (order < 2) return PSGDK_OK;  // psgd_pro.py:101: a single factor is left alone
+  int sel[MAXB], nsel = 0;
+  for (int b = 0; b < g->nb; ++b)
+    if (flags[b]) sel[nsel++] = b;
+  if (!nsel) return PSGDK_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t dims[2] = {g->m, g->n};
+  for (int i = 0; i < order; ++i) {
+    const int f = fac[i];
+    const int64_t sz = g->kind[f] == PSGDK_FACTOR_DENSE ? dims[f] * dims[f] : dims[f];
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nsel; a.m = 1; a.n = sz; a.i0 = PB;
+    for (int j = 0; j < nsel; ++j) { a.in[j] = g->Q[f][sel[j]]; a.out[j] = part[sel[j]] + i * PB; }
+    PSGDK_HIP(absmax_launch(a, st), "balance absmax");
+  }
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nsel; a.i0 = PB; a.i1 = order;
+    for (int j = 0; j < nsel; ++j) { a.in2[j] = part[sel[j]]; a.out[j] = sc[sel[j]]; }
+    PSGDK_HIP(balance_scalar_launch(a, st), "balance scalars");
+  }
+  for (int i = 0; i < order; ++i) {
+    const int f = fac[i];
+    const int64_t sz = g->kind[f] == PSGDK_FACTOR_DENSE ? dims[f] * dims[f] : dims[f];
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nsel; a.m = 1; a.n = sz; a.i1 = i;
+    for (int j = 0; j < nsel; ++j) { a.out[j] = g->Q[f][sel[j]]; a.sc[j] = sc[sel[j]]; }
+    PSGDK_HIP(scale_by_dev_launch(a, st), "balance scale");
+  }
+  for (int i = 0; i < order; ++i) {
+    const int f = fac[i];
+    if (g->kind[f] == PSGDK_FACTOR_DENSE) PSGDK_TRY(refresh_p_dense(g, f, tri, sel, nsel, st));
+    else PSGDK_TRY(refresh_p_diag(g, f, sel, nsel, st));
+  }
+  return PSGDK_OK;
+}
+
+int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const* mom, const void* const* g,
+                   psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(numel, "numel"));
+  PSGDK_TRY(check_dt(g_dtype, "g"));
+  PSGDK_TRY(check_ptrs(mom, nb, "mom"));
+  PSGDK_TRY(check_ptrs(g, nb, "g"));
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.m = 1; a.n = numel; a.dt = g_dtype; a.f0 = beta;
+  for (int b = 0; b < nb; ++b) { a.in[b] = g[b]; a.out[b] = mom[b]; }
+  return hip_check(momentum_launch(a, (hipStream_t)stream), "momentum");
+}
+
+int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream) {
+  PSGDK_TRY(check_prec(prec));
+  if (!A || !B || !C) return fail(PSGDK_EINVAL, "null pointer");
+  return hip_check(debug_mfma_launch(A, B, C, prec, (hipStream_t)stream), "debug mfma");
+}
+
+}  // extern "C"

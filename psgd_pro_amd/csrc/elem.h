@@ -1,0 +1,50 @@
+// Elementwise and reduction kernels around the contractions: argument blocks and launchers.
+#pragma once
+#include "common.h"
+#include "gemm.h"
+
+namespace psgdk {
+
+struct EwArgs {
+  int nb;
+  long long m, n;          // matrix shape (rows, cols) of the operands
+  long long ld;            // leading dimension of the (square) operand for tile kernels
+  int dt;                  // storage dtype of `in` (0 fp32, 1 bf16)
+  float f0, f1, f2, f3;    // kernel-specific host scalars
+  int i0, i1;              // kernel-specific ints
+  const void* in[MAXB];
+  const float* in2[MAXB];
+  const float* in3[MAXB];
+  float* out[MAXB];
+  void* out2[MAXB];
+  float* sc[MAXB];         // device scalars
+};
+
+// X = G + (damping + eps |G|) * N                      (psgd_pro.py:121-123)
+hipError_t noise_launch(const EwArgs& a, hipStream_t st);
+// R = Q^T - Q (sign = +1) or Q - Q^T (sign = -1), square d x d  (psgd_pro.py:87; psgd_pro_fast.py:147)
+hipError_t rform_launch(const EwArgs& a, hipStream_t st);
+// Procrustes step size from the trace partials     (psgd_pro.py:91-93)
+hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st);
+// out = in * p_row[i] * p_col[j] (diagonal factors' P = q * q; null pointer = 1)
+hipError_t diag_scale_launch(const EwArgs& a, hipStream_t st);
+// diagonal factor term1: sums of squares along rows (i0 = 0) or columns (i0 = 1) of Pg  (psgd_pro.py:125-126)
+hipError_t diag_term1_launch(const EwArgs& a, hipStream_t st);
+// diagonal factor update: ell, L EMA, q *= 1 - lr/L (term1 - term2), P = q * q  (psgd_pro.py:127-130)
+hipError_t diag_update_launch(const EwArgs& a, hipStream_t st);
+// clip + parameter update from the sum-of-squares partials  (psgd_pro.py:371-381)
+hipError_t clip_update_launch(const EwArgs& a, hipStream_t st);
+// max |x| partials and scaling for balancing (psgd_pro.py:96-105)
+hipError_t absmax_launch(const EwArgs& a, hipStream_t st);
+hipError_t balance_scalar_launch(const EwArgs& a, hipStream_t st);
+hipError_t scale_by_dev_launch(const EwArgs& a, hipStream_t st);
+// m = beta m + (1 - beta) g                           (psgd_pro.py:340-341)
+hipError_t momentum_launch(const EwArgs& a, hipStream_t st);
+// sum of the split partials: out[i] = sum_s in[s * m * n + i]
+hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
+// sum-of-squares partials in the GEMM's EPI_SUMSQ format (i0 blocks per problem)
+hipError_t sumsq_launch(const EwArgs& a, hipStream_t st);
+// full symmetric matrix from the packed upper triangle
+hipError_t unpack_launch(const EwArgs& a, hipStream_t st);
+
+}  // namespace psgdk

@@ -1,0 +1,371 @@
+// Elementwise and small reduction kernels of the PSGD-Kron step. All reductions are deterministic: fixed-order
+// partial sums, no float atomics.
+#include "elem.h"
+
+namespace psgdk {
+
+template <typename T> __device__ __forceinline__ float ld_as_f32(const void* p, long long i) {
+  return to_f32<T>(reinterpret_cast<const T*>(p)[i]);
+}
+__device__ __forceinline__ float ldv(const void* p, int dt, long long i) {
+  return dt ? ld_as_f32<bf16_t>(p, i) : ld_as_f32<float>(p, i);
+}
+
+constexpr int EW_THREADS = 256;
+constexpr int EW_PER_THREAD = 8;
+
+__device__ __forceinline__ void ew_range(long long total, int blocks_per, long long& beg, long long& end) {
+  const long long chunk = (total + blocks_per - 1) / blocks_per;
+  beg = (long long)(blockIdx.x % blocks_per) * chunk;
+  end = beg + chunk < total ? beg + chunk : total;
+}
+
+static int ew_blocks(long long total) {
+  long long b = (total + (long long)EW_THREADS * EW_PER_THREAD - 1) / ((long long)EW_THREADS * EW_PER_THREAD);
+  if (b < 1) b = 1;
+  if (b > 4096) b = 4096;
+  return (int)b;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const void* G = a.in[b];
+  const float* N = a.in2[b];
+  float* X = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    const float g = ldv(G, a.dt, i);
+    X[i] = g + (a.f0 + a.f1 * fabsf(g)) * N[i];
+  }
+}
+hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(noise_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// R[i][j] = sign * (Q[j][i] - Q[i][j]); 64 x 64 tiles through LDS. grid: T*T*nb.
+__global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
+  __shared__ float t[64][65];
+  const int d = (int)a.m, T = (d + 63) / 64;
+  const int b = blockIdx.x / (T * T), tile = blockIdx.x % (T * T);
+  const int I = tile / T, J = tile % T;
+  const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
+  float* __restrict__ R = a.out[b];
+  const long long ld = a.ld;
+  const float sg = (float)a.i0;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // load Q[J-block rows][I-block cols] transposed into t
+  for (int r = ty; r < 64; r += 4) {
+    const int gi = J * 64 + r, gj = I * 64 + tx;
+    t[tx][r] = (gi < d && gj < d) ? Q[(long long)gi * ld + gj] : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int gi = I * 64 + r, gj = J * 64 + tx;
+    if (gi < d && gj < d) R[(long long)gi * ld + gj] = sg * (t[r][tx] - Q[(long long)gi * ld + gj]);
+  }
+}
+hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
+  const int T = (int)((a.m + 63) / 64);
+  hipLaunchKernelGGL(rform_kernel, dim3(T * T * a.nb), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// in2[b] = trace partials (2 per tile, i0 tiles), sc[b][0] = 1 / (bound + smallest normal).
+// out[b] = {a, scale}: a = min(-tr(RQ)/tr(RRQ), f0) if tr(RRQ) < 0 else f0.
+__global__ void __launch_bounds__(256) proc_scalar_kernel(const EwArgs a) {
+  __shared__ float red[16];
+  const int b = blockIdx.x;
+  const float* part = a.in2[b];
+  float t1 = 0.f, t2 = 0.f;
+  for (int t = threadIdx.x; t < a.i0; t += blockDim.x) { t1 += part[2 * t]; t2 += part[2 * t + 1]; }
+  t1 = block_sum(t1, red);
+  t2 = block_sum(t2, red);
+  if (threadIdx.x == 0) {
+    float step = a.f0;
+    if (t2 < 0.f) {
+      const float x = -t1 / t2;
+      step = x > a.f0 ? a.f0 : x;
+    }
+    a.out[b][0] = step;
+    a.out[b][1] = a.sc[b][0];
+    a.out[b][2] = t1;
+    a.out[b][3] = t2;
+  }
+}
+hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(proc_scalar_kernel, dim3(a.nb), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(EW_THREADS) diag_scale_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const void* X = a.in[b];
+  const float* pr = a.in2[b];
+  const float* pc = a.in3[b];
+  float* Y = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    const long long r = i / a.n, c = i % a.n;
+    float v = ldv(X, a.dt, i);
+    if (pr) v *= pr[r];
+    if (pc) v *= pc[c];
+    Y[i] = v;
+  }
+}
+hipError_t diag_scale_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(diag_scale_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// rows (i0 = 0): one wave per row; columns (i0 = 1): one thread per column.
+__global__ void __launch_bounds__(256) diag_term1_rows_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per, blk = blockIdx.x % blocks_per;
+  const float* X = reinterpret_cast<const float*>(a.in[b]);
+  float* out = a.out[b];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (long long r = (long long)blk * 4 + w; r < a.m; r += (long long)blocks_per * 4) {
+    float s = 0.f;
+    for (long long c = lane; c < a.n; c += 64) { const float v = X[r * a.n + c]; s += v * v; }
+    s = wave_sum(s);
+    if (lane == 0) out[r] = s;
+  }
+}
+__global__ void __launch_bounds__(256) diag_term1_cols_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per, blk = blockIdx.x % blocks_per;
+  const float* X = reinterpret_cast<const float*>(a.in[b]);
+  float* out = a.out[b];
+  for (long long c = (long long)blk * 256 + threadIdx.x; c < a.n; c += (long long)blocks_per * 256) {
+    float s = 0.f;
+    for (long long r = 0; r < a.m; ++r) { const float v = X[r * a.n + c]; s += v * v; }
+    out[c] = s;
+  }
+}
+hipError_t diag_term1_launch(const EwArgs& a, hipStream_t st) {
+  if (a.i0 == 0) {
+    int bp = (int)((a.m + 3) / 4);
+    if (bp > 1024) bp = 1024;
+    hipLaunchKernelGGL(diag_term1_rows_kernel, dim3(bp * a.nb), dim3(256), 0, st, a, bp);
+  } else {
+    int bp = (int)((a.n + 255) / 256);
+    if (bp > 1024) bp = 1024;
+    hipLaunchKernelGGL(diag_term1_cols_kernel, dim3(bp * a.nb), dim3(256), 0, st, a, bp);
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// One workgroup per factor: in2 = term1 (m values), out = q (in place), out2 = P = q * q, sc = L (1 float).
+// f0 = lr, f1 = beta, f2 = term2.
+__global__ void __launch_bounds__(1024) diag_update_kernel(const EwArgs a) {
+  __shared__ float red[16];
+  __shared__ float s_c;
+  const int b = blockIdx.x;
+  const float* t1 = a.in2[b];
+  float* q = a.out[b];
+  float* P = reinterpret_cast<float*>(a.out2[b]);
+  float mx = -INFINITY;
+  for (long long i = threadIdx.x; i < a.m; i += blockDim.x) mx = fmaxf(mx, t1[i]);
+  mx = block_max(mx, red);
+  if (threadIdx.x == 0) {
+    const float ell = mx + a.f2;
+    float* L = a.sc[b];
+    const float Ln = fmaxf(a.f1 * L[0] + (1.f - a.f1) * ell, ell);
+    L[0] = Ln;
+    s_c = a.f0 / Ln;
+  }
+  __syncthreads();
+  const float c = s_c;
+  for (long long i = threadIdx.x; i < a.m; i += blockDim.x) {
+    const float v = q[i] * (1.f - c * (t1[i] - a.f2));
+    q[i] = v;
+    if (P) P[i] = v * v;
+  }
+}
+hipError_t diag_update_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(diag_update_kernel, dim3(a.nb), dim3(1024), 0, st, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// in = param (dtype dt, m*n), in2 = pre (fp32), in3 = sum-of-squares partials (value at [2 t], i0 partials),
+// out2 (optional) = the clipped gradient. f0 = max average amplitude, f1 = max element amplitude, f2 = lr.
+__global__ void __launch_bounds__(EW_THREADS) clip_update_kernel(const EwArgs a, int blocks_per) {
+  __shared__ float red[16];
+  const int b = blockIdx.x / blocks_per;
+  const float* part = a.in3[b];
+  float s = 0.f;
+  for (int t = threadIdx.x; t < a.i0; t += blockDim.x) s += part[2 * t];
+  s = block_sum(s, red);
+  const long long total = a.m * a.n;
+  const float avg = sqrtf(s / (float)total);
+  const bool scale = avg > a.f0;
+  const float sc = a.f0 / avg;
+  long long beg, end;
+  ew_range(total, blocks_per, beg, end);
+  const float* pre = a.in2[b];
+  void* prm = const_cast<void*>(a.in[b]);
+  float* gout = reinterpret_cast<float*>(a.out2[b]);
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    float g = pre[i];
+    if (scale) g *= sc;
+    g = fminf(fmaxf(g, -a.f1), a.f1);
+    if (gout) gout[i] = g;
+    if (a.dt) {
+      bf16_t* p = reinterpret_cast<bf16_t*>(prm);
+      p[i] = f32_to_bf16(bf16_to_f32(p[i]) - a.f2 * g);
+    } else {
+      float* p = reinterpret_cast<float*>(prm);
+      p[i] = p[i] - a.f2 * g;
+    }
+  }
+}
+hipError_t clip_update_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(clip_update_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out[b][blk] = max |in[b][i]| over the block's range (i0 = blocks per problem).
+__global__ void __launch_bounds__(EW_THREADS) absmax_kernel(const EwArgs a, int blocks_per) {
+  __shared__ float red[16];
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const float* x = reinterpret_cast<const float*>(a.in[b]);
+  float m = 0.f;
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) m = fmaxf(m, fabsf(x[i]));
+  m = block_max(m, red);
+  if (threadIdx.x == 0) a.out[b][blockIdx.x % blocks_per] = m;
+}
+hipError_t absmax_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(absmax_kernel, dim3(a.i0 * a.nb), dim3(EW_THREADS), 0, st, a, a.i0);
+  return hipGetLastError();
+}
+
+// One workgroup per parameter: in2[b] = partial maxima of its i1 factors (i0 partials each, factor-major);
+// out[b][f] = gmean / max|q_f| with gmean = (prod_f max|q_f|)^(1/i1).
+__global__ void __launch_bounds__(64) balance_scalar_kernel(const EwArgs a) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const float* part = a.in2[b];
+  float norms[8];
+  float prod = 1.f;
+  for (int f = 0; f < a.i1; ++f) {
+    float m = 0.f;
+    for (int t = lane; t < a.i0; t += 64) m = fmaxf(m, part[f * a.i0 + t]);
+    m = wave_max(m);
+    norms[f] = m;
+    prod *= m;
+  }
+  const float g = powf(prod, 1.f / (float)a.i1);
+  if (lane == 0)
+    for (int f = 0; f < a.i1; ++f) a.out[b][f] = g / norms[f];
+}
+hipError_t balance_scalar_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(balance_scalar_kernel, dim3(a.nb), dim3(64), 0, st, a);
+  return hipGetLastError();
+}
+
+// out[b][i] *= sc[b][i1]
+__global__ void __launch_bounds__(EW_THREADS) scale_by_dev_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const float s = a.sc[b][a.i1];
+  float* x = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) x[i] *= s;
+}
+hipError_t scale_by_dev_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(scale_by_dev_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(EW_THREADS) momentum_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const void* g = a.in[b];
+  float* m = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) m[i] = m[i] * a.f0 + (1.f - a.f0) * ldv(g, a.dt, i);
+}
+hipError_t momentum_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(momentum_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(EW_THREADS) splitk_sum_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  const long long mn = a.m * a.n;
+  ew_range(mn, blocks_per, beg, end);
+  const float* in = a.in2[b];
+  float* out = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    float s = 0.f;
+    for (int k = 0; k < a.i0; ++k) s += in[(long long)k * mn + i];
+    out[i] = s;
+  }
+}
+hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n);
+  hipLaunchKernelGGL(splitk_sum_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out[b][2 blk] = sum of squares over the block's range, out[b][2 blk + 1] = 0 (i0 = blocks per problem).
+__global__ void __launch_bounds__(EW_THREADS) sumsq_kernel(const EwArgs a, int blocks_per) {
+  __shared__ float red[16];
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  ew_range(a.m * a.n, blocks_per, beg, end);
+  const float* x = reinterpret_cast<const float*>(a.in[b]);
+  float s = 0.f;
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) s += x[i] * x[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) {
+    a.out[b][2 * (blockIdx.x % blocks_per)] = s;
+    a.out[b][2 * (blockIdx.x % blocks_per) + 1] = 0.f;
+  }
+}
+hipError_t sumsq_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(sumsq_kernel, dim3(a.i0 * a.nb), dim3(EW_THREADS), 0, st, a, a.i0);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Full symmetric n x n (ld) from the row-major packed upper triangle.
+__global__ void __launch_bounds__(EW_THREADS) unpack_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  long long beg, end;
+  const long long n = a.n;
+  ew_range(n * n, blocks_per, beg, end);
+  const float* pk = a.in2[b];
+  float* C = a.out[b];
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    const long long r = i / n, c = i % n;
+    const long long lo = r < c ? r : c, hi = r < c ? c : r;
+    C[r * a.ld + c] = pk[lo * n - lo * (lo - 1) / 2 + (hi - lo)];
+  }
+}
+hipError_t unpack_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.n * a.n);
+  hipLaunchKernelGGL(unpack_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+}  // namespace psgdk

@@ -1,0 +1,43 @@
+// MFMA GEMM engine: argument block shared by the host launcher and the kernels.
+#pragma once
+#include "common.h"
+
+namespace psgdk {
+
+constexpr int MAXB = 16;  // problems per grouped launch (kernel-argument space, captured by value)
+
+// Epilogues. acc is op(A) op(B) accumulated in fp32; s = the problem's device scalars.
+enum Epi : int {
+  EPI_STORE = 0,   // C = alpha * acc + beta * C
+  EPI_FACTOR = 1,  // C = X1 - s[0] * (acc - s[1] * X1)              (Q - lr/L (term1 Q - term2 Q))
+  EPI_PROC = 2,    // C = X1 + a X2 + a^2/2 * s[1] * acc, a = s[0]    (Procrustes: Q + a RQ + a^2/2 R RQ)
+  EPI_SCALE = 3,   // C = s[0] * acc
+  EPI_RQ = 4,      // C = s[0] * acc and trace partials of tr(C), tr(s[0] X1 C) into part[]  (Procrustes RQ)
+  EPI_SUMSQ = 5,   // C = alpha * acc and partial sums of C^2 into part[]                    (apply + clip stats)
+};
+
+struct GemmArgs {
+  int M, N, K;
+  int amode, bmode;     // OpMode of A (rows m) and B (rows n), both viewed as X[mn][k]
+  int asign, bsign;     // SYM sign
+  long long lda, ldb, ldc, ldx;
+  float alpha, beta;
+  int epi;
+  int tri;              // 1: upper-triangular tile grid (SYRK: M == N, B is A)
+  int out_mode;         // tri: 0 upper triangle only, 1 mirrored full matrix, 2 packed upper triangle
+  int tiles_m, tiles_n, ntiles;
+  int avec, bvec;       // 16-byte vector loads allowed for A / B (alignment of base and ld)
+  int kbeg_tri;         // A is upper-triangular (SYM, sign 0): start the k loop at the tile's first row
+  int splitk, kchunk;   // split-K (EPI_STORE only): split s covers k in [s kchunk, (s+1) kchunk) and writes its
+                        // partial product to C + s * M * ldc
+  int nb;
+  const void* A[MAXB];
+  const void* B[MAXB];
+  float* C[MAXB];
+  const float* X1[MAXB];
+  const float* X2[MAXB];
+  const float* s[MAXB];
+  float* part[MAXB];
+};
+
+}  // namespace psgdk

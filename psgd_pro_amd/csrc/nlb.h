@@ -1,0 +1,47 @@
+// Norm lower bound stages: argument blocks shared by the host launchers and the kernels.
+#pragma once
+#include "common.h"
+#include "gemm.h"
+
+namespace psgdk {
+
+constexpr int NLB_K = 32;  // rows of the random start V
+
+// per-matrix device scalars (scal[b][...])
+enum : int { NLB_NF = 0, NLB_J = 1, NLB_BOUND = 2, NLB_NSCAL = 4 };
+
+struct NlbArgs {
+  int nb, n, T, sign, splits;
+  long long lda;
+  const float* A[MAXB];     // n x n, upper triangle read
+  const float* Vin[MAXB];   // init: the random start (32 x n)
+  float* Vout[MAXB];        // init: V0; reduce: the scaled product
+  float* part[MAXB];        // reduce input: splits x 32 x n partial products
+  const float* ssin[MAXB];  // reduce (normalize_in) / final: per-(row, column block) sums of squares of the input
+  float* ssout[MAXB];       // reduce output sums of squares
+  float* rpart[MAXB];       // T x T x 64 row-norm partials
+  float* cpart[MAXB];       // T x 64 diagonal-tile column partials
+  float* tmax[MAXB];        // per stored tile max |A_ij|
+  float* dmax[MAXB];        // per stored tile max diagonal
+  float* rn2[MAXB];         // n squared row norms
+  float* scal[MAXB];        // NLB_NSCAL scalars
+  float* amax_out[MAXB];    // optional: max |A_ij| of the stored triangle (init)
+};
+
+enum : int { NLB_FINAL_NONE = 0, NLB_FINAL_FACTOR = 1, NLB_FINAL_SCALE = 2 };
+
+struct NlbFinal {
+  int mode;
+  float lr, beta, term2;
+  float* L[MAXB];     // factor: the smoothness EMA (1 float)
+  float* coef[MAXB];  // factor: {lr / L, term2}; scale: {1 / (bound + smallest normal)}
+};
+
+hipError_t nlb_rownorm_launch(const NlbArgs& a, hipStream_t st);
+hipError_t nlb_init_launch(const NlbArgs& a, hipStream_t st);
+hipError_t nlb_reduce_launch(const NlbArgs& a, int normalize_in, hipStream_t st);
+hipError_t nlb_final_launch(const NlbArgs& a, const NlbFinal& f, hipStream_t st);
+hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
+hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
+
+}  // namespace psgdk

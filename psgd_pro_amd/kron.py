@@ -1,0 +1,391 @@
+"""KronWhiten: the PSGD-Kron optimizer (dQ = Q^0.5 E Q^1.5, whitening preconditioner) on the HIP engine.
+
+Drop-in for psgd_pro.KronWhiten / psgd_pro_fast.KronWhiten (psgd_pro.py:251-384, psgd_pro_fast.py:239-499): the same
+constructor arguments, mutable attributes, step(closure) returning the closure's value and step_math(grads); plus
+state_dict() / load_state_dict() (absent in the reference). Every parameter's preconditioner update and gradient
+apply run through libpsgdk.so's grouped entry points (psgdk_kron2d_update / _apply / _balance, psgdk_momentum):
+parameters of one shape and factor structure form a group of up to 16 that every kernel launch covers at once, and
+no step synchronizes the host with the device.
+
+Parameters are handled as m x n matrices after squeezing: 2-D as is, 1-D as 1 x n, scalars as 1 x 1 (one diagonal
+factor). Tensors of order 3 or more are rejected (NotImplementedError).
+
+Random draws (psgd_pro.py:123,35,59,138,345): draws="host" reproduces psgd_pro.py's stream on a CPU generator
+(update coin, then per parameter the damping noise, two 32 x d starts per dense factor, the balancing coin) and
+uploads the normals; draws="device" draws the coins on the CPU (update coin, then one balancing coin per parameter,
+as psgd_pro_fast.py:482-483) and the normals on the device generator.
+"""
+import ctypes
+
+import torch
+
+from . import _lib as L
+from .ops import make_ops
+
+_K = L.NLB_K
+
+
+def _is_dense(size, numel, max_size, max_skew):
+    # psgd_pro.py:189
+    return not (size <= 1 or size > max_size or size ** 2 > max_skew * numel)
+
+
+class _Param:
+    __slots__ = ("index", "shape", "m", "n", "kind", "Q", "P", "L", "group", "slot", "scalar")
+
+
+class _Group:
+    __slots__ = ("key", "members", "m", "n", "kind", "struct", "Qs", "Ps", "Ls", "g_dtype", "p_dtype")
+
+
+class KronWhiten:
+    """See the module docstring. Arguments as psgd_pro_fast.KronWhiten; keyword-only extras:
+    precision "fp32" | "bf16" (MFMA input precision of the contractions), draws "device" | "host", seed (a private
+    CPU generator for the coins and host draws; None = torch's default generator, as the reference), tri (term1 and P
+    kept as upper triangles)."""
+
+    def __init__(self, params_with_grad,
+                 preconditioner_max_size=float("inf"),
+                 preconditioner_max_skew=1.0,
+                 preconditioner_init_scale=None,
+                 lr_params=0.001,
+                 lr_preconditioner=0.1,
+                 betaL=0.9,
+                 damping=1e-9,
+                 momentum=0.0,
+                 grad_clip_max_amps=(2.0, 10.0),
+                 preconditioner_update_probability=1.0,
+                 update_preconditioner_first=True,
+                 whiten_grad=True,
+                 compile=None,
+                 ops=None,
+                 batch=False,
+                 cache_p=False,
+                 graph_rng=False,
+                 p2d=True,
+                 r2=False,
+                 *,
+                 precision=None,
+                 draws="device",
+                 seed=None,
+                 tri=None):
+        self.lr_params = lr_params
+        self.lr_preconditioner = lr_preconditioner
+        self.betaL = betaL
+        self.damping = damping
+        self.momentum = momentum if (0 < momentum < 1) else 0.0
+        self.grad_clip_max_amps = grad_clip_max_amps
+        self.preconditioner_update_probability = preconditioner_update_probability
+        self.update_preconditioner_first = update_preconditioner_first
+
+        self._preconditioner_max_size = preconditioner_max_size
+        self._preconditioner_max_skew = preconditioner_max_skew
+        params_with_grad = [params_with_grad] if isinstance(params_with_grad, torch.Tensor) else params_with_grad
+        self._params_with_grad = [p for p in params_with_grad if p.requires_grad]
+        self._whiten_grad = whiten_grad
+        if not whiten_grad:
+            assert self.momentum > 0, "Cannot whiten momentum if the momentum setting is invalid."
+        if compile is not None:
+            raise ValueError("compile: the HIP engine runs without torch.compile (pass compile=None)")
+        if r2:
+            raise NotImplementedError("r2 (procrustes_step_r2) is not provided by this version of the engine")
+        flags = getattr(ops, "flags", frozenset()) if ops is not None else frozenset()
+        self.ops = ops if ops is not None else make_ops(())
+        if precision is None:
+            precision = "bf16" if "bf16" in flags else "fp32"
+        if precision not in ("fp32", "bf16"):
+            raise ValueError("precision: 'fp32' or 'bf16'")
+        self._prec = L.PREC_BF16 if precision == "bf16" else L.PREC_F32
+        self._tri = (3 if ("tri" in flags) else 0) if tri is None else (3 if tri else 0)
+        if draws not in ("device", "host"):
+            raise ValueError("draws: 'device' or 'host'")
+        self._draws = draws
+        self._gen = torch.Generator().manual_seed(seed) if seed is not None else None
+        self.capture, self.pre = False, []
+        self._params = None
+        self._groups = None
+        self._ms, self._counter_m = None, 0
+        self._ws_upd, self._ws_app, self._ws_bal = L.Workspace(), L.Workspace(), L.Workspace()
+        self._init_scale = preconditioner_init_scale
+        if preconditioner_init_scale is not None:
+            self._init([p.squeeze() for p in self._params_with_grad], preconditioner_init_scale)
+
+    # ----------------------------------------------------------------------------------------------------------
+    def _rand(self):
+        return float(torch.rand([], generator=self._gen))
+
+    def _init(self, grads, scale):
+        """Factors of init_kron (psgd_pro.py:141-210): Q = scale^(1/order) I or ones, L = 0, and P = Q^T Q."""
+        L.lib()
+        self._params = []
+        for i, g in enumerate(grads):
+            if not g.is_cuda:
+                raise RuntimeError("psgd_pro_amd.KronWhiten runs on the GPU; parameter %d is on %s" % (i, g.device))
+            p = _Param()
+            p.index, p.shape = i, tuple(g.shape)
+            numel = max(1, g.numel())
+            if g.dim() == 0:
+                p.m, p.n, p.kind, p.scalar = 1, 1, (L.FACTOR_DIAG, L.FACTOR_NONE), True
+            elif g.dim() == 1:
+                d = g.shape[0]
+                k = L.FACTOR_DENSE if _is_dense(d, numel, self._preconditioner_max_size,
+                                                self._preconditioner_max_skew) else L.FACTOR_DIAG
+                p.m, p.n, p.kind, p.scalar = 1, d, (L.FACTOR_NONE, k), False
+            elif g.dim() == 2:
+                m, n = g.shape
+                k0 = L.FACTOR_DENSE if _is_dense(m, numel, self._preconditioner_max_size,
+                                                 self._preconditioner_max_skew) else L.FACTOR_DIAG
+                k1 = L.FACTOR_DENSE if _is_dense(n, numel, self._preconditioner_max_size,
+                                                 self._preconditioner_max_skew) else L.FACTOR_DIAG
+                p.m, p.n, p.kind, p.scalar = m, n, (k0, k1), False
+            else:
+                raise NotImplementedError(f"parameter {i}: tensors of order {g.dim()} are not supported")
+            self._params.append(p)
+        self._build_groups(grads, scale)
+
+    def _build_groups(self, grads, scale):
+        by_key = {}
+        for p, g in zip(self._params, grads):
+            prm = self._params_with_grad[p.index]
+            key = (p.m, p.n, p.kind, g.dtype, prm.dtype, g.device)
+            by_key.setdefault(key, []).append(p)
+        self._groups = []
+        for key, members in by_key.items():
+            for c in range(0, len(members), L.MAXB):
+                grp = _Group()
+                grp.key, grp.members = key, members[c:c + L.MAXB]
+                grp.m, grp.n, grp.kind = key[0], key[1], key[2]
+                grp.g_dtype, grp.p_dtype = L.dtype_code(key[3]), L.dtype_code(key[4])
+                dev = key[5]
+                nb = len(grp.members)
+                order = sum(k != L.FACTOR_NONE for k in grp.kind)
+                grp.Qs, grp.Ps, grp.Ls = [None, None], [None, None], [None, None]
+                for f, (k, d) in enumerate(zip(grp.kind, (grp.m, grp.n))):
+                    if k == L.FACTOR_NONE:
+                        continue
+                    s = scale if grp.members[0].scalar else scale ** (1.0 / order)
+                    if k == L.FACTOR_DENSE:
+                        Q = torch.eye(d, device=dev, dtype=torch.float32).mul_(s).expand(nb, d, d).contiguous()
+                        P = torch.empty(nb, d, d, device=dev, dtype=torch.float32)
+                    else:
+                        Q = torch.full((nb, d), s, device=dev, dtype=torch.float32)
+                        P = torch.empty(nb, d, device=dev, dtype=torch.float32)
+                    grp.Qs[f], grp.Ps[f] = Q, P
+                    grp.Ls[f] = torch.zeros(nb, 1, device=dev, dtype=torch.float32)
+                for j, p in enumerate(grp.members):
+                    p.group, p.slot = grp, j
+                grp.struct = self._struct(grp)
+                self._groups.append(grp)
+                self._refresh_p(grp)
+
+    def _struct(self, grp):
+        s = L.Kron2d()
+        s.nb, s.prec, s.m, s.n = len(grp.members), self._prec, grp.m, grp.n
+        s.kind[0], s.kind[1] = grp.kind
+        s.g_dtype, s.p_dtype = grp.g_dtype, grp.p_dtype
+        for f in range(2):
+            if grp.Qs[f] is None:
+                continue
+            for j in range(len(grp.members)):
+                s.Q[f][j] = grp.Qs[f][j].data_ptr()
+                s.P[f][j] = grp.Ps[f][j].data_ptr()
+                s.L[f][j] = grp.Ls[f][j].data_ptr()
+        return s
+
+    def _refresh_p(self, grp):
+        L.check(L.lib().psgdk_kron2d_refresh_p(grp.struct, 3, self._tri, L.stream_of(grp.Qs[0] if grp.Qs[0] is not None
+                                                                                   else grp.Qs[1])))
+
+    # ----------------------------------------------------------------------------------------------------------
+    def _dense_dims(self, p):
+        return [d for k, d in zip(p.kind, (p.m, p.n)) if k == L.FACTOR_DENSE]
+
+    def _bind_sources(self, grp, srcs):
+        """Points the group's G slots at this call's gradients (or momentum buffers) and sets their dtype."""
+        s = grp.struct
+        dt = srcs[grp.members[0].index].dtype
+        for j, p in enumerate(grp.members):
+            t = srcs[p.index]
+            if t.dtype != dt:
+                raise TypeError(f"parameters {grp.members[0].index} and {p.index} share a group but their gradients "
+                                f"have dtypes {dt} and {t.dtype}")
+            s.G[j] = t.data_ptr()
+        s.g_dtype = L.dtype_code(dt)
+        return dt
+
+    def _draw_update(self, srcs):
+        """Normals of one update (noise, then per dense factor the SPD and skew starts) in one device buffer,
+        in psgd_pro.py's order; returns (per-parameter noise views, per-parameter V views, balance coins)."""
+        sizes = []
+        for p in self._params:
+            sizes.append((p.m * p.n, sum(2 * _K * d for d in self._dense_dims(p))))
+        total = sum(a + b for a, b in sizes)
+        dev = srcs[0].device
+        coins = []
+        if self._draws == "host":
+            parts = []
+            for p, (a, b) in zip(self._params, sizes):
+                parts.append(torch.randn(a, generator=self._gen))
+                for d in self._dense_dims(p):
+                    parts.append(torch.randn(_K * d, generator=self._gen))
+                    parts.append(torch.randn(_K * d, generator=self._gen))
+                coins.append(self._rand() < 0.01)
+            flat = torch.cat(parts).pin_memory().to(dev, non_blocking=True) if total else None
+        else:
+            coins = (torch.rand(len(self._params), generator=self._gen) < 0.01).tolist()
+            flat = torch.randn(total, device=dev, dtype=torch.float32)
+        noise, V, off = [], [], 0
+        for a, b in sizes:
+            noise.append(flat[off:off + a])
+            V.append(flat[off + a:off + a + b] if b else None)
+            off += a + b
+        return noise, V, coins
+
+    def _update(self, srcs):
+        noise, V, coins = self._draw_update(srcs)
+        o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, 0)
+        for grp in self._groups:
+            s = grp.struct
+            gdt = self._bind_sources(grp, srcs)
+            o.grad_eps = torch.finfo(gdt).eps
+            nz = L.ptrs([noise[p.index] for p in grp.members])
+            vv = L.ptrs([V[p.index] for p in grp.members])
+            L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=self._ws_upd, device=srcs[0].device,
+                      stream=L.stream_of(srcs[0]))
+        for grp in self._groups:
+            flags = [int(coins[p.index]) for p in grp.members]
+            if any(flags):
+                fl = (ctypes.c_int32 * len(flags))(*flags)
+                L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=self._ws_bal,
+                          device=srcs[0].device, stream=L.stream_of(srcs[0]))
+
+    def _apply(self, srcs):
+        max_avg, max_el = self.grad_clip_max_amps
+        o = L.ApplyOpts(self.lr_params, max_avg, max_el, self._tri)
+        pre = [torch.empty(p.m, p.n, device=srcs[0].device, dtype=torch.float32) for p in self._params] \
+            if self.capture else None
+        for grp in self._groups:
+            s = grp.struct
+            self._bind_sources(grp, srcs)
+            prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
+            po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
+            L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=self._ws_app, device=srcs[0].device,
+                      stream=L.stream_of(srcs[0]))
+        if pre is not None:
+            self.pre = [t.view(p.shape) for t, p in zip(pre, self._params)]
+
+    # ----------------------------------------------------------------------------------------------------------
+    @torch.no_grad()
+    def step_math(self, grads):
+        """One step with the gradients given (psgd_pro_fast.py:441-490)."""
+        grads = [g.squeeze() for g in grads]
+        for i, g in enumerate(grads):
+            if g.dtype not in (torch.float32, torch.bfloat16):
+                raise TypeError(f"gradient {i}: float32 or bfloat16 expected, got {g.dtype}")
+        grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
+        if self._params is None:
+            # psgd_pro.py:329-332: scale = (max_p mean|g|^4 + damping^4)^(-1/8) (one host read at initialisation)
+            m4 = max(float(torch.mean(g.float().abs() ** 4)) for g in grads)
+            self._init(grads, (m4 + self.damping ** 4) ** (-1.0 / 8))
+        if self.momentum > 0:
+            beta = min(self._counter_m / (1 + self._counter_m), self.momentum)
+            self._counter_m += 1
+            if self._ms is None:
+                self._ms = [torch.zeros(g.shape, device=g.device, dtype=torch.float32) for g in grads]
+            for dt in (torch.float32, torch.bfloat16):
+                idx = [i for i, g in enumerate(grads) if g.dtype == dt]
+                for c in range(0, len(idx), L.MAXB):
+                    ch = idx[c:c + L.MAXB]
+                    sizes = {grads[i].numel() for i in ch}
+                    for sz in sizes:
+                        sel = [i for i in ch if grads[i].numel() == sz]
+                        L.check(L.lib().psgdk_momentum(sz, beta, L.dtype_code(dt), len(sel),
+                                                       L.ptrs([self._ms[i] for i in sel]),
+                                                       L.ptrs([grads[i] for i in sel]), L.stream_of(grads[0])))
+        else:
+            self._ms, self._counter_m = None, 0
+        update = self._rand() < self.preconditioner_update_probability
+        src = grads if self._whiten_grad else self._ms
+        if update and self.update_preconditioner_first:
+            self._update(src)
+        self._apply(self._ms if self.momentum > 0 else grads)
+        if update and not self.update_preconditioner_first:
+            self._update(src)
+
+    @torch.no_grad()
+    def step(self, closure):
+        """psgd_pro.py:319-384: evaluates the closure, takes the gradients with torch.autograd.grad, steps, and
+        returns whatever the closure returned."""
+        with torch.enable_grad():
+            closure_returns = closure()
+            loss = closure_returns if isinstance(closure_returns, torch.Tensor) else closure_returns[0]
+            grads = torch.autograd.grad(loss, self._params_with_grad)
+        self.step_math(grads)
+        return closure_returns
+
+    # ----------------------------------------------------------------------------------------------------------
+    def factors(self, i):
+        """(Q, L) of parameter i as lists over its factors (views of the group storage; diagonal factors are
+        vectors, a scalar parameter's factor is 0-d)."""
+        p = self._params[i]
+        Q, Ls = [], []
+        for f in range(2):
+            if p.kind[f] == L.FACTOR_NONE:
+                continue
+            q = p.group.Qs[f][p.slot]
+            Q.append(q.view(()) if p.scalar else q)
+            Ls.append(p.group.Ls[f][p.slot].view(()))
+        return Q, Ls
+
+    def state_dict(self):
+        """Q, L (and P) per parameter, momentum buffers and counter, the CPU generator state and the mutable
+        hyperparameters. P is saved for exactness of the next step; it is recomputed from Q when absent."""
+        st = dict(version=1, hyper=dict(lr_params=self.lr_params, lr_preconditioner=self.lr_preconditioner,
+                                        betaL=self.betaL, damping=self.damping, momentum=self.momentum,
+                                        grad_clip_max_amps=tuple(self.grad_clip_max_amps),
+                                        preconditioner_update_probability=self.preconditioner_update_probability,
+                                        update_preconditioner_first=self.update_preconditioner_first),
+                  counter_m=self._counter_m,
+                  momentum_buffers=[m.clone() for m in self._ms] if self._ms is not None else None,
+                  generator=self._gen.get_state() if self._gen is not None else None)
+        if self._params is not None:
+            st["params"] = []
+            for p in self._params:
+                ent = dict(shape=p.shape, kind=tuple(p.kind), Q=[], P=[], L=[])
+                for f in range(2):
+                    if p.kind[f] == L.FACTOR_NONE:
+                        continue
+                    ent["Q"].append(p.group.Qs[f][p.slot].clone())
+                    ent["P"].append(p.group.Ps[f][p.slot].clone())
+                    ent["L"].append(p.group.Ls[f][p.slot].clone())
+                st["params"].append(ent)
+        return st
+
+    def load_state_dict(self, st):
+        for k, v in st["hyper"].items():
+            setattr(self, k, v)
+        self._counter_m = st["counter_m"]
+        self._ms = [m.clone() for m in st["momentum_buffers"]] if st["momentum_buffers"] is not None else None
+        if st["generator"] is not None:
+            if self._gen is None:
+                self._gen = torch.Generator()
+            self._gen.set_state(st["generator"])
+        if "params" not in st:
+            return
+        dev = self._params_with_grad[0].device
+        if self._params is None:
+            grads = [torch.zeros(e["shape"], device=dev, dtype=p.dtype)
+                     for e, p in zip(st["params"], self._params_with_grad)]
+            self._init(grads, 1.0)
+        for p, ent in zip(self._params, st["params"]):
+            if tuple(ent["kind"]) != tuple(p.kind) or tuple(ent["shape"]) != p.shape:
+                raise ValueError(f"state for parameter {p.index} does not match its shape/factor structure")
+            fs = [f for f in range(2) if p.kind[f] != L.FACTOR_NONE]
+            for j, f in enumerate(fs):
+                p.group.Qs[f][p.slot].copy_(ent["Q"][j])
+                p.group.Ls[f][p.slot].copy_(ent["L"][j])
+                if ent.get("P"):
+                    p.group.Ps[f][p.slot].copy_(ent["P"][j])
+        if not all(ent.get("P") for ent in st["params"]):
+            for grp in self._groups:
+                self._refresh_p(grp)

@@ -1,0 +1,212 @@
+"""Each HIP kernel of libpsgdk.so against a float64 reference of the same operation (computed on the CPU).
+
+fp32 path: elementwise |C - ref| <= 64 eps_f32 * (|A| |B|) (a few ulps of the accumulation's natural error bound).
+bf16 path: the reference multiplies the bf16-rounded inputs in float64, so the only error is fp32 accumulation:
+the same bound applies. Triangle-reading kernels get a NaN-filled strict lower triangle: any read of it would show.
+"""
+import math
+
+import pytest
+import torch
+
+from psgd_pro_amd import _lib as L
+from psgd_pro_amd import ops as K
+from tests.metrics import rel_err_norm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+EPS32 = torch.finfo(torch.float32).eps
+
+
+def rnd(*shape, seed=0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+def bf(x):
+    return x.to(torch.bfloat16).float()
+
+
+def check_gemm_bound(C, A64, B64, tol=64):
+    """|C - A B| <= tol * eps32 * |A| |B| elementwise (A64, B64: float64 CPU operands as multiplied)."""
+    ref = A64 @ B64
+    bound = tol * EPS32 * (A64.abs() @ B64.abs()) + 1e-30
+    err = (C.double().cpu() - ref).abs()
+    worst = float((err / bound).max())
+    assert worst <= 1.0, f"max err/bound = {worst}"
+
+
+def poison_lower(S):
+    return S.masked_fill(torch.ones_like(S, dtype=torch.bool).tril(-1), float("nan"))
+
+
+# --------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("prec", [0, 1])
+def test_mfma_lane_layout(hip, prec):
+    k = 32 if prec else 4
+    A = rnd(16, k, seed=1)
+    B = rnd(k, 16, seed=2)
+    if prec:
+        A, B = bf(A), bf(B)
+    Ad, Bd = A.to(DEV), B.to(DEV)
+    Cd = torch.empty(16, 16, device=DEV)
+    L.check(hip.psgdk_debug_mfma(prec, C_ptr(Ad), C_ptr(Bd), C_ptr(Cd), L.stream_of(Ad)))
+    torch.cuda.synchronize()
+    check_gemm_bound(Cd, A.double(), B.double(), tol=8)
+
+
+def C_ptr(t):
+    import ctypes
+    return ctypes.c_void_p(t.data_ptr())
+
+
+GEMM_SHAPES = [(128, 128, 128), (256, 384, 320), (100, 70, 33), (1, 50, 77), (33, 129, 200), (768, 256, 768),
+               (32, 96, 1000)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_gemm(hip, m, n, k, ta, tb, prec):
+    A = rnd(*((k, m) if ta else (m, k)), seed=m + k)
+    B = rnd(*((n, k) if tb else (k, n)), seed=n + 3 * k)
+    C = K.gemm(A.to(DEV), B.to(DEV), bool(ta), bool(tb), bool(prec))
+    A64 = (bf(A) if prec else A).double()
+    B64 = (bf(B) if prec else B).double()
+    check_gemm_bound(C, A64.T if ta else A64, B64.T if tb else B64)
+
+
+@pytest.mark.parametrize("adt,bdt", [(torch.bfloat16, torch.float32), (torch.float32, torch.bfloat16),
+                                     (torch.bfloat16, torch.bfloat16)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_gemm_storage_dtypes(hip, adt, bdt, prec):
+    m, n, k = 200, 136, 264
+    A = rnd(m, k, seed=5).to(adt)
+    B = rnd(k, n, seed=6).to(bdt)
+    C = K.gemm(A.to(DEV), B.to(DEV), False, False, bool(prec))
+    A64 = (bf(A.float()) if prec else A.float()).double()
+    B64 = (bf(B.float()) if prec else B.float()).double()
+    check_gemm_bound(C, A64, B64)
+
+
+def test_gemm_grouped_and_alpha_beta(hip):
+    m, n, k, nb = 96, 160, 128, 5
+    As = [rnd(m, k, seed=i).to(DEV) for i in range(nb)]
+    Bs = [rnd(k, n, seed=10 + i).to(DEV) for i in range(nb)]
+    Cs = [rnd(m, n, seed=20 + i).to(DEV) for i in range(nb)]
+    C0 = [c.clone() for c in Cs]
+    L.check(hip.psgdk_gemm(0, 0, 0, m, n, k, 0.5, 0, 0, nb, L.ptrs(As), k, L.ptrs(Bs), n, -2.0, L.ptrs(Cs), n,
+                           L.stream_of(As[0])))
+    for A, B, C, c0 in zip(As, Bs, Cs, C0):
+        ref = 0.5 * (A.double().cpu() @ B.double().cpu()) - 2.0 * c0.double().cpu()
+        assert rel_err_norm(C, ref) < 1e-6
+
+
+# --------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n,k", [(128, 128), (256, 64), (200, 333), (768, 2304), (65, 17), (1, 9)])
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_syrk(hip, n, k, trans, prec):
+    A = rnd(*((k, n) if trans else (n, k)), seed=n * 7 + k)
+    Ad = A.to(DEV)
+    X64 = (bf(A) if prec else A).double()
+    X64 = X64.T if trans else X64
+    full = K.syrk(Ad, trans, L.OUT_MIRROR, bool(prec))
+    check_gemm_bound(full, X64, X64.T)
+    assert torch.equal(full, full.T)  # mirrored: exactly symmetric
+    up = torch.full((n, n), float("nan"), device=DEV)
+    L.check(hip.psgdk_syrk(prec, int(trans), L.OUT_UPPER, n, k, 0, 1, L.ptrs([Ad]), Ad.stride(0), L.ptrs([up]), n,
+                           L.stream_of(Ad)))
+    triu = torch.ones(n, n, dtype=torch.bool, device=DEV).triu()
+    assert torch.equal(up[triu], full[triu])
+    assert bool(torch.isnan(up[~triu]).all())  # the strict lower triangle is not written
+    pk = K.syrk(Ad, trans, L.OUT_PACKED, bool(prec))
+    assert torch.equal(pk, K.pack_upper(full))
+    assert torch.equal(K.unpack(pk, n), full)
+
+
+# --------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n,p", [(128, 64), (200, 130), (768, 768), (64, 1), (37, 300)])
+@pytest.mark.parametrize("sign", [1, -1])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_symm_reads_only_the_upper_triangle(hip, n, p, sign, prec):
+    X = rnd(n, n, seed=n)
+    S = (X + X.T) if sign > 0 else (X - X.T)
+    B = rnd(n, p, seed=p)
+    Sd = poison_lower(S).to(DEV)
+    C = K.symm(Sd, B.to(DEV), sign, bool(prec))
+    S64 = (bf(S) if prec else S).double()
+    B64 = (bf(B) if prec else B).double()
+    check_gemm_bound(C, S64, B64)
+    Bt = rnd(p, n, seed=p + 1)
+    Cr = K.symm_right(Bt.to(DEV), Sd, sign, bool(prec))
+    check_gemm_bound(Cr, (bf(Bt) if prec else Bt).double(), S64)
+
+
+@pytest.mark.parametrize("n,p", [(256, 256), (200, 77), (512, 512)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_trmm(hip, n, p, prec):
+    Q = rnd(n, n, seed=3)
+    B = rnd(n, p, seed=4)
+    C = K.trmm(poison_lower(Q).to(DEV), B.to(DEV), bool(prec))
+    Q64 = torch.triu((bf(Q) if prec else Q).double())
+    check_gemm_bound(C, Q64, (bf(B) if prec else B).double())
+
+
+# --------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [64, 100, 768, 1031])
+@pytest.mark.parametrize("sign", [1, -1])
+def test_tri_rownorm2(hip, n, sign):
+    X = rnd(n, n, seed=n)
+    S = (X + X.T) if sign > 0 else (X - X.T)
+    rn2, amax = K.tri_rownorm2(poison_lower(S).to(DEV), sign)
+    S64 = S.double()
+    assert rel_err_norm(rn2, (S64 * S64).sum(1)) < 1e-6
+    assert float(amax) == float(S.abs().max())
+
+
+@pytest.mark.parametrize("n", [64, 200, 768])
+@pytest.mark.parametrize("sign", [1, -1])
+def test_tri_vmm(hip, n, sign):
+    X = rnd(n, n, seed=n + 1)
+    S = (X + X.T) if sign > 0 else (X - X.T)
+    V = rnd(32, n, seed=9)
+    W = K.tri_vmm(V.to(DEV), poison_lower(S).to(DEV), sign)
+    check_gemm_bound(W, V.double(), S.double())
+
+
+@pytest.mark.parametrize("n", [64, 130, 768, 1024])
+@pytest.mark.parametrize("sign", [1, -1])
+def test_norm_lower_bound_matches_oracle(hip, n, sign):
+    from oracle.psgd_oracle import norm_lower_bound
+    X = rnd(n, n // 2 + 1, seed=n + 2)
+    S = X @ X.T if sign > 0 else (lambda Y: Y - Y.T)(rnd(n, n, seed=n + 3))
+    V = rnd(32, n, seed=11)
+    got = float(K.norm_lower_bound(poison_lower(S).to(DEV), V.to(DEV), sign))
+    ref = float(norm_lower_bound(S.double(), V.double(), skew=sign < 0))
+    assert got == pytest.approx(ref, rel=1e-5)
+    top = float(torch.linalg.matrix_norm(S.double(), 2))
+    assert got <= top * (1 + 1e-5)
+
+
+def test_hip_ops_plugin_methods(hip):
+    """The ops class methods (psgd_pro_fast.EagerOps interface) against their eager definitions."""
+    ops = K.make_ops(())
+    X = rnd(96, 160, seed=1).to(DEV)
+    assert rel_err_norm(ops.syrk(X, True), X.double().cpu().T @ X.double().cpu()) < 1e-6
+    assert rel_err_norm(ops.sym(X, False), X.double().cpu() @ X.double().cpu().T) < 1e-6
+    assert rel_err_norm(ops.gram(X, 0, None), X.double().cpu() @ X.double().cpu().T) < 1e-6
+    S = ops.syrk(X, False)
+    Y = rnd(96, 40, seed=2).to(DEV)
+    assert rel_err_norm(ops.symm(S, Y), S.double().cpu() @ Y.double().cpu()) < 1e-6
+    Z = rnd(40, 96, seed=3).to(DEV)
+    assert rel_err_norm(ops.symm_r(Z, S), Z.double().cpu() @ S.double().cpu()) < 1e-6
+    q = rnd(96, 96, seed=4).to(DEV)
+    assert rel_err_norm(ops.gram_q(q), q.double().cpu().T @ q.double().cpu()) < 1e-6
+    tri = K.make_ops({"tri", "nan"})
+    T = tri.sym(X, False)
+    assert bool(torch.isnan(T.tril(-1)[1:, :1]).all())
+    assert rel_err_norm(tri.symm(T, Y), S.double().cpu() @ Y.double().cpu()) < 1e-6
+    pk = K.make_ops({"packed"})
+    P = pk.sym(X, False)
+    assert P.dim() == 1 and rel_err_norm(pk.symm(P, Y), S.double().cpu() @ Y.double().cpu()) < 1e-6

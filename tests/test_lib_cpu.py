@@ -1,0 +1,127 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/psgdk.h declares, answers workspace
+queries, and rejects bad arguments with an error code and message before touching the device."""
+import ctypes as C
+import os
+import re
+
+import pytest
+import torch
+
+from psgd_pro_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "psgdk.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(psgdk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_and_binding_agree():
+    assert declared() == sorted(L.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.psgdk_version() == 1
+
+
+def test_nm_exports():
+    out = os.popen(f"nm -D --defined-only {L.LIB_PATH}").read()
+    syms = set(re.findall(r"\bT (psgdk_\w+)", out))
+    assert set(declared()) <= syms
+
+
+def _err():
+    return L.lib().psgdk_last_error().decode()
+
+
+def test_argument_validation():
+    lib = L.lib()
+    one = L.ptrs([0x1000])
+    null = L.ptrs([None])
+    # nb out of range
+    rc = lib.psgdk_syrk(0, 0, 1, 64, 64, 0, 0, one, 64, one, 64, None)
+    assert rc == L.EINVAL and "nb" in _err()
+    rc = lib.psgdk_syrk(0, 0, 1, 64, 64, 0, 17, one, 64, one, 64, None)
+    assert rc == L.EINVAL
+    # null device pointer
+    rc = lib.psgdk_syrk(0, 0, 1, 64, 64, 0, 1, null, 64, one, 64, None)
+    assert rc == L.EINVAL and "A[0]" in _err()
+    # bad precision / dtype / out mode / shapes
+    assert lib.psgdk_syrk(7, 0, 1, 64, 64, 0, 1, one, 64, one, 64, None) == L.EINVAL
+    assert lib.psgdk_syrk(0, 0, 1, 64, 64, 5, 1, one, 64, one, 64, None) == L.EINVAL
+    assert lib.psgdk_syrk(0, 0, 9, 64, 64, 0, 1, one, 64, one, 64, None) == L.EINVAL
+    assert lib.psgdk_syrk(0, 0, 1, 0, 64, 0, 1, one, 64, one, 64, None) == L.ESHAPE
+    assert lib.psgdk_syrk(0, 0, 1, 64, 64, 0, 1, one, 32, one, 64, None) == L.ESHAPE
+    assert lib.psgdk_gemm(0, 0, 0, 8, 8, 8, 1.0, 0, 0, 1, one, 4, one, 8, 0.0, one, 8, None) == L.ESHAPE
+    assert lib.psgdk_symm(0, 2, 1, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
+    assert lib.psgdk_symm(0, 1, 0, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
+    assert lib.psgdk_symm(0, 0, 3, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
+
+
+def test_workspace_queries_need_no_device():
+    lib = L.lib()
+    sz = C.c_size_t(0)
+    assert lib.psgdk_norm_lower_bound(768, 1, 12, None, 768, None, None, None, C.byref(sz), None) == L.OK
+    n, nb = 768, 12
+    T = (n + 63) // 64
+    assert sz.value >= nb * (2 * 32 * n + T * T * 64) * 4
+    small = sz.value
+    assert lib.psgdk_norm_lower_bound(3072, 1, 12, None, 3072, None, None, None, C.byref(sz), None) == L.OK
+    assert sz.value > small
+    # too small a workspace is an error, not an overrun
+    g = L.Kron2d()
+    g.nb, g.prec, g.m, g.n = 1, 0, 64, 32
+    g.kind[0], g.kind[1] = L.FACTOR_DENSE, L.FACTOR_DIAG
+    for f in range(2):
+        g.Q[f][0] = g.P[f][0] = g.L[f][0] = 0x1000
+    g.G[0] = 0x1000
+    o = L.UpdateOpts(0.1, 0.9, 1e-9, 1.19e-7, 0, 0)
+    assert lib.psgdk_kron2d_update(g, o, L.ptrs([0x1000]), L.ptrs([0x1000]), None, C.byref(sz), None) == L.OK
+    need = sz.value
+    assert need > 3 * 64 * 32 * 4
+    tiny = C.c_size_t(16)
+    assert lib.psgdk_kron2d_update(g, o, L.ptrs([0x1000]), L.ptrs([0x1000]), C.c_void_p(0x1000), C.byref(tiny),
+                                   None) == L.EWORKSPACE
+
+
+def test_group_validation():
+    lib = L.lib()
+    sz = C.c_size_t(0)
+    g = L.Kron2d()
+    g.nb, g.prec, g.m, g.n = 1, 0, 4, 8
+    g.kind[0], g.kind[1] = L.FACTOR_NONE, L.FACTOR_DENSE  # NONE needs size 1
+    g.G[0] = 0x1000
+    for f in range(2):
+        g.Q[f][0] = g.P[f][0] = g.L[f][0] = 0x1000
+    o = L.UpdateOpts(0.1, 0.9, 1e-9, 1.19e-7, 0, 0)
+    assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.ESHAPE
+    g.kind[0] = 7
+    assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.EINVAL
+    g.kind[0] = L.FACTOR_DENSE
+    g.Q[0][0] = None
+    assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.EINVAL
+    assert "Q" in _err()
+    o.r2 = 1
+    g.Q[0][0] = 0x1000
+    assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.EINVAL
+
+
+def test_python_surface_on_cpu():
+    """The optimizer and the ops refuse CPU tensors with a clear error (no silent CPU path)."""
+    from psgd_pro_amd import KronWhiten, make_ops
+    W = torch.zeros(8, 8, requires_grad=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        KronWhiten([W], preconditioner_init_scale=1.0)
+    ops = make_ops(())
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ops.syrk(torch.zeros(4, 4), False)
+    with pytest.raises(ValueError):
+        make_ops({"nan"})
+    with pytest.raises(ValueError):
+        KronWhiten([W], compile="default")
