@@ -226,7 +226,7 @@ class OracleKron:
                  preconditioner_init_scale=None, lr_params=0.001, lr_preconditioner=0.1, betaL=0.9, damping=1e-9,
                  momentum=0.0, grad_clip_max_amps=(2.0, 10.0), preconditioner_update_probability=1.0,
                  update_preconditioner_first=True, whiten_grad=True, seed=0, dtype=None, grad_eps=None, r2=False):
-        self.params = list(params)
+        self.params = list(params)  # updated in place
         self.max_size, self.max_skew = preconditioner_max_size, preconditioner_max_skew
         self.lr_params, self.lr_preconditioner = lr_params, lr_preconditioner
         self.betaL, self.damping = betaL, damping

@@ -240,7 +240,7 @@ int run_nlb(int64_t n, int sign, int nb, const float* const* A, int64_t lda, boo
 // ------------------------------------------------------------------------------------------------------------
 // Kron 2-D group helpers
 
-int check_group(const psgdk_kron2d_t* g) {
+int check_group(const psgdk_kron2d_t* g, bool need_g = true) {
   if (!g) return fail(PSGDK_EINVAL, "null group");
   PSGDK_TRY(check_nb(g->nb));
   PSGDK_TRY(check_prec(g->prec));
@@ -260,7 +260,7 @@ int check_group(const psgdk_kron2d_t* g) {
       PSGDK_TRY(check_ptrs(g->L[f], g->nb, "L"));
     }
   }
-  PSGDK_TRY(check_ptrs(g->G, g->nb, "G"));
+  if (need_g) PSGDK_TRY(check_ptrs(g->G, g->nb, "G"));
   return PSGDK_OK;
 }
 
@@ -744,7 +744,7 @@ int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, voi
 }
 
 int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, psgdk_stream_t stream) {
-  PSGDK_TRY(check_group(g));
+  PSGDK_TRY(check_group(g, false));
   int sel[MAXB];
   for (int b = 0; b < g->nb; ++b) sel[b] = b;
   for (int f = 0; f < 2; ++f) {
@@ -757,7 +757,7 @@ int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, ps
 
 int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri, void* ws, size_t* ws_bytes,
                          psgdk_stream_t stream) {
-  PSGDK_TRY(check_group(g));
+  PSGDK_TRY(check_group(g, false));
   if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
   constexpr int PB = 64;  // partial maxima per factor
   Ws w(ws);

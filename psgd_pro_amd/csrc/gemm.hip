@@ -22,6 +22,8 @@ namespace psgdk {
 
 enum LoadHow : int { LD_KC = 0, LD_MC = 1, LD_SCALAR = 2, LD_ZERO = 3 };
 
+constexpr int KCHUNK = 128;  // k per accumulation chunk
+
 template <int PREC> struct Prec;
 template <> struct Prec<0> { static constexpr int BK = 32, CE = 4, ESZ = 4; };
 template <> struct Prec<1> { static constexpr int BK = 64, CE = 8, ESZ = 2; };
@@ -236,6 +238,15 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
   }
   __syncthreads();
 
+  // The k loop accumulates KCHUNK-wide chunks in `part` and folds each chunk into `acc`: one long fp32 FMA chain over
+  // all of K carries several times the rounding error of blocked summation against an fp64 product.
+  constexpr int KC_TILES = KCHUNK / BK;
+  f32x4_t part[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
@@ -259,7 +270,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < FN; ++j) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], part[i][j], 0, 0, 0);
       }
     } else {
 #pragma unroll
@@ -276,8 +287,17 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bfr[j][s], part[i][j], 0, 0, 0);
       }
+    }
+    if ((kt + 1) % KC_TILES == 0 || !more) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          acc[i][j] += part[i][j];
+          part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
     }
     if (more) {
       la.store(As0 + (cur ^ 1) * ASZ);

@@ -279,9 +279,13 @@ class KronWhiten:
     def step_math(self, grads):
         """One step with the gradients given (psgd_pro_fast.py:441-490)."""
         grads = [g.squeeze() for g in grads]
-        for i, g in enumerate(grads):
+        for i, (g, p) in enumerate(zip(grads, self._params_with_grad)):
             if g.dtype not in (torch.float32, torch.bfloat16):
                 raise TypeError(f"gradient {i}: float32 or bfloat16 expected, got {g.dtype}")
+            if g.device != p.device or not g.is_cuda:
+                raise RuntimeError(f"gradient {i} is on {g.device}; its parameter is on {p.device} (GPU expected)")
+            if g.numel() != p.numel():
+                raise RuntimeError(f"gradient {i} has {g.numel()} elements, its parameter {p.numel()}")
         grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
         if self._params is None:
             # psgd_pro.py:329-332: scale = (max_p mean|g|^4 + damping^4)^(-1/8) (one host read at initialisation)
