@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the PSGD-Kron preconditioner update + gradient apply on one MI355X.
+
+Default workload (one line of JSON on stdout): one optimizer step (preconditioner update of every factor, then
+precondition + clip + parameter update) over the ViT-B/16 weight set, 12 blocks x {qkv 768x2304, proj 768x768,
+fc1 768x3072, fc2 3072x768} = 48 weights, bf16 gradients N(0, 1e-4) resident in HBM, fp32 Kron factors initialised
+to the identity, max_size 8192, max_skew inf (every side dense), update probability 1, contractions on the bf16
+MFMA path (fp32 accumulate). Synthetic data; weights random-initialised.
+
+    python bench.py [--steps K] [--warmup W] [--precision bf16|fp32] [--skew inf|1] [--no-cpu]
+    python bench.py --config syrk      # SYRK / TRMM microbenchmark lines (n = k in 512..4096, fp32 and bf16)
+
+`roofline` is measured live: every MFMA-engine launch in the timed steps is bracketed by HIP events on its stream;
+the dominant kernel instantiation (largest total time) is reported with its algorithmic TFLOP/s against the bf16
+(or fp32) MFMA peak. `traffic` (HBM bytes per launch of that kernel) comes from the committed rocprofv3 counter
+summary when present. `cpu_baseline` times the CPU oracle (oracle/psgd_oracle.py, float32, torch CPU threads) on
+one ViT-B block (4 of the 48 weights) and scales it to the whole set.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"bf16": 2516.6, "fp32": 157.3}  # TFLOP/s, MI355X dense MFMA
+VIT_B = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+METRIC = "Kron update+apply ms/step & SYRK TFLOP/s (% MFMA peak) at ViT-B shapes, 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_bf16_vitb16_traffic.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
+    ap.add_argument("--skew", default="inf")
+    ap.add_argument("--blocks", type=int, default=12)
+    ap.add_argument("--config", choices=["vitb", "syrk", "copy"], default="vitb")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary (lines `kernel: ...` and
+    `bytes_per_launch: ...`), or None."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    k = b = None
+    for ln in lines:
+        if ln.startswith("kernel:"):
+            k = ln.split(":", 1)[1].strip()
+        if ln.startswith("bytes_per_launch:"):
+            b = float(ln.split(":", 1)[1].strip())
+    return b if (k == kernel and b is not None) else None
+
+
+def aggregate(recs):
+    """Per kernel instantiation: launches, total ms, total algorithmic flops; plus the SYRK subset."""
+    agg, syrk = {}, {}
+    for kid, tri, nb, ms, fl in recs:
+        a = agg.setdefault(kid, [0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += ms
+        a[2] += fl
+        if tri:
+            s = syrk.setdefault(kid, [0, 0.0, 0.0])
+            s[0] += 1
+            s[1] += ms
+            s[2] += fl
+    return agg, syrk
+
+
+def cpu_baseline(precision, skew, seconds):
+    """The CPU oracle (float32) on one ViT-B block (4 weights), 1 warmup step, then timed steps until `seconds` of
+    work; scaled x12 to the 48-weight set."""
+    import torch
+    from oracle import psgd_oracle as O
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
+    grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).float() for s in VIT_B]
+    W = [torch.zeros(s) for s in VIT_B]
+    eps = torch.finfo(torch.bfloat16).eps if precision == "bf16" else None
+    ora = O.OracleKron(W, preconditioner_max_size=8192, preconditioner_max_skew=skew, preconditioner_init_scale=1.0,
+                       seed=0, dtype=torch.float32, grad_eps=eps)
+    ora.step(grads)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        ora.step(grads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > seconds or len(times) >= 20:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return dict(value=round(med * 1e3 * 12, 2), unit="ms/step", cores=threads, kind="port",
+                sample=f"oracle float32 on 1 ViT-B block (4 of 48 weights), median of {len(times)} steps after 1 "
+                       f"warmup, x12")
+
+
+def bench_vitb(args):
+    import torch
+    from oracle.psgd_oracle import flops_2d, is_dense
+    from psgd_pro_amd import KronWhiten
+    from psgd_pro_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    skew = math.inf if args.skew == "inf" else float(args.skew)
+    shapes = VIT_B * args.blocks
+    gen = torch.Generator().manual_seed(0)
+    params = [(0.02 * torch.randn(s, generator=gen)).to(dev).requires_grad_(True) for s in shapes]
+    grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
+    opt = KronWhiten(params, preconditioner_max_size=8192, preconditioner_max_skew=skew,
+                     preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0)
+    flops_step = sum(flops_2d(m, n, is_dense(m, m * n, 8192, skew), is_dense(n, m * n, 8192, skew))
+                     for m, n in shapes)
+    for _ in range(args.warmup):
+        opt.step_math(grads)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    L.profile_start()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        opt.step_math(grads)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    recs = L.profile_stop()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+    ev_ms = e0.elapsed_time(e1) / args.steps
+    agg, syrk = aggregate(recs)
+    kid = max(agg, key=lambda k: agg[k][1])
+    n_l, ms_tot, fl_tot = agg[kid]
+    prec_of = "bf16" if (kid >= 5000 or (kid % 1000) // 100 == 1) else "fp32"
+    achieved = fl_tot / (ms_tot * 1e-3) / 1e12
+    kname = L.kernel_name(kid)
+    traffic = read_traffic(kname)
+    s_l = sum(v[0] for v in syrk.values())
+    s_ms = sum(v[1] for v in syrk.values())
+    s_fl = sum(v[2] for v in syrk.values())
+    syrk_tf = s_fl / (s_ms * 1e-3) / 1e12 if s_ms else 0.0
+    mfma_ms = sum(v[1] for v in agg.values()) / args.steps
+    out = {
+        "metric": METRIC,
+        "value": round(wall_ms, 3),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.precision,
+        "data": "synthetic",
+        "config": {"workload": "vit-b16-kron-update-apply", "weights": "12 x {768x2304, 768x768, 768x3072, 3072x768}",
+                   "blocks": args.blocks, "grad_dtype": "bf16", "factor_dtype": "fp32", "max_size": 8192,
+                   "max_skew": args.skew, "update_probability": 1.0, "parallelism": "none"},
+        "gpu_ms_per_step": round(ev_ms, 3),
+        "algorithmic_tflop_per_step": round(flops_step / 1e12, 4),
+        "tflops": round(flops_step / (wall_ms * 1e-3) / 1e12, 2),
+        "mfma_ms_per_step": round(mfma_ms, 3),
+        "syrk": {"tflops": round(syrk_tf, 2), "frac": round(syrk_tf / PEAK[args.precision], 4),
+                 "launches_per_step": s_l / args.steps, "ms_per_step": round(s_ms / args.steps, 3)},
+        "roofline": {"bound": "mfma", "kernel": kname, "launches_per_step": n_l / args.steps,
+                     "avg_launch_us": round(ms_tot * 1e3 / n_l, 2),
+                     "flops_per_launch": fl_tot / n_l,
+                     "achieved": round(achieved, 2), "peak": PEAK[prec_of], "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK[prec_of], 4), "traffic": traffic},
+        "kernels": {L.kernel_name(k): {"launches_per_step": v[0] / args.steps, "ms_per_step": round(v[1] / args.steps, 3),
+                                       "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2)} for k, v in agg.items()},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.precision, skew, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    return out
+
+
+def bench_syrk(args):
+    """SYRK C = triu(A A^T) (A n x k, n = k) and TRMM triu(Q) B microbenchmarks, fp32 and bf16 inputs."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    lines = []
+    dev = torch.device("cuda:0")
+    st = L.stream_of(torch.empty(1, device=dev))
+    for prec, name in ((1, "bf16"), (0, "fp32")):
+        dt = torch.bfloat16 if prec else torch.float32
+        for n in (512, 1024, 2048, 4096):
+            A = torch.randn(n, n, device=dev).to(dt)
+            C = torch.empty(n, n, device=dev)
+            adt = L.dtype_code(dt)
+            for _ in range(3):
+                L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+            torch.cuda.synchronize()
+            reps = max(5, int(2e10 / (n ** 3)))
+            L.profile_start()
+            for _ in range(reps):
+                L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+            recs = L.profile_stop()
+            ms = sum(r[3] for r in recs) / len(recs)
+            tf = n * (n + 1) * n / (ms * 1e-3) / 1e12
+            lines.append({"op": "syrk", "n": n, "k": n, "dtype": name, "us": round(ms * 1e3, 2),
+                          "tflops": round(tf, 2), "frac": round(tf / PEAK[name], 4)})
+            B = torch.randn(n, n, device=dev)
+            Af = A.float()
+            L.profile_start()
+            for _ in range(reps):
+                L.check(L.lib().psgdk_trmm(prec, n, n, 0, 1, L.ptrs([Af]), n, L.ptrs([B]), n, L.ptrs([C]), n, st))
+            recs = L.profile_stop()
+            ms = sum(r[3] for r in recs) / len(recs)
+            tf = n * n * (n + 1) / (ms * 1e-3) / 1e12
+            lines.append({"op": "trmm", "n": n, "dtype": name, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
+                          "frac": round(tf / PEAK[name], 4)})
+    return lines
+
+
+def bench_copy(args):
+    """Calibration for the HBM counters: one device-to-device copy of 256 MiB (read 256 MiB, write 256 MiB)."""
+    import torch
+    n = 64 * 1024 * 1024
+    x = torch.randn(n, device="cuda:0")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    return {"op": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 3}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the preconditioner "
+              f"would shard by parameter across GPUs, which is not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    if args.config == "copy":
+        print(json.dumps(bench_copy(args)), flush=True)
+        return
+    if args.config == "syrk":
+        for ln in bench_syrk(args):
+            print(json.dumps(ln), flush=True)
+        return
+    print(json.dumps(bench_vitb(args)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -115,6 +115,11 @@ typedef struct psgdk_kron2d {
   float* Q[2][PSGDK_MAXB];   /* dense: d x d; diagonal: d values; none: unused */
   float* P[2][PSGDK_MAXB];   /* Q^T Q (dense: full symmetric, or upper triangle with tri bit 1) or q * q */
   float* L[2][PSGDK_MAXB];   /* one float each: the factor's Lipschitz smoothness EMA */
+  /* bf16 shadows of dense factors for prec = PSGDK_PREC_BF16 (optional: NULL selects the general path): Qt16 is
+   * Q^T and P16 is P in bfloat16, d x d row-major. The library keeps them in step with Q and P (update, refresh,
+   * balance); psgdk_kron2d_refresh_p rebuilds both from the fp32 state. */
+  void* Qt16[2][PSGDK_MAXB];
+  void* P16[2][PSGDK_MAXB];
 } psgdk_kron2d_t;
 
 typedef struct psgdk_update_opts {
@@ -151,7 +156,8 @@ int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, voi
                        psgdk_stream_t stream);
 
 /* P = Q^T Q (dense) or q * q (diagonal) for the factors selected by factor_mask (bit f = factor f):
- * gram_2d (psgd_pro_fast.py:164-165,191-192,447-449). tri bit 1: P written as its upper triangle. */
+ * gram_2d (psgd_pro_fast.py:164-165,191-192,447-449). tri bit 1: P written as its upper triangle. With bf16
+ * shadows, Qt16 = bf16(Q^T) is rebuilt first and P16 written with P. */
 int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, psgdk_stream_t stream);
 
 /* Balance the factors of the parameters whose flag is set (host array of nb ints): q_f *= gmean / max|q_f|,
@@ -163,6 +169,22 @@ int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri,
 /* m = beta m + (1 - beta) g for nb tensors of numel elements (psgd_pro.py:340-341). */
 int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const* mom, const void* const* g,
                    psgdk_stream_t stream);
+
+/* Launch profiling (diagnostic, single host thread): after psgdk_profile_start every MFMA-engine launch is
+ * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
+ * waits for the recorded events and fills one record per launch: the kernel instantiation id
+ * (cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype; cfg 0 = 128 x 128 tiles, 1 = 32 x 128), whether it was a
+ * SYRK (triangular grid), the problems in the launch, its device time and its algorithmic flop count
+ * (SYRK n(n+1)k, TRMM n(n+1)p, GEMM 2mnk, per problem). With out NULL only *n_records is set (records kept). */
+typedef struct psgdk_prof_record {
+  int32_t kernel_id;
+  int32_t tri;
+  int32_t nb;
+  float ms;
+  double flops;
+} psgdk_prof_record_t;
+int psgdk_profile_start(void);
+int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
  * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B. Checks the compiler builtins' lane layout. */

@@ -31,7 +31,7 @@ class Kron2d(C.Structure):
     _fields_ = [("nb", C.c_int32), ("prec", C.c_int32), ("m", C.c_int64), ("n", C.c_int64),
                 ("kind", C.c_int32 * 2), ("g_dtype", C.c_int32), ("p_dtype", C.c_int32),
                 ("G", C.c_void_p * MAXB), ("Q", (C.c_void_p * MAXB) * 2), ("P", (C.c_void_p * MAXB) * 2),
-                ("L", (C.c_void_p * MAXB) * 2)]
+                ("L", (C.c_void_p * MAXB) * 2), ("Qt16", (C.c_void_p * MAXB) * 2), ("P16", (C.c_void_p * MAXB) * 2)]
 
 
 class UpdateOpts(C.Structure):
@@ -42,6 +42,11 @@ class UpdateOpts(C.Structure):
 class ApplyOpts(C.Structure):
     _fields_ = [("lr_params", C.c_float), ("max_avg_amp", C.c_float), ("max_element_amp", C.c_float),
                 ("tri", C.c_int32)]
+
+
+class ProfRecord(C.Structure):
+    _fields_ = [("kernel_id", C.c_int32), ("tri", C.c_int32), ("nb", C.c_int32), ("ms", C.c_float),
+                ("flops", C.c_double)]
 
 
 _SIGS = {
@@ -61,6 +66,8 @@ _SIGS = {
     "psgdk_kron2d_refresh_p": (_i32, [C.POINTER(Kron2d), _i32, _i32, _vp]),
     "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
     "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),
+    "psgdk_profile_start": (_i32, []),
+    "psgdk_profile_stop": (_i32, [C.POINTER(ProfRecord), _i32, C.POINTER(C.c_int)]),
     "psgdk_debug_mfma": (_i32, [_i32, _vp, _vp, _vp, _vp]),
 }
 
@@ -124,6 +131,32 @@ class Workspace:
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
             self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
         return self.buf
+
+
+def kernel_name(kernel_id):
+    """Kernel template name of a profiling kernel id."""
+    if kernel_id >= 5000:
+        t = 128 if kernel_id % 10 else 256
+        return f"gemm_bf16_kernel<{t}, {t}>"
+    cfg, rest = divmod(kernel_id, 1000)
+    prec, rest = divmod(rest, 100)
+    adt, bdt = divmod(rest, 10)
+    t = {0: "float", 1: "unsigned short"}
+    tile = "32, 128, 1, 4" if cfg else "128, 128, 2, 2"
+    return f"gemm_kernel<{prec}, {t[adt]}, {t[bdt]}, {tile}>"
+
+
+def profile_start():
+    check(lib().psgdk_profile_start())
+
+
+def profile_stop():
+    """List of (kernel_id, tri, nb, ms, flops) for the launches since profile_start()."""
+    n = C.c_int(0)
+    check(lib().psgdk_profile_stop(None, 0, C.byref(n)))
+    arr = (ProfRecord * max(1, n.value))()
+    check(lib().psgdk_profile_stop(arr, n.value, C.byref(n)))
+    return [(r.kernel_id, r.tri, r.nb, r.ms, r.flops) for r in arr[:n.value]]
 
 
 def call_ws(fn, *args, ws, device, stream):

@@ -7,10 +7,12 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/psgdk.h"
 #include "elem.h"
 #include "gemm.h"
+#include "gemm_bf16.h"
 #include "nlb.h"
 
 namespace psgdk {
@@ -96,6 +98,29 @@ int check_dims(int64_t v, const char* name) {
   return PSGDK_OK;
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Launch profiling (psgdk_profile_start / _stop): a HIP event pair around every MFMA-engine launch, recorded on the
+// launch's stream, with the launch's kernel instantiation and algorithmic flop count. Diagnostic; one thread.
+struct ProfRec {
+  int kernel_id, tri, nb;
+  double flops;
+  hipEvent_t a, b;
+};
+struct Prof {
+  bool on = false;
+  std::vector<ProfRec> recs;
+  std::vector<hipEvent_t> pool;
+  hipEvent_t ev() {
+    if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+} g_prof;
+
+// Instantiation id of gemm_kernel<PREC, TA, TB, tile config>: cfg * 1000 + prec * 100 + adt * 10 + bdt.
+int kernel_id(int prec, int adt, int bdt, int cfg) { return cfg * 1000 + prec * 100 + adt * 10 + bdt; }
+
 void gemm_init(GemmArgs& a) {
   std::memset(&a, 0, sizeof a);
   a.alpha = 1.f;
@@ -145,7 +170,78 @@ int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, c
     a.A[b] = A.p[b]; a.B[b] = B.p[b]; a.C[b] = C[b];
     a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
   }
-  return hip_check(gemm_launch(a, prec, A.dt, B.dt, gemm_cfg(M), st), "gemm launch");
+  const int cfg = gemm_cfg(M);
+  if (!g_prof.on) return hip_check(gemm_launch(a, prec, A.dt, B.dt, cfg, st), "gemm launch");
+  ProfRec r;
+  r.kernel_id = kernel_id(prec, A.dt, B.dt, cfg);
+  r.tri = tri;
+  r.nb = nb;
+  if (tri) r.flops = (double)M * (M + 1) * K * nb;                    // SYRK: n(n+1)k
+  else if (kbeg_tri) r.flops = (double)M * (M + 1) * N * nb;         // TRMM: n(n+1)p
+  else r.flops = 2.0 * M * N * K * nb;
+  r.a = g_prof.ev();
+  r.b = g_prof.ev();
+  if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
+  PSGDK_HIP(hipEventRecord(r.a, st), "profiling event");
+  PSGDK_TRY(hip_check(gemm_launch(a, prec, A.dt, B.dt, cfg, st), "gemm launch"));
+  PSGDK_HIP(hipEventRecord(r.b, st), "profiling event");
+  g_prof.recs.push_back(r);
+  return PSGDK_OK;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// bf16 k-contiguous GEMM (gemm_bf16.hip). A: M x K rows, B: N x K rows (bf16, k contiguous); C = acc A B^T.
+struct B16Out {
+  float* C[MAXB] = {};
+  bf16_t* Cb[MAXB] = {};
+  bf16_t* CTb[MAXB] = {};
+  int64_t ldc = 0, ldcb = 0, ldct = 0;
+};
+
+int b16_cfg(int64_t M, int64_t N, int tri, int nb) { return gemm_bf16_tiles(M, N, tri, 0) * nb >= 160 ? 0 : 1; }
+
+// Operand contract of gemm_bf16: K and both leading dimensions multiples of 8, 16-byte aligned bases, each operand
+// under 2 GiB (buffer extent).
+template <typename P>
+bool b16_operands_ok(int nb, int64_t M, int64_t N, int64_t K, P const* A, int64_t lda, P const* B, int64_t ldb) {
+  if (K % 8 || lda % 8 || ldb % 8 || lda < K || ldb < K) return false;
+  if (M * lda * 2 >= ((int64_t)1 << 31) || N * ldb * 2 >= ((int64_t)1 << 31)) return false;
+  for (int b = 0; b < nb; ++b)
+    if (!aligned16(A[b]) || !aligned16(B[b])) return false;
+  return true;
+}
+
+int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64_t lda, const void* const* B,
+            int64_t ldb, const B16Out& o, const EpiSpec& e, int tri, int out_mode, int* ntiles, hipStream_t st) {
+  if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb))
+    return fail(PSGDK_EINVAL, "bf16 kernel operand contract violated (K, leading dimensions, alignment or size)");
+  GB16Args a;
+  std::memset(&a, 0, sizeof a);
+  a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.lda = lda; a.ldb = ldb; a.ldc = o.ldc; a.ldcb = o.ldcb; a.ldct = o.ldct; a.ldx = e.ldx;
+  a.alpha = e.alpha; a.epi = e.epi; a.tri = tri; a.out_mode = out_mode; a.nb = nb;
+  for (int b = 0; b < nb; ++b) {
+    a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
+    a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
+    a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b];
+    a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
+  }
+  const int cfg = b16_cfg(M, N, tri, nb);
+  if (ntiles) *ntiles = gemm_bf16_tiles(M, N, tri, cfg);
+  if (!g_prof.on) return hip_check(gemm_bf16_launch(a, cfg, st), "bf16 gemm launch");
+  ProfRec r;
+  r.kernel_id = 5000 + cfg;
+  r.tri = tri;
+  r.nb = nb;
+  r.flops = tri ? (double)M * (M + 1) * K * nb : 2.0 * M * N * K * nb;
+  r.a = g_prof.ev();
+  r.b = g_prof.ev();
+  if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
+  PSGDK_HIP(hipEventRecord(r.a, st), "profiling event");
+  PSGDK_TRY(hip_check(gemm_bf16_launch(a, cfg, st), "bf16 gemm launch"));
+  PSGDK_HIP(hipEventRecord(r.b, st), "profiling event");
+  g_prof.recs.push_back(r);
+  return PSGDK_OK;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -348,8 +444,52 @@ int precondition(const psgdk_kron2d_t* g, const void* const* X, int xdt, float* 
   return PSGDK_OK;
 }
 
+// The bf16 path with k-contiguous bf16 operands applies to groups with two dense factors, bf16 shadows for both,
+// rows of whole 16-byte vectors and full (not triangle) storage.
+bool b16_group(const psgdk_kron2d_t* g, int tri) {
+  if (g->prec != PSGDK_PREC_BF16 || tri) return false;
+  if (g->kind[0] != PSGDK_FACTOR_DENSE || g->kind[1] != PSGDK_FACTOR_DENSE) return false;
+  if (g->m % 8 || g->n % 8) return false;
+  for (int f = 0; f < 2; ++f)
+    for (int b = 0; b < g->nb; ++b)
+      if (!g->Qt16[f][b] || !g->P16[f][b] || !aligned16(g->Qt16[f][b]) || !aligned16(g->P16[f][b])) return false;
+  for (int b = 0; b < g->nb; ++b)
+    if (!aligned16(g->G[b])) return false;
+  const int64_t big = std::max(g->m, g->n);
+  if (big * big * 2 >= ((int64_t)1 << 31) || g->m * g->n * 2 >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+bool has_shadows(const psgdk_kron2d_t* g, int f, const int* sel, int nsel) {
+  if (g->prec != PSGDK_PREC_BF16 || g->kind[f] != PSGDK_FACTOR_DENSE) return false;
+  const int64_t d = f == 0 ? g->m : g->n;
+  if (d % 8 || d * d * 2 >= ((int64_t)1 << 31)) return false;
+  for (int i = 0; i < nsel; ++i)
+    if (!g->Qt16[f][sel[i]] || !g->P16[f][sel[i]] || !aligned16(g->Qt16[f][sel[i]]) || !aligned16(g->P16[f][sel[i]]))
+      return false;
+  return true;
+}
+
 int refresh_p_dense(const psgdk_kron2d_t* g, int f, int tri, const int* sel, int nsel, hipStream_t st) {
   const int64_t d = f == 0 ? g->m : g->n;
+  if (!(tri & 2) && has_shadows(g, f, sel, nsel)) {
+    // Qt16 = bf16(Q^T), then P = Qt16 Qt16^T (= Q^T Q) with its bf16 copy
+    EwArgs c;
+    std::memset(&c, 0, sizeof c);
+    c.nb = nsel; c.m = d; c.n = d; c.ld = d; c.i0 = 1;
+    for (int i = 0; i < nsel; ++i) { c.in[i] = g->Q[f][sel[i]]; c.out2[i] = g->Qt16[f][sel[i]]; }
+    PSGDK_HIP(to_bf16_launch(c, st), "Q^T shadow");
+    const void* A[MAXB];
+    B16Out o;
+    o.ldc = d; o.ldcb = d;
+    for (int i = 0; i < nsel; ++i) {
+      A[i] = g->Qt16[f][sel[i]];
+      o.C[i] = g->P[f][sel[i]];
+      o.Cb[i] = reinterpret_cast<bf16_t*>(g->P16[f][sel[i]]);
+    }
+    EpiSpec e;
+    return run_b16(nsel, d, d, d, A, d, A, d, o, e, 1, PSGDK_OUT_MIRROR, nullptr, st);
+  }
   Opnd A;
   A.mode = MC; A.ld = d;
   float* C[MAXB];
@@ -365,6 +505,221 @@ int refresh_p_diag(const psgdk_kron2d_t* g, int f, const int* sel, int nsel, hip
   a.nb = nsel; a.m = 1; a.n = d; a.dt = PSGDK_F32;
   for (int i = 0; i < nsel; ++i) { a.in[i] = g->Q[f][sel[i]]; a.in3[i] = g->Q[f][sel[i]]; a.out[i] = g->P[f][sel[i]]; }
   return hip_check(diag_scale_launch(a, st), "diag P refresh");
+}
+
+// One preconditioner update of a bf16-path group (b16_group): every contraction on gemm_bf16 with k-contiguous bf16
+// operands; producers write the bf16 (and transposed) copies their consumers read.
+//   X  = G + (damping + eps |G|) N                      -> Xb
+//   Y  = X P2            (A = Xb,   B = P2 shadow)      -> Y^T bf16
+//   Pg = P1 Y            (A = P1 shadow, B = Y^T)       -> Pg bf16, Pg^T bf16
+//   per factor: term1 = SYRK (Pg or Pg^T) -> fp32 + bf16; bound, L, lr/L; Qn = Q - lr/L (term1 Q - term2 Q)
+//   (B = Q^T shadow) -> fp32 + Qn^T bf16; R = Qn^T - Qn -> fp32 + bf16; skew bound; RQ (B = Qn^T) -> fp32 +
+//   RQ^T bf16 + traces; step size; Q = Qn + a RQ + a^2/2 R RQ (B = RQ^T) -> Q fp32 + Q^T shadow
+//   P = Q^T Q (SYRK of the Q^T shadow) -> P fp32 + P shadow
+int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+               const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st) {
+  const int nb = g->nb;
+  const int64_t m = g->m, n = g->n, mn = m * n, dmx = std::max(m, n);
+  const int64_t dims[2] = {m, n};
+  Ws w(ws);
+  bf16_t *Xb[MAXB], *YTb[MAXB], *Pgb[MAXB], *PgTb[MAXB], *T1b[MAXB], *QnTb[MAXB], *Rb[MAXB], *RQTb[MAXB];
+  float *T1[MAXB], *Qn[MAXB], *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
+  const int tp = gemm_bf16_tiles(dmx, dmx, 0, 1);
+  for (int b = 0; b < nb; ++b) {
+    Xb[b] = w.take<bf16_t>(mn);
+    YTb[b] = w.take<bf16_t>(mn);
+    Pgb[b] = w.take<bf16_t>(mn);
+    PgTb[b] = w.take<bf16_t>(mn);
+    T1b[b] = w.take<bf16_t>(dmx * dmx);
+    QnTb[b] = w.take<bf16_t>(dmx * dmx);
+    Rb[b] = w.take<bf16_t>(dmx * dmx);
+    RQTb[b] = w.take<bf16_t>(dmx * dmx);
+    T1[b] = w.take<float>(dmx * dmx);
+    Qn[b] = w.take<float>(dmx * dmx);
+    R[b] = w.take<float>(dmx * dmx);
+    RQ[b] = w.take<float>(dmx * dmx);
+    coef[b] = w.take<float>(4);
+    rs[b] = w.take<float>(4);
+    pc[b] = w.take<float>(4);
+    tpart[b] = w.take<float>(2 * (size_t)tp);
+  }
+  NlbWs nw;
+  nlb_take(w, dmx, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(noise, nb, "noise"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = o->damping; a.f1 = o->grad_eps;
+    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[b]; a.out2[b] = Xb[b]; }
+    PSGDK_HIP(noise_launch(a, st), "noise");
+  }
+  const void *A[MAXB], *B[MAXB];
+  {  // Y = X P2 -> Y^T
+    B16Out out;
+    out.ldct = m;
+    for (int b = 0; b < nb; ++b) { A[b] = Xb[b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[b]; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+  }
+  {  // Pg = P1 Y -> Pg, Pg^T
+    B16Out out;
+    out.ldcb = n; out.ldct = m;
+    for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[b]; out.Cb[b] = Pgb[b]; out.CTb[b] = PgTb[b]; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, nullptr, st));
+  }
+  int64_t voff = 0;
+  for (int f = 0; f < 2; ++f) {
+    const int64_t d = dims[f], other = dims[1 - f];
+    const float term2 = (float)mn / (float)d;
+    {  // term1 = Pg Pg^T (f = 0) or Pg^T Pg (f = 1), full symmetric fp32 + bf16
+      B16Out out;
+      out.ldc = d; out.ldcb = d;
+      for (int b = 0; b < nb; ++b) { A[b] = f == 0 ? (const void*)Pgb[b] : (const void*)PgTb[b]; out.C[b] = T1[b]; out.Cb[b] = T1b[b]; }
+      EpiSpec e;
+      PSGDK_TRY(run_b16(nb, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
+    }
+    const float *Vs[MAXB], *Vk[MAXB];
+    for (int b = 0; b < nb; ++b) { Vs[b] = V[b] + voff; Vk[b] = V[b] + voff + NLB_K * d; }
+    voff += 2 * NLB_K * d;
+    {
+      NlbFinal fin;
+      std::memset(&fin, 0, sizeof fin);
+      fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL; fin.term2 = term2;
+      const float* T1c[MAXB];
+      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; T1c[b] = T1[b]; }
+      PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, true, Vs, fin, nw, st));
+    }
+    {  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16
+      B16Out out;
+      out.ldc = d; out.ldct = d;
+      EpiSpec e;
+      e.epi = EPI_FACTOR; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        A[b] = T1b[b]; B[b] = g->Qt16[f][b]; out.C[b] = Qn[b]; out.CTb[b] = QnTb[b];
+        e.X1[b] = g->Q[f][b]; e.s[b] = coef[b];
+      }
+      PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+    }
+    {  // R = Qn^T - Qn -> fp32 + bf16
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
+      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out[b] = R[b]; a.out2[b] = Rb[b]; }
+      PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
+    }
+    {
+      NlbFinal fin;
+      std::memset(&fin, 0, sizeof fin);
+      fin.mode = NLB_FINAL_SCALE;
+      const float* Rc[MAXB];
+      for (int b = 0; b < nb; ++b) { fin.coef[b] = rs[b]; Rc[b] = R[b]; }
+      PSGDK_TRY(run_nlb(d, -1, nb, Rc, d, true, Vk, fin, nw, st));
+    }
+    int nt = 0;
+    {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials
+      B16Out out;
+      out.ldc = d; out.ldct = d;
+      EpiSpec e;
+      e.epi = EPI_RQ; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        A[b] = Rb[b]; B[b] = QnTb[b]; out.C[b] = RQ[b]; out.CTb[b] = RQTb[b];
+        e.X1[b] = R[b]; e.s[b] = rs[b]; e.part[b] = tpart[b];
+      }
+      PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, &nt, st));
+    }
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.i0 = nt; a.f0 = 0.125f;
+      for (int b = 0; b < nb; ++b) { a.in2[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
+      PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
+    }
+    {  // Q = Qn + a RQ + a^2/2 R RQ -> Q fp32 + Q^T shadow
+      B16Out out;
+      out.ldc = d; out.ldct = d;
+      EpiSpec e;
+      e.epi = EPI_PROC; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        A[b] = Rb[b]; B[b] = RQTb[b]; out.C[b] = g->Q[f][b]; out.CTb[b] = reinterpret_cast<bf16_t*>(g->Qt16[f][b]);
+        e.X1[b] = Qn[b]; e.X2[b] = RQ[b]; e.s[b] = pc[b];
+      }
+      PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+    }
+  }
+  for (int f = 0; f < 2; ++f) {  // P = Q^T Q from the fresh Q^T shadow
+    const int64_t d = dims[f];
+    B16Out out;
+    out.ldc = d; out.ldcb = d;
+    for (int b = 0; b < nb; ++b) {
+      A[b] = g->Qt16[f][b];
+      out.C[b] = g->P[f][b];
+      out.Cb[b] = reinterpret_cast<bf16_t*>(g->P16[f][b]);
+    }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, d, d, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
+  }
+  return PSGDK_OK;
+}
+
+// Precondition + clip + update of a bf16-path group: Y = G P2 (A = G bf16, B = P2 shadow) -> Y^T bf16;
+// pre = P1 Y (A = P1 shadow, B = Y^T) -> fp32 + sum-of-squares partials; clip + update.
+int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params, float* const* pre_out,
+              float* const* clipped_out, void* ws, size_t* ws_bytes, hipStream_t st) {
+  const int nb = g->nb;
+  const int64_t m = g->m, n = g->n, mn = m * n;
+  Ws w(ws);
+  bf16_t *Gb[MAXB], *YTb[MAXB];
+  float *pre[MAXB], *part[MAXB];
+  const int np_max = gemm_bf16_tiles(m, n, 0, 1);
+  const bool conv = g->g_dtype != PSGDK_BF16;
+  for (int b = 0; b < nb; ++b) {
+    Gb[b] = conv ? w.take<bf16_t>(mn) : nullptr;
+    YTb[b] = w.take<bf16_t>(mn);
+    pre[b] = w.take<float>(mn);
+    part[b] = w.take<float>(2 * (size_t)np_max);
+  }
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(params, nb, "params"));
+  for (int b = 0; b < nb; ++b)
+    if (pre_out && pre_out[b]) pre[b] = pre_out[b];
+  const void *A[MAXB], *B[MAXB];
+  if (conv) {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype;
+    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.out2[b] = Gb[b]; }
+    PSGDK_HIP(noise_launch(a, st), "G to bf16");
+  }
+  {
+    B16Out out;
+    out.ldct = m;
+    for (int b = 0; b < nb; ++b) { A[b] = conv ? (const void*)Gb[b] : g->G[b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[b]; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+  }
+  int np = 0;
+  {
+    B16Out out;
+    out.ldc = n;
+    EpiSpec e;
+    e.epi = EPI_SUMSQ;
+    for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[b]; out.C[b] = pre[b]; e.part[b] = part[b]; }
+    PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, &np, st));
+  }
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.m = m; a.n = n; a.dt = g->p_dtype; a.i0 = np;
+  a.f0 = o->max_avg_amp; a.f1 = o->max_element_amp; a.f2 = o->lr_params;
+  for (int b = 0; b < nb; ++b) {
+    a.in[b] = params[b]; a.in2[b] = pre[b]; a.in3[b] = part[b];
+    a.out2[b] = clipped_out ? clipped_out[b] : nullptr;
+  }
+  return hip_check(clip_update_launch(a, st), "clip + update");
 }
 
 }  // namespace
@@ -387,6 +742,14 @@ int psgdk_syrk(int prec, int trans, int out_mode, int64_t n, int64_t k, int a_dt
   if (out_mode < 0 || out_mode > 2) return fail(PSGDK_EINVAL, "out_mode = %d", out_mode);
   if (lda < (trans ? n : k)) return fail(PSGDK_ESHAPE, "lda = %lld too small", (long long)lda);
   if (out_mode != PSGDK_OUT_PACKED && ldc < n) return fail(PSGDK_ESHAPE, "ldc = %lld < n", (long long)ldc);
+  if (prec == PSGDK_PREC_BF16 && a_dtype == PSGDK_BF16 && !trans && out_mode != PSGDK_OUT_PACKED &&
+      b16_operands_ok(nb, n, n, k, A, lda, A, lda)) {
+    B16Out o;
+    o.ldc = ldc;
+    for (int b = 0; b < nb; ++b) o.C[b] = C[b];
+    EpiSpec e;
+    return run_b16(nb, n, n, k, A, lda, A, lda, o, e, 1, out_mode, nullptr, (hipStream_t)stream);
+  }
   Opnd a;
   a.mode = trans ? MC : KC; a.ld = lda; a.dt = a_dtype;
   for (int b = 0; b < nb; ++b) a.p[b] = A[b];
@@ -445,6 +808,15 @@ int psgdk_gemm(int prec, int trans_a, int trans_b, int64_t m, int64_t n, int64_t
   PSGDK_TRY(check_ptrs(B, nb, "B"));
   PSGDK_TRY(check_ptrs(C, nb, "C"));
   if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldc < n) return fail(PSGDK_ESHAPE, "leading dimension too small");
+  if (prec == PSGDK_PREC_BF16 && a_dtype == PSGDK_BF16 && b_dtype == PSGDK_BF16 && !trans_a && trans_b &&
+      beta == 0.f && b16_operands_ok(nb, m, n, k, A, lda, B, ldb)) {  // k-contiguous bf16 operands: bf16 kernel
+    B16Out o;
+    o.ldc = ldc;
+    for (int b = 0; b < nb; ++b) o.C[b] = C[b];
+    EpiSpec e;
+    e.alpha = alpha;
+    return run_b16(nb, m, n, k, A, lda, B, ldb, o, e, 0, 0, nullptr, (hipStream_t)stream);
+  }
   Opnd oa, ob;
   oa.mode = trans_a ? MC : KC; oa.ld = lda; oa.dt = a_dtype;
   ob.mode = trans_b ? KC : MC; ob.ld = ldb; ob.dt = b_dtype;
@@ -555,6 +927,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
   if (!o) return fail(PSGDK_EINVAL, "null options");
   if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
   if (o->r2) return fail(PSGDK_EINVAL, "r2 is not provided by this version");
+  if (b16_group(g, o->tri)) return b16_update(g, o, noise, V, ws, ws_bytes, (hipStream_t)stream);
   const int nb = g->nb;
   const int64_t m = g->m, n = g->n, mn = m * n, dmx = dense_max(g);
   const int64_t dims[2] = {m, n};
@@ -714,6 +1087,7 @@ int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, voi
   PSGDK_TRY(check_group(g));
   if (!o) return fail(PSGDK_EINVAL, "null options");
   if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  if (b16_group(g, o->tri)) return b16_apply(g, o, params, pre_out, clipped_out, ws, ws_bytes, (hipStream_t)stream);
   const int nb = g->nb;
   const int64_t m = g->m, n = g->n, mn = m * n;
   Ws w(ws);
@@ -821,6 +1195,34 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
   a.nb = nb; a.m = 1; a.n = numel; a.dt = g_dtype; a.f0 = beta;
   for (int b = 0; b < nb; ++b) { a.in[b] = g[b]; a.out[b] = mom[b]; }
   return hip_check(momentum_launch(a, (hipStream_t)stream), "momentum");
+}
+
+int psgdk_profile_start(void) {
+  for (auto& r : g_prof.recs) { g_prof.pool.push_back(r.a); g_prof.pool.push_back(r.b); }
+  g_prof.recs.clear();
+  g_prof.on = true;
+  return PSGDK_OK;
+}
+
+int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records) {
+  g_prof.on = false;
+  if (!n_records) return fail(PSGDK_EINVAL, "n_records is null");
+  const int n = (int)g_prof.recs.size();
+  *n_records = n;
+  if (!out) return PSGDK_OK;
+  if (max_records < n) return fail(PSGDK_EINVAL, "max_records %d < %d records", max_records, n);
+  for (int i = 0; i < n; ++i) {
+    ProfRec& r = g_prof.recs[i];
+    PSGDK_HIP(hipEventSynchronize(r.b), "profiling sync");
+    float ms = 0.f;
+    PSGDK_HIP(hipEventElapsedTime(&ms, r.a, r.b), "profiling elapsed");
+    out[i].kernel_id = r.kernel_id;
+    out[i].tri = r.tri;
+    out[i].nb = r.nb;
+    out[i].ms = ms;
+    out[i].flops = r.flops;
+  }
+  return PSGDK_OK;
 }
 
 int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream) {

@@ -20,9 +20,10 @@ struct EwArgs {
   float* sc[MAXB];         // device scalars
 };
 
-// X = G + (damping + eps |G|) * N                      (psgd_pro.py:121-123)
+// X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N null: X = G)  (psgd_pro.py:121-123)
 hipError_t noise_launch(const EwArgs& a, hipStream_t st);
-// R = Q^T - Q (sign = +1) or Q - Q^T (sign = -1), square d x d  (psgd_pro.py:87; psgd_pro_fast.py:147)
+// R = Q^T - Q (sign = +1) or Q - Q^T (sign = -1), square d x d, plus an optional bf16 copy in out2
+// (psgd_pro.py:87; psgd_pro_fast.py:147)
 hipError_t rform_launch(const EwArgs& a, hipStream_t st);
 // Procrustes step size from the trace partials     (psgd_pro.py:91-93)
 hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st);
@@ -46,5 +47,7 @@ hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
 hipError_t sumsq_launch(const EwArgs& a, hipStream_t st);
 // full symmetric matrix from the packed upper triangle
 hipError_t unpack_launch(const EwArgs& a, hipStream_t st);
+// bf16 copy (i0 = 0) or bf16 transposed copy (i0 = 1) of an fp32 matrix into out2 (m x n, leading dimension n)
+hipError_t to_bf16_launch(const EwArgs& a, hipStream_t st);
 
 }  // namespace psgdk

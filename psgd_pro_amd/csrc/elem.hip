@@ -35,9 +35,12 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   const void* G = a.in[b];
   const float* N = a.in2[b];
   float* X = a.out[b];
+  bf16_t* Xb = reinterpret_cast<bf16_t*>(a.out2[b]);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     const float g = ldv(G, a.dt, i);
-    X[i] = g + (a.f0 + a.f1 * fabsf(g)) * N[i];
+    const float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[i] : g;
+    if (X) X[i] = x;
+    if (Xb) Xb[i] = f32_to_bf16(x);
   }
 }
 hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
@@ -64,9 +67,14 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
     t[tx][r] = (gi < d && gj < d) ? Q[(long long)gi * ld + gj] : 0.f;
   }
   __syncthreads();
+  bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
   for (int r = ty; r < 64; r += 4) {
     const int gi = I * 64 + r, gj = J * 64 + tx;
-    if (gi < d && gj < d) R[(long long)gi * ld + gj] = sg * (t[r][tx] - Q[(long long)gi * ld + gj]);
+    if (gi < d && gj < d) {
+      const float v = sg * (t[r][tx] - Q[(long long)gi * ld + gj]);
+      R[(long long)gi * ld + gj] = v;
+      if (Rb) Rb[(long long)gi * ld + gj] = f32_to_bf16(v);
+    }
   }
 }
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
@@ -365,6 +373,41 @@ __global__ void __launch_bounds__(EW_THREADS) unpack_kernel(const EwArgs a, int 
 hipError_t unpack_launch(const EwArgs& a, hipStream_t st) {
   const int bp = ew_blocks(a.n * a.n);
   hipLaunchKernelGGL(unpack_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out2[b] (bf16, m x n row-major, leading dimension n) = bf16(in[b]) (i0 = 0) or bf16(in[b]^T) (i0 = 1, in is
+// n x m with leading dimension a.ld); 64 x 64 tiles through LDS. grid: tiles * nb.
+__global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
+  __shared__ float t[64][65];
+  const int TM = (int)((a.m + 63) / 64), TN = (int)((a.n + 63) / 64);
+  const int b = blockIdx.x / (TM * TN), tile = blockIdx.x % (TM * TN);
+  const int I = tile / TN, J = tile % TN;  // output tile (rows I, cols J)
+  const float* __restrict__ X = reinterpret_cast<const float*>(a.in[b]);
+  bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if (a.i0 == 0) {
+    for (int r = ty; r < 64; r += 4) {
+      const long long gi = (long long)I * 64 + r, gj = (long long)J * 64 + tx;
+      if (gi < a.m && gj < a.n) Y[gi * a.n + gj] = f32_to_bf16(X[gi * a.ld + gj]);
+    }
+    return;
+  }
+  // transposed: output (gi, gj) = in (gj, gi); load in rows J-block, cols I-block
+  for (int r = ty; r < 64; r += 4) {
+    const long long si = (long long)J * 64 + r, sj = (long long)I * 64 + tx;
+    t[r][tx] = (si < a.n && sj < a.m) ? X[si * a.ld + sj] : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const long long gi = (long long)I * 64 + r, gj = (long long)J * 64 + tx;
+    if (gi < a.m && gj < a.n) Y[gi * a.n + gj] = f32_to_bf16(t[tx][r]);
+  }
+}
+hipError_t to_bf16_launch(const EwArgs& a, hipStream_t st) {
+  const int TM = (int)((a.m + 63) / 64), TN = (int)((a.n + 63) / 64);
+  hipLaunchKernelGGL(to_bf16_kernel, dim3(TM * TN * a.nb), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -1,0 +1,33 @@
+// bf16 MFMA GEMM with k-contiguous bf16 operands: argument block shared by the host launcher and the kernel.
+#pragma once
+#include "gemm.h"
+
+namespace psgdk {
+
+// C = op over acc = A B^T where A is M x K and B is N x K, both row-major bf16 with k contiguous (X[mn][k]).
+// Outputs (each optional per launch): C (fp32, row-major, ldc), Cb (bf16, row-major, ldcb), CTb (bf16 of C^T,
+// row-major N x M, ldct). Epilogues as in gemm.h (EPI_STORE uses alpha only).
+struct GB16Args {
+  int M, N, K;
+  long long lda, ldb, ldc, ldcb, ldct, ldx;
+  float alpha;
+  int epi;
+  int tri, out_mode;  // tri: SYRK (B is A); out_mode 0 upper, 1 mirrored
+  int tiles_m, tiles_n, ntiles, nb;
+  int vec;            // reserved
+  const bf16_t* A[MAXB];
+  const bf16_t* B[MAXB];
+  float* C[MAXB];
+  bf16_t* Cb[MAXB];
+  bf16_t* CTb[MAXB];
+  const float* X1[MAXB];
+  const float* X2[MAXB];
+  const float* s[MAXB];
+  float* part[MAXB];
+};
+
+// cfg 0: 256 x 256 tiles, cfg 1: 128 x 128 tiles
+hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
+int gemm_bf16_tiles(long long M, long long N, int tri, int cfg);
+
+}  // namespace psgdk

@@ -1,0 +1,314 @@
+// bf16 MFMA GEMM for k-contiguous bf16 operands (the bf16 path of the Kron update and apply).
+//
+// Every operand arrives in HBM as bf16 rows with k contiguous (producers write transposed copies where a consumer
+// needs one), so the main loop is only 16-byte global loads, 16-byte LDS stores and 16-byte LDS fragment reads: no
+// conversion, no in-register transposes. Macro tile BM x BN x 64 with 4 waves (2 x 2), each wave owning a
+// (BM/2) x (BN/2) block of v_mfma_f32_16x16x32_bf16 tiles (8 x 8 for 256 x 256: 256 fp32 accumulators per lane).
+// LDS holds two stages of A and B, rows padded to 144 bytes (64 bf16 + 8): 16 lanes reading 16 consecutive rows
+// at the same k hit 16 distinct 16-byte bank groups. Global loads for tile k+1 are in flight while tile k is
+// multiplied; one barrier per k tile. The (problem, tile) list is dealt out so each XCD gets a contiguous run.
+// Operands: K a multiple of 8, leading dimensions multiples of 8, 16-byte aligned bases, under 2 GiB each (the host
+// routes anything else to the general engine); ragged M, N and K edges read zeros through the buffer extent.
+#include "gemm_bf16.h"
+
+namespace psgdk {
+
+namespace {
+
+constexpr int BK = 64, KP = 72, NT = 256;
+
+__device__ __forceinline__ int remap_xcd(int w, int G) {
+  const int cnt = G / 8, rem = G % 8, xcd = w % 8, slot = w / 8;
+  return xcd < rem ? xcd * (cnt + 1) + slot : rem * (cnt + 1) + (xcd - rem) * cnt + slot;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long long bytes) {
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// Global -> register -> LDS staging of one ROWS x 64 bf16 tile with buffer loads. Lane `tid` owns the 16-byte
+// k chunk tid % 8 of rows tid / 8 + 32 i (i < NV): the lane part of the byte offset is the VGPR offset, the row
+// group and the tile's k origin are the scalar offset. A lane whose row is past the operand or whose k chunk is
+// past K (K is a multiple of 8) gets an offset beyond the buffer extent: it reads zero (or, where the scalar part
+// wraps the 32-bit sum, some element of the same buffer), and either way only feeds outputs that are not stored.
+template <int ROWS>
+struct Ld {
+  static constexpr int NV = ROWS * (BK / 8) / NT;  // 16-byte vectors per thread
+  uint4 r[NV];
+
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int voff, long long ld, int mn0, int rows, int k0,
+                                       int K) {
+    const int lrow = threadIdx.x >> 3;
+    const bool kok = k0 + (threadIdx.x & 7) * 8 < K;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int base = mn0 + i * (NT / 8);
+      const bool ok = kok && base + lrow < rows;
+      const int soff = (int)(((long long)base * ld + k0) * 2);
+      r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff : 0x7fffffff, soff, 0));
+    }
+  }
+
+  __device__ __forceinline__ void store(bf16_t* lds) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int v = tid + NT * i, row = v >> 3, kv = v & 7;
+      *reinterpret_cast<uint4*>(lds + row * KP + kv * 8) = r[i];
+    }
+  }
+};
+
+}  // namespace
+
+template <int BM, int BN, int EPI>
+__global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
+  constexpr int FM = BM / 32, FN = BN / 32;  // 16x16 tiles per wave along m, n (2 x 2 waves)
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16_t* const As0 = reinterpret_cast<bf16_t*>(smem);
+  bf16_t* const Bs0 = As0 + 2 * BM * KP;
+
+  const int G = p.ntiles * p.nb;
+  const int logical = remap_xcd(blockIdx.x, G);
+  const int b = logical / p.ntiles, tile = logical % p.ntiles;
+  int ti, tj;
+  if (p.tri) {
+    ti = 0;
+    int rem = tile, rowlen = p.tiles_m;
+    while (rem >= rowlen) { rem -= rowlen; ++ti; --rowlen; }
+    tj = ti + rem;
+  } else {
+    ti = tile / p.tiles_n;
+    tj = tile % p.tiles_n;
+  }
+  const int m0 = ti * BM, n0 = tj * BN;
+  const bf16_t* __restrict__ Ap = p.A[b];
+  const bf16_t* __restrict__ Bp = p.tri ? p.A[b] : p.B[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 15, g = lane >> 4;
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (p.K + BK - 1) / BK;
+  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(Ap, (long long)p.M * p.lda * 2);
+  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bp, (long long)(p.tri ? p.M : p.N) * p.ldb * 2);
+  const int rowsB = p.tri ? p.M : p.N;
+  const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * 8) * 2);
+  const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * 8) * 2);
+  Ld<BM> la;
+  Ld<BN> lb;
+  la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K);
+  lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K);
+  la.store(As0);
+  lb.store(Bs0);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load(rsA, voffA, p.lda, m0, p.M, (kt + 1) * BK, p.K);
+      lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 1) * BK, p.K);
+    }
+    const bf16_t* As = As0 + cur * BM * KP;
+    const bf16_t* Bs = Bs0 + cur * BN * KP;
+#pragma unroll 1
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8_t bfr[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * FN * 16 + j * 16 + r) * KP + ks * 32 + g * 8);
+      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * FM * 16 + r) * KP + ks * 32 + g * 8);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        bf16x8_t a_nxt = a_cur;
+        if (i + 1 < FM)
+          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * FM * 16 + (i + 1) * 16 + r) * KP + ks * 32 + g * 8);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, bfr[j], acc[i][j], 0, 0, 0);
+        a_cur = a_nxt;
+      }
+    }
+    if (more) {
+      la.store(As0 + (cur ^ 1) * BM * KP);
+      lb.store(Bs0 + (cur ^ 1) * BN * KP);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue through LDS (idle after the main loop), in two halves of each wave's rows so that 4 waves x
+  // (BM/4 x BN/2) fp32 fit: (1) the wave parks half of its accumulators in its own LDS slot (static register
+  // indices only); (2) row pass: each lane takes 4 consecutive columns of a row, applies the epilogue, writes the
+  // value back to LDS and stores C / Cb rows (16- and 8-byte stores); (3) column pass: each lane takes 4
+  // consecutive rows of a column for the transposed bf16 copy, the SYRK mirror and the Procrustes trace.
+  constexpr int HR = BM / 4;       // rows per wave per half
+  constexpr int WC = BN / 2;       // columns per wave
+  constexpr int EP = WC + 4;       // LDS row pitch (floats)
+  float* const ep = reinterpret_cast<float*>(smem) + wave * HR * EP;
+  float* __restrict__ C = p.C[b];
+  bf16_t* __restrict__ Cb = p.Cb[b];
+  bf16_t* __restrict__ CTb = p.CTb[b];
+  const float* __restrict__ X1 = p.X1[b];
+  const float* __restrict__ X2 = p.X2[b];
+  float s0 = 0.f, s1 = 0.f;
+  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_SCALE || EPI == EPI_RQ) s0 = p.s[b][0];
+  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) s1 = p.s[b][1];
+  const bool mirror = p.tri && p.out_mode == 1;
+  const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ;
+  float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // (1) park accumulators: tile (i, j) of this half at local row (i - h FM/2) * 16 + 4g + e, column 16 j + r
+#pragma unroll
+    for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ep[(ii * 16 + g * 4 + e) * EP + j * 16 + r] = acc[h * (FM / 2) + ii][j][e];
+    __syncthreads();
+    const int grow0 = m0 + wm * (BM / 2) + h * HR;  // global row of local row 0
+    const int gcol0 = n0 + wn * WC;
+    // (2) row pass
+    for (int idx = lane; idx < HR * (WC / 4); idx += 64) {
+      const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
+      const int row = grow0 + lr, col = gcol0 + lc;
+      float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
+      float v[4] = {a.x, a.y, a.z, a.w};
+      bool ok[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ok[e] = row < p.M && col + e < p.N && !(p.tri && row > col + e);
+      const long long xo = (long long)row * p.ldx + col;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (EPI == EPI_FACTOR) {
+          const float q = ok[e] ? X1[xo + e] : 0.f;
+          v[e] = q - s0 * (v[e] - s1 * q);
+        } else if constexpr (EPI == EPI_PROC) {
+          v[e] = ok[e] ? X1[xo + e] + s0 * X2[xo + e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
+        } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
+          v[e] = s0 * v[e];
+          if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
+        } else {
+          v[e] = p.alpha * v[e];
+          if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
+        }
+      }
+      *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
+      const bool all = ok[0] && ok[1] && ok[2] && ok[3];
+      if (C) {
+        float* dst = C + (long long)row * p.ldc + col;
+        if (all && (p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        else
+#pragma unroll
+          for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = v[e];
+      }
+      if (Cb) {
+        bf16_t* dst = Cb + (long long)row * p.ldcb + col;
+        if (all && (p.ldcb & 3) == 0)
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                       pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+        else
+#pragma unroll
+          for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
+      }
+    }
+    __syncthreads();
+    // (3) column pass
+    if (colpass) {
+      for (int idx = lane; idx < WC * (HR / 4); idx += 64) {
+        const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
+        const int col = gcol0 + lc, row = grow0 + lr;
+        float v[4];
+        bool ok[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = ep[(lr + e) * EP + lc];
+          ok[e] = row + e < p.M && col < p.N && !(p.tri && row + e > col);
+        }
+        const bool all = ok[0] && ok[1] && ok[2] && ok[3];
+        if constexpr (EPI == EPI_RQ) {
+          const float* x = X1 + (long long)col * p.ldx + row;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (ok[e]) t2 += s0 * x[e] * v[e];
+        }
+        if (CTb) {
+          bf16_t* dst = CTb + (long long)col * p.ldct + row;
+          if (all && (p.ldct & 3) == 0)
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                         pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+          else
+#pragma unroll
+            for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
+        }
+        if (mirror) {  // element (row, col) with row < col also at (col, row)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (!ok[e] || row + e == col) continue;
+            if (C) C[(long long)col * p.ldc + row + e] = v[e];
+            if (Cb) Cb[(long long)col * p.ldcb + row + e] = f32_to_bf16(v[e]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if constexpr (EPI == EPI_RQ || EPI == EPI_SUMSQ) {
+    __shared__ float red[16];
+    t1 = block_sum(t1, red);
+    if constexpr (EPI == EPI_RQ) t2 = block_sum(t2, red);
+    if (tid == 0) {
+      p.part[b][2 * tile] = t1;
+      p.part[b][2 * tile + 1] = t2;
+    }
+  }
+}
+
+int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
+  const int T = cfg ? 128 : 256;
+  const long long tm = (M + T - 1) / T, tn = (N + T - 1) / T;
+  return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
+}
+
+template <int BM, int BN, int EPI>
+static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
+  constexpr int smem_main = 2 * (BM + BN) * KP * 2, smem_epi = 4 * (BM / 4) * (BN / 2 + 4) * 4;
+  constexpr int smem = smem_main > smem_epi ? smem_main : smem_epi;
+  auto fn = gemm_bf16_kernel<BM, BN, EPI>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = (a.N + BN - 1) / BN;
+  a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;
+  hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(NT), smem, st, a);
+  return hipGetLastError();
+}
+
+template <int BM, int BN>
+static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
+  switch (a.epi) {
+    case EPI_FACTOR: return launch_b16<BM, BN, EPI_FACTOR>(a, st);
+    case EPI_PROC: return launch_b16<BM, BN, EPI_PROC>(a, st);
+    case EPI_SCALE: return launch_b16<BM, BN, EPI_SCALE>(a, st);
+    case EPI_RQ: return launch_b16<BM, BN, EPI_RQ>(a, st);
+    case EPI_SUMSQ: return launch_b16<BM, BN, EPI_SUMSQ>(a, st);
+    default: return launch_b16<BM, BN, EPI_STORE>(a, st);
+  }
+}
+
+hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st) {
+  if (cfg == 1) return launch_epi<128, 128>(a, st);
+  return launch_epi<256, 256>(a, st);
+}
+
+}  // namespace psgdk

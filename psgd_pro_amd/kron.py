@@ -35,7 +35,7 @@ class _Param:
 
 
 class _Group:
-    __slots__ = ("key", "members", "m", "n", "kind", "struct", "Qs", "Ps", "Ls", "g_dtype", "p_dtype")
+    __slots__ = ("key", "members", "m", "n", "kind", "struct", "Qs", "Ps", "Ls", "Qt16", "P16", "g_dtype", "p_dtype")
 
 
 class KronWhiten:
@@ -160,6 +160,7 @@ class KronWhiten:
                 nb = len(grp.members)
                 order = sum(k != L.FACTOR_NONE for k in grp.kind)
                 grp.Qs, grp.Ps, grp.Ls = [None, None], [None, None], [None, None]
+                grp.Qt16, grp.P16 = [None, None], [None, None]
                 for f, (k, d) in enumerate(zip(grp.kind, (grp.m, grp.n))):
                     if k == L.FACTOR_NONE:
                         continue
@@ -167,6 +168,11 @@ class KronWhiten:
                     if k == L.FACTOR_DENSE:
                         Q = torch.eye(d, device=dev, dtype=torch.float32).mul_(s).expand(nb, d, d).contiguous()
                         P = torch.empty(nb, d, d, device=dev, dtype=torch.float32)
+                        if (self._prec == L.PREC_BF16 and not self._tri and grp.kind == (L.FACTOR_DENSE, L.FACTOR_DENSE)
+                                and grp.m % 8 == 0 and grp.n % 8 == 0):
+                            # bf16 shadows (Q^T and P) read by the bf16 contractions; the library keeps them current
+                            grp.Qt16[f] = torch.empty(nb, d, d, device=dev, dtype=torch.bfloat16)
+                            grp.P16[f] = torch.empty(nb, d, d, device=dev, dtype=torch.bfloat16)
                     else:
                         Q = torch.full((nb, d), s, device=dev, dtype=torch.float32)
                         P = torch.empty(nb, d, device=dev, dtype=torch.float32)
@@ -190,6 +196,9 @@ class KronWhiten:
                 s.Q[f][j] = grp.Qs[f][j].data_ptr()
                 s.P[f][j] = grp.Ps[f][j].data_ptr()
                 s.L[f][j] = grp.Ls[f][j].data_ptr()
+                if grp.Qt16[f] is not None:
+                    s.Qt16[f][j] = grp.Qt16[f][j].data_ptr()
+                    s.P16[f][j] = grp.P16[f][j].data_ptr()
         return s
 
     def _refresh_p(self, grp):

@@ -210,3 +210,38 @@ def test_hip_ops_plugin_methods(hip):
     pk = K.make_ops({"packed"})
     P = pk.sym(X, False)
     assert P.dim() == 1 and rel_err_norm(pk.symm(P, Y), S.double().cpu() @ Y.double().cpu()) < 1e-6
+
+
+# -------------------------------------------------------------------------------------------------------------- bf16
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 768, 320), (768, 768, 2304), (100, 70, 33), (1, 50, 77),
+                                   (264, 520, 72), (3072, 768, 768), (4096, 4096, 256)])
+def test_gemm_bf16_k_contiguous(hip, m, n, k):
+    """A (m x k) B^T (B given n x k), both bf16 k-contiguous: the dedicated bf16 kernel (256 or 128 tiles)."""
+    A = rnd(m, k, seed=m).to(torch.bfloat16)
+    B = rnd(n, k, seed=n + 1).to(torch.bfloat16)
+    C = K.gemm(A.to(DEV), B.to(DEV), False, True, True)
+    check_gemm_bound(C, A.double(), B.double().T)
+
+
+@pytest.mark.parametrize("nb,m,n,k", [(12, 768, 768, 768), (12, 1024, 1024, 512)])
+def test_gemm_bf16_grouped(hip, nb, m, n, k):
+    As = [rnd(m, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
+    Bs = [rnd(n, k, seed=50 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
+    Cs = [torch.empty(m, n, device=DEV) for _ in range(nb)]
+    L.check(hip.psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(As), k, L.ptrs(Bs), k, 0.0, L.ptrs(Cs), n,
+                           L.stream_of(As[0])))
+    for A, B, C in zip(As, Bs, Cs):
+        check_gemm_bound(C, A.double().cpu(), B.double().cpu().T)
+
+
+@pytest.mark.parametrize("nb,n,k", [(1, 768, 2304), (1, 3072, 768), (16, 1024, 256), (1, 200, 72)])
+def test_syrk_bf16_k_contiguous(hip, nb, n, k):
+    As = [rnd(n, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
+    Cs = [torch.full((n, n), float("nan"), device=DEV) for _ in range(nb)]
+    L.check(hip.psgdk_syrk(1, 0, L.OUT_UPPER, n, k, 1, nb, L.ptrs(As), k, L.ptrs(Cs), n, L.stream_of(As[0])))
+    triu = torch.ones(n, n, dtype=torch.bool).triu()
+    for A, C in zip(As, Cs):
+        X = A.double().cpu()
+        Cc = C.cpu()
+        assert bool(torch.isnan(Cc[~triu]).all())
+        check_gemm_bound(torch.where(triu, Cc, Cc.T), X, X.T)

@@ -200,3 +200,12 @@ def test_step_closure_and_loss_curve(hip):
     d_32 = max(abs(a - b) / abs(b) for a, b in zip(l32, l64))
     print(f"loss curve: gpu vs fp64 {d_gpu:.2e}, oracle-fp32 vs fp64 {d_32:.2e}", flush=True)
     assert d_gpu <= max(1e-4, 3 * d_32), (d_gpu, d_32)
+
+
+def test_bf16_parity_general_path(hip):
+    """bf16 groups outside the bf16 kernel's reach (rows not a multiple of 8, a diagonal factor) use the general
+    engine at bf16 input precision."""
+    eps16 = torch.finfo(torch.bfloat16).eps
+    worst, _ = run_pair([(100, 70), (96, 64)], steps=6, skew=1.0, prec="bf16", gdt=torch.bfloat16,
+                        grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
+    assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
