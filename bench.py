@@ -78,6 +78,19 @@ def aggregate(recs):
     return agg, syrk
 
 
+def launch_classes(recs, steps, top=12):
+    """The most expensive (kernel, problems, flops per launch) classes of MFMA launches, per step."""
+    agg = {}
+    for kid, tri, nb, ms, fl in recs:
+        a = agg.setdefault((kid, tri, nb, round(fl)), [0, 0.0])
+        a[0] += 1
+        a[1] += ms
+    rows = sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]
+    return [{"kernel": k[0], "syrk": bool(k[1]), "nb": k[2], "gflop": round(k[3] / 1e9, 2),
+             "launches_per_step": v[0] / steps, "us": round(v[1] * 1e3 / v[0], 1),
+             "tflops": round(k[3] / (v[1] / v[0] * 1e-3) / 1e12, 1)} for k, v in rows]
+
+
 def cpu_baseline(precision, skew, seconds):
     """The CPU oracle (float32) on one ViT-B block (4 weights), 1 warmup step, then timed steps until `seconds` of
     work; scaled x12 to the 48-weight set."""
@@ -179,6 +192,7 @@ def bench_vitb(args):
                      "flops_per_launch": fl_tot / n_l,
                      "achieved": round(achieved, 2), "peak": PEAK[prec_of], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK[prec_of], 4), "traffic": traffic},
+        "launch_classes": launch_classes(recs, args.steps),
         "kernels": {L.kernel_name(k): {"launches_per_step": v[0] / args.steps, "ms_per_step": round(v[1] / args.steps, 3),
                                        "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2)} for k, v in agg.items()},
     }

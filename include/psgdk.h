@@ -95,6 +95,14 @@ int psgdk_tri_vmm(int64_t n, int sign, int nb, const float* const* V, const floa
 int psgdk_norm_lower_bound(int64_t n, int sign, int nb, const float* const* A, int64_t lda, const float* const* V,
                            float* const* out, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
 
+/* Norm lower bound of the fully stored SPD (sign +1) or skew-symmetric (sign -1) n x n matrix A (row-major, lda;
+ * a_dtype PSGDK_F32 or PSGDK_BF16; both triangles read), random start V (32 x n fp32); out[b] (device, one float)
+ * receives the bound. With bf16 storage the products V A run in bf16 with fp32 accumulation.
+ * Replaces norm_lower_bound_spd / _skh (psgd_pro.py:19-41, :43-65) on full matrices. */
+int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_dtype,
+                                const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
+                                psgdk_stream_t stream);
+
 /* Full symmetric n x n matrix from its row-major packed upper triangle.
  * Replaces psgd::unpack (kernels/ops.py:112-116, kernels/k2.py:88-103). */
 int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int64_t ldc, psgdk_stream_t stream);
@@ -185,6 +193,12 @@ typedef struct psgdk_prof_record {
 } psgdk_prof_record_t;
 int psgdk_profile_start(void);
 int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);
+
+/* Tuning switches (process-wide): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
+ * XCD); option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256, 1 = 128 x 128); option 2 = workgroups
+ * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of that
+ * kernel (2, 4 or 8; default 4). */
+int psgdk_set_option(int option, int value);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
  * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B. Checks the compiler builtins' lane layout. */

@@ -60,12 +60,14 @@ _SIGS = {
     "psgdk_tri_rownorm2": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_tri_vmm": (_i32, [_i64, _i32, _i32, _vpa, _vpa, _i64, _vpa, _vp, _szp, _vp]),
     "psgdk_norm_lower_bound": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_norm_lower_bound_full": (_i32, [_i64, _i32, _i32, _vpa, _i64, _i32, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_unpack": (_i32, [_i64, _i32, _vpa, _vpa, _i64, _vp]),
     "psgdk_kron2d_update": (_i32, [C.POINTER(Kron2d), C.POINTER(UpdateOpts), _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_kron2d_apply": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_kron2d_refresh_p": (_i32, [C.POINTER(Kron2d), _i32, _i32, _vp]),
     "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
     "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),
+    "psgdk_set_option": (_i32, [_i32, _i32]),
     "psgdk_profile_start": (_i32, []),
     "psgdk_profile_stop": (_i32, [C.POINTER(ProfRecord), _i32, C.POINTER(C.c_int)]),
     "psgdk_debug_mfma": (_i32, [_i32, _vp, _vp, _vp, _vp]),

@@ -198,7 +198,15 @@ struct B16Out {
   int64_t ldc = 0, ldcb = 0, ldct = 0;
 };
 
-int b16_cfg(int64_t M, int64_t N, int tri, int nb) { return gemm_bf16_tiles(M, N, tri, 0) * nb >= 160 ? 0 : 1; }
+int g_tile_order = 0;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous runs
+int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's tile config
+int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
+int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
+
+int b16_cfg(int64_t M, int64_t N, int tri, int nb) {
+  if (g_force_cfg >= 0) return g_force_cfg;
+  return gemm_bf16_tiles(M, N, tri, 0) * nb >= 160 ? 0 : 1;
+}
 
 // Operand contract of gemm_bf16: K and both leading dimensions multiples of 8, 16-byte aligned bases, each operand
 // under 2 GiB (buffer extent).
@@ -220,6 +228,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
   a.lda = lda; a.ldb = ldb; a.ldc = o.ldc; a.ldcb = o.ldcb; a.ldct = o.ldct; a.ldx = e.ldx;
   a.alpha = e.alpha; a.epi = e.epi; a.tri = tri; a.out_mode = out_mode; a.nb = nb;
+  a.vec = g_tile_order;
   for (int b = 0; b < nb; ++b) {
     a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
     a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
@@ -252,6 +261,7 @@ struct NlbWs {
   float *rpart[MAXB], *cpart[MAXB], *tmax[MAXB], *dmax[MAXB], *rn2[MAXB], *scal[MAXB];
   int splits;
   int64_t kchunk;
+  int64_t part_cols;  // capacity of part[b] in columns of 32 rows
 };
 
 void nlb_plan(int64_t n, int nb, int& splits, int64_t& kchunk) {
@@ -263,13 +273,26 @@ void nlb_plan(int64_t n, int nb, int& splits, int64_t& kchunk) {
   splits = (int)((n + kchunk - 1) / kchunk);
 }
 
+// Split of the full-storage V A products: about g_nlb_target workgroups of 32 x 128 outputs, k slices of at least
+// 128, at most 8 slices (the reduce kernel's unrolled width), within the partial capacity (columns of 32 rows per
+// matrix).
+void nlb_full_plan(int64_t n, int nb, int64_t part_cols, int& ksplit, int& kslice) {
+  const int64_t ncb = (n + 127) / 128;
+  int64_t s = (g_nlb_target + ncb * nb - 1) / (ncb * nb);
+  s = std::min(s, std::max<int64_t>(1, (n + 127) / 128));
+  s = std::max<int64_t>(1, std::min({s, part_cols / n, (int64_t)8}));
+  kslice = (int)(((n + s - 1) / s + 63) / 64 * 64);
+  ksplit = (int)((n + kslice - 1) / kslice);
+}
+
 void nlb_take(Ws& w, int64_t n, int nb, NlbWs& o) {
   nlb_plan(n, nb, o.splits, o.kchunk);
   const int64_t T = (n + 63) / 64, nbk = T, ntri = T * (T + 1) / 2;
+  o.part_cols = std::max<int64_t>(o.splits, 8) * n;
   for (int b = 0; b < nb; ++b) {
     o.vb0[b] = w.take<float>(NLB_K * n);
     o.vb1[b] = w.take<float>(NLB_K * n);
-    o.part[b] = w.take<float>((size_t)o.splits * NLB_K * n);
+    o.part[b] = w.take<float>((size_t)o.part_cols * NLB_K);
     o.ss0[b] = w.take<float>(NLB_K * nbk);
     o.ss1[b] = w.take<float>(NLB_K * nbk);
     o.rpart[b] = w.take<float>((size_t)T * T * 64);
@@ -285,6 +308,7 @@ NlbArgs nlb_args(int64_t n, int sign, int nb, const float* const* A, int64_t lda
   NlbArgs a;
   std::memset(&a, 0, sizeof a);
   a.nb = nb; a.n = (int)n; a.T = (int)((n + 63) / 64); a.sign = sign; a.splits = w.splits; a.lda = lda;
+  a.ssc = 64;
   for (int b = 0; b < nb; ++b) {
     a.A[b] = A[b];
     a.rpart[b] = w.rpart[b]; a.cpart[b] = w.cpart[b]; a.tmax[b] = w.tmax[b]; a.dmax[b] = w.dmax[b];
@@ -326,6 +350,38 @@ int run_nlb(int64_t n, int sign, int nb, const float* const* A, int64_t lda, boo
       a.ssout[b] = ss[normalize][b];
     }
     PSGDK_HIP(nlb_reduce_launch(a, normalize, st), "nlb_reduce");
+    cur ^= 1;
+  }
+  for (int b = 0; b < nb; ++b) a.ssin[b] = ss[1][b];
+  PSGDK_HIP(nlb_final_launch(a, fin, st), "nlb_final");
+  return PSGDK_OK;
+}
+
+// Norm lower bound of fully stored matrices (fp32 or bf16): row norms, init, 4 V A products with folded scaling,
+// final. 7 launches.
+int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_bf16, const float* const* V,
+                 const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
+  const float* Af[MAXB];
+  for (int b = 0; b < nb; ++b) Af[b] = reinterpret_cast<const float*>(A[b]);
+  NlbArgs a = nlb_args(n, sign, nb, Af, lda, w);
+  a.ssc = 128;
+  nlb_full_plan(n, nb, w.part_cols, a.ksplit, a.kslice);
+  a.vmm_u = g_vmm_u;
+  PSGDK_HIP(nlb_full_launch(a, 0, a_bf16, 0, st), "row norms");
+  for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
+  PSGDK_HIP(nlb_full_launch(a, 1, a_bf16, 0, st), "nlb init");
+  float* const* vb[2] = {w.vb0, w.vb1};
+  float* const* ss[2] = {w.ss0, w.ss1};
+  int cur = 0;
+  for (int it = 0; it < 4; ++it) {
+    const int normalize = it & 1;
+    for (int b = 0; b < nb; ++b) {
+      a.Vin[b] = vb[cur][b];
+      a.Vout[b] = vb[cur ^ 1][b];
+      a.ssin[b] = ss[0][b];
+      a.ssout[b] = ss[normalize][b];
+    }
+    PSGDK_HIP(nlb_full_launch(a, 2, a_bf16, normalize, st), "V A");
     cur ^= 1;
   }
   for (int b = 0; b < nb; ++b) a.ssin[b] = ss[1][b];
@@ -523,7 +579,7 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
   const int64_t dims[2] = {m, n};
   Ws w(ws);
   bf16_t *Xb[MAXB], *YTb[MAXB], *Pgb[MAXB], *PgTb[MAXB], *T1b[MAXB], *QnTb[MAXB], *Rb[MAXB], *RQTb[MAXB];
-  float *T1[MAXB], *Qn[MAXB], *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
+  float *Qn[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
   const int tp = gemm_bf16_tiles(dmx, dmx, 0, 1);
   for (int b = 0; b < nb; ++b) {
     Xb[b] = w.take<bf16_t>(mn);
@@ -534,9 +590,7 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
     QnTb[b] = w.take<bf16_t>(dmx * dmx);
     Rb[b] = w.take<bf16_t>(dmx * dmx);
     RQTb[b] = w.take<bf16_t>(dmx * dmx);
-    T1[b] = w.take<float>(dmx * dmx);
     Qn[b] = w.take<float>(dmx * dmx);
-    R[b] = w.take<float>(dmx * dmx);
     RQ[b] = w.take<float>(dmx * dmx);
     coef[b] = w.take<float>(4);
     rs[b] = w.take<float>(4);
@@ -575,10 +629,10 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
   for (int f = 0; f < 2; ++f) {
     const int64_t d = dims[f], other = dims[1 - f];
     const float term2 = (float)mn / (float)d;
-    {  // term1 = Pg Pg^T (f = 0) or Pg^T Pg (f = 1), full symmetric fp32 + bf16
+    {  // term1 = Pg Pg^T (f = 0) or Pg^T Pg (f = 1), full symmetric bf16 (its only consumers read bf16)
       B16Out out;
-      out.ldc = d; out.ldcb = d;
-      for (int b = 0; b < nb; ++b) { A[b] = f == 0 ? (const void*)Pgb[b] : (const void*)PgTb[b]; out.C[b] = T1[b]; out.Cb[b] = T1b[b]; }
+      out.ldcb = d;
+      for (int b = 0; b < nb; ++b) { A[b] = f == 0 ? (const void*)Pgb[b] : (const void*)PgTb[b]; out.Cb[b] = T1b[b]; }
       EpiSpec e;
       PSGDK_TRY(run_b16(nb, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
     }
@@ -589,9 +643,9 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       NlbFinal fin;
       std::memset(&fin, 0, sizeof fin);
       fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL; fin.term2 = term2;
-      const float* T1c[MAXB];
-      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; T1c[b] = T1[b]; }
-      PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, true, Vs, fin, nw, st));
+      const void* T1c[MAXB];
+      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; T1c[b] = T1b[b]; }
+      PSGDK_TRY(run_nlb_full(d, 1, nb, T1c, d, 1, Vs, fin, nw, st));
     }
     {  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16
       B16Out out;
@@ -604,30 +658,30 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
-    {  // R = Qn^T - Qn -> fp32 + bf16
+    {  // R = Qn^T - Qn -> bf16
       EwArgs a;
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out[b] = R[b]; a.out2[b] = Rb[b]; }
+      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out2[b] = Rb[b]; }
       PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
     }
     {
       NlbFinal fin;
       std::memset(&fin, 0, sizeof fin);
       fin.mode = NLB_FINAL_SCALE;
-      const float* Rc[MAXB];
-      for (int b = 0; b < nb; ++b) { fin.coef[b] = rs[b]; Rc[b] = R[b]; }
-      PSGDK_TRY(run_nlb(d, -1, nb, Rc, d, true, Vk, fin, nw, st));
+      const void* Rc[MAXB];
+      for (int b = 0; b < nb; ++b) { fin.coef[b] = rs[b]; Rc[b] = Rb[b]; }
+      PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st));
     }
     int nt = 0;
-    {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials
+    {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials (tr(R RQ) reads the bf16 R of the product)
       B16Out out;
       out.ldc = d; out.ldct = d;
       EpiSpec e;
       e.epi = EPI_RQ; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
         A[b] = Rb[b]; B[b] = QnTb[b]; out.C[b] = RQ[b]; out.CTb[b] = RQTb[b];
-        e.X1[b] = R[b]; e.s[b] = rs[b]; e.part[b] = tpart[b];
+        e.X1[b] = reinterpret_cast<const float*>(Rb[b]); e.s[b] = rs[b]; e.part[b] = tpart[b];
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, &nt, st));
     }
@@ -907,6 +961,33 @@ int psgdk_norm_lower_bound(int64_t n, int sign, int nb, const float* const* A, i
   return PSGDK_OK;
 }
 
+int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_dtype,
+                                const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
+                                psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_dt(a_dtype, "A"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  Ws w(ws);
+  NlbWs nw;
+  nlb_take(w, n, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(A, nb, "A"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  PSGDK_TRY(check_ptrs(out, nb, "out"));
+  if (sign != 1 && sign != -1) return fail(PSGDK_EINVAL, "sign = %d", sign);
+  if (lda < n) return fail(PSGDK_ESHAPE, "lda < n");
+  hipStream_t st = (hipStream_t)stream;
+  NlbFinal fin;
+  std::memset(&fin, 0, sizeof fin);
+  fin.mode = NLB_FINAL_NONE;
+  PSGDK_TRY(run_nlb_full(n, sign, nb, A, lda, a_dtype == PSGDK_BF16, V, fin, nw, st));
+  for (int b = 0; b < nb; ++b)
+    PSGDK_HIP(hipMemcpyAsync(out[b], nw.scal[b] + NLB_BOUND, sizeof(float), hipMemcpyDeviceToDevice, st), "copy bound");
+  return PSGDK_OK;
+}
+
 int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int64_t ldc, psgdk_stream_t stream) {
   PSGDK_TRY(check_nb(nb));
   PSGDK_TRY(check_dims(n, "n"));
@@ -1014,7 +1095,8 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
       for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; }
       const float* T1c[MAXB];
       for (int b = 0; b < nb; ++b) T1c[b] = T1[b];
-      PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, !term_tri, Vs, fin, nw, st));
+      if (term_tri) PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, false, Vs, fin, nw, st));
+      else PSGDK_TRY(run_nlb_full(d, 1, nb, reinterpret_cast<const void* const*>(T1c), d, 0, Vs, fin, nw, st));
     }
     // Qn = Q - lr/L (term1 Q - term2 Q)   (psgd_pro.py:135)
     {
@@ -1041,9 +1123,9 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
       std::memset(&fin, 0, sizeof fin);
       fin.mode = NLB_FINAL_SCALE;
       for (int b = 0; b < nb; ++b) fin.coef[b] = rs[b];
-      const float* Rc[MAXB];
+      const void* Rc[MAXB];
       for (int b = 0; b < nb; ++b) Rc[b] = R[b];
-      PSGDK_TRY(run_nlb(d, -1, nb, Rc, d, true, Vk, fin, nw, st));
+      PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 0, Vk, fin, nw, st));
     }
     {
       Opnd a, bq;
@@ -1195,6 +1277,22 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
   a.nb = nb; a.m = 1; a.n = numel; a.dt = g_dtype; a.f0 = beta;
   for (int b = 0; b < nb; ++b) { a.in[b] = g[b]; a.out[b] = mom[b]; }
   return hip_check(momentum_launch(a, (hipStream_t)stream), "momentum");
+}
+
+int psgdk_set_option(int option, int value) {
+  if (option == 0) { g_tile_order = value; return PSGDK_OK; }
+  if (option == 1) { g_force_cfg = value; return PSGDK_OK; }
+  if (option == 2) {
+    if (value < 1) return fail(PSGDK_EINVAL, "option 2 (V A workgroup target) must be >= 1");
+    g_nlb_target = value;
+    return PSGDK_OK;
+  }
+  if (option == 3) {
+    if (value != 2 && value != 4 && value != 8) return fail(PSGDK_EINVAL, "option 3 (V A load batch) must be 2, 4 or 8");
+    g_vmm_u = value;
+    return PSGDK_OK;
+  }
+  return fail(PSGDK_EINVAL, "unknown option %d", option);
 }
 
 int psgdk_profile_start(void) {

@@ -34,6 +34,9 @@ __device__ __forceinline__ uint32_t pack2(bf16_t lo, bf16_t hi) { return (uint32
 template <typename T> __device__ __forceinline__ float to_f32(T v);
 template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ float to_f32<bf16_t>(bf16_t v) { return bf16_to_f32(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return f32_to_bf16(v); }
 
 // wave64 reductions
 __device__ __forceinline__ float wave_sum(float v) {
@@ -46,6 +49,14 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes (clamped to 2^31 - 1) return zero,
+// so a lane with nothing to load passes offset 0x7fffffff instead of branching.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long long bytes) {
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+constexpr int kOob = 0x7fffffff;
 
 // Block-wide reductions for blockDim.x a multiple of 64 (<= 1024). `red` holds >= 16 floats of LDS.
 __device__ __forceinline__ float block_sum(float v, float* red) {

@@ -50,36 +50,51 @@ hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// R[i][j] = sign * (Q[j][i] - Q[i][j]); 64 x 64 tiles through LDS. grid: T*T*nb.
+// R[i][j] = sign * (Q[j][i] - Q[i][j]) and R[j][i] = -R[i][j] from one read of each 64 x 64 tile pair (I <= J):
+// both tiles are staged in LDS, each output tile is written row-major from there. Outputs: R fp32 (out, optional)
+// and R bf16 (out2, optional). grid: nb * T (T + 1) / 2, T = ceil(d / 64).
 __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
-  __shared__ float t[64][65];
-  const int d = (int)a.m, T = (d + 63) / 64;
-  const int b = blockIdx.x / (T * T), tile = blockIdx.x % (T * T);
-  const int I = tile / T, J = tile % T;
+  __shared__ float qa[64][65];  // Q[I block][J block]
+  __shared__ float qb[64][65];  // Q[J block][I block]
+  const int d = (int)a.m, T = (d + 63) / 64, np = T * (T + 1) / 2;
+  const int b = blockIdx.x / np;
+  int t = blockIdx.x % np, I = 0;
+  while (t >= T - I) { t -= T - I; ++I; }
+  const int J = I + t;
   const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
   float* __restrict__ R = a.out[b];
+  bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
   const long long ld = a.ld;
   const float sg = (float)a.i0;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  // load Q[J-block rows][I-block cols] transposed into t
   for (int r = ty; r < 64; r += 4) {
-    const int gi = J * 64 + r, gj = I * 64 + tx;
-    t[tx][r] = (gi < d && gj < d) ? Q[(long long)gi * ld + gj] : 0.f;
+    const int i = I * 64 + r, j = J * 64 + tx, i2 = J * 64 + r, j2 = I * 64 + tx;
+    qa[r][tx] = (i < d && j < d) ? Q[(long long)i * ld + j] : 0.f;
+    qb[r][tx] = (i2 < d && j2 < d) ? Q[(long long)i2 * ld + j2] : 0.f;
   }
   __syncthreads();
-  bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
   for (int r = ty; r < 64; r += 4) {
-    const int gi = I * 64 + r, gj = J * 64 + tx;
-    if (gi < d && gj < d) {
-      const float v = sg * (t[r][tx] - Q[(long long)gi * ld + gj]);
-      R[(long long)gi * ld + gj] = v;
-      if (Rb) Rb[(long long)gi * ld + gj] = f32_to_bf16(v);
+    {  // R[I*64 + r][J*64 + tx] = sg (Q[J*64 + tx][I*64 + r] - Q[I*64 + r][J*64 + tx])
+      const int i = I * 64 + r, j = J * 64 + tx;
+      if (i < d && j < d) {
+        const float v = sg * (qb[tx][r] - qa[r][tx]);
+        if (R) R[(long long)i * ld + j] = v;
+        if (Rb) Rb[(long long)i * ld + j] = f32_to_bf16(v);
+      }
+    }
+    if (I != J) {  // R[J*64 + r][I*64 + tx] = sg (Q[I*64 + tx][J*64 + r] - Q[J*64 + r][I*64 + tx])
+      const int i = J * 64 + r, j = I * 64 + tx;
+      if (i < d && j < d) {
+        const float v = sg * (qa[tx][r] - qb[r][tx]);
+        if (R) R[(long long)i * ld + j] = v;
+        if (Rb) Rb[(long long)i * ld + j] = f32_to_bf16(v);
+      }
     }
   }
 }
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
-  const int T = (int)((a.m + 63) / 64);
-  hipLaunchKernelGGL(rform_kernel, dim3(T * T * a.nb), dim3(256), 0, st, a);
+  const long long T = (a.m + 63) / 64;
+  hipLaunchKernelGGL(rform_kernel, dim3((unsigned)(T * (T + 1) / 2 * a.nb)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -6,7 +6,8 @@ namespace psgdk {
 
 // C = op over acc = A B^T where A is M x K and B is N x K, both row-major bf16 with k contiguous (X[mn][k]).
 // Outputs (each optional per launch): C (fp32, row-major, ldc), Cb (bf16, row-major, ldcb), CTb (bf16 of C^T,
-// row-major N x M, ldct). Epilogues as in gemm.h (EPI_STORE uses alpha only).
+// row-major N x M, ldct). Epilogues as in gemm.h (EPI_STORE uses alpha only), except that EPI_RQ reads X1 (R) as
+// bf16.
 struct GB16Args {
   int M, N, K;
   long long lda, ldb, ldc, ldcb, ldct, ldx;
@@ -14,7 +15,7 @@ struct GB16Args {
   int epi;
   int tri, out_mode;  // tri: SYRK (B is A); out_mode 0 upper, 1 mirrored
   int tiles_m, tiles_n, ntiles, nb;
-  int vec;            // reserved
+  int vec;            // 1: deal tiles to XCDs in contiguous runs; 0: problem-major order (WG id = tile)
   const bf16_t* A[MAXB];
   const bf16_t* B[MAXB];
   float* C[MAXB];

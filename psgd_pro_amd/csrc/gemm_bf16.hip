@@ -22,10 +22,6 @@ __device__ __forceinline__ int remap_xcd(int w, int G) {
   return xcd < rem ? xcd * (cnt + 1) + slot : rem * (cnt + 1) + (xcd - rem) * cnt + slot;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long long bytes) {
-  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
 
 // Global -> register -> LDS staging of one ROWS x 64 bf16 tile with buffer loads. Lane `tid` owns the 16-byte
 // k chunk tid % 8 of rows tid / 8 + 32 i (i < NV): the lane part of the byte offset is the VGPR offset, the row
@@ -70,7 +66,7 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
   bf16_t* const Bs0 = As0 + 2 * BM * KP;
 
   const int G = p.ntiles * p.nb;
-  const int logical = remap_xcd(blockIdx.x, G);
+  const int logical = p.vec ? remap_xcd(blockIdx.x, G) : (int)blockIdx.x;
   const int b = logical / p.ntiles, tile = logical % p.ntiles;
   int ti, tj;
   if (p.tri) {
@@ -232,11 +228,11 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
           ok[e] = row + e < p.M && col < p.N && !(p.tri && row + e > col);
         }
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
-        if constexpr (EPI == EPI_RQ) {
-          const float* x = X1 + (long long)col * p.ldx + row;
+        if constexpr (EPI == EPI_RQ) {  // X1: R in bf16, read at (col, row..row+3)
+          const bf16_t* x = reinterpret_cast<const bf16_t*>(X1) + (long long)col * p.ldx + row;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (ok[e]) t2 += s0 * x[e] * v[e];
+            if (ok[e]) t2 += s0 * bf16_to_f32(x[e]) * v[e];
         }
         if (CTb) {
           bf16_t* dst = CTb + (long long)col * p.ldct + row;
@@ -247,12 +243,31 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
         }
-        if (mirror) {  // element (row, col) with row < col also at (col, row)
+        if (mirror) {  // element (row, col) with row < col also at (col, row): rows row..row+3 are contiguous there
+          if (all && row + 3 < col) {
+            if (C) {
+              float* dst = C + (long long)col * p.ldc + row;
+              if ((p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+              else
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (!ok[e] || row + e == col) continue;
-            if (C) C[(long long)col * p.ldc + row + e] = v[e];
-            if (Cb) Cb[(long long)col * p.ldcb + row + e] = f32_to_bf16(v[e]);
+                for (int e = 0; e < 4; ++e) dst[e] = v[e];
+            }
+            if (Cb) {
+              bf16_t* dst = Cb + (long long)col * p.ldcb + row;
+              if ((p.ldcb & 3) == 0)
+                *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                             pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+              else
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dst[e] = f32_to_bf16(v[e]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (!ok[e] || row + e == col) continue;
+              if (C) C[(long long)col * p.ldc + row + e] = v[e];
+              if (Cb) Cb[(long long)col * p.ldcb + row + e] = f32_to_bf16(v[e]);
+            }
           }
         }
       }

@@ -12,6 +12,10 @@ enum : int { NLB_NF = 0, NLB_J = 1, NLB_BOUND = 2, NLB_NSCAL = 4 };
 
 struct NlbArgs {
   int nb, n, T, sign, splits;
+  int ssc;                  // columns per sum-of-squares block of the V A outputs (64: split-K path, 128: full path)
+  int vmm_u;                // full path: MFMA steps per load batch of the V A kernel (2, 4 or 8)
+  int ksplit, kslice;       // full path: k slices per V A product and their length (a multiple of 64); part holds
+                            // ksplit x 32 x n partial products
   long long lda;
   const float* A[MAXB];     // n x n, upper triangle read
   const float* Vin[MAXB];   // init: the random start (32 x n)
@@ -41,6 +45,8 @@ hipError_t nlb_rownorm_launch(const NlbArgs& a, hipStream_t st);
 hipError_t nlb_init_launch(const NlbArgs& a, hipStream_t st);
 hipError_t nlb_reduce_launch(const NlbArgs& a, int normalize_in, hipStream_t st);
 hipError_t nlb_final_launch(const NlbArgs& a, const NlbFinal& f, hipStream_t st);
+// fully stored matrices: stage 0 row norms (rn2, rpart = row max |A|, cpart = diagonal), 1 init, 2 one V A product
+hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st);
 hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
 

@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(256) nlb_reduce_kernel(const NlbArgs p, int no
 // One workgroup (64 threads) per matrix: bound = nf * max_r |V4_r|, then the consumer's scalars.
 __global__ void __launch_bounds__(64) nlb_final_kernel(const NlbArgs p, NlbFinal f) {
   const int b = blockIdx.x, lane = threadIdx.x;
-  const int nbk = (p.n + 63) / 64;
+  const int nbk = (p.n + p.ssc - 1) / p.ssc;
   const float* __restrict__ ss = p.ssin[b];
   float m = 0.f;
   if (lane < NLB_K) {
@@ -225,6 +225,378 @@ hipError_t nlb_reduce_launch(const NlbArgs& a, int normalize_in, hipStream_t st)
 }
 hipError_t nlb_final_launch(const NlbArgs& a, const NlbFinal& f, hipStream_t st) {
   hipLaunchKernelGGL(nlb_final_kernel, dim3(a.nb), dim3(64), 0, st, a, f);
+  return hipGetLastError();
+}
+
+
+// ================================================================================================================
+// Norm lower bounds of fully stored matrices (fp32 or bf16 storage): row-parallel row norms, an init kernel that
+// reads them directly, and split-K V A products whose partials a second kernel sums in a fixed order (the
+// input-row normalisation and 1/nf are folded into that epilogue, which also writes the sums of squares the next
+// product normalises with).
+
+// Row statistics of a fully stored matrix, one wave per row: rn2[i] = sum_j A_ij^2, rpart[i] = max_j |A_ij|,
+// cpart[i] = A_ii (skew: the diagonal counts as zero, psgd_pro.py:50 takes max |A| of a matrix whose diagonal is
+// zero). Rows are read in 16-byte chunks when every row start is 16-byte aligned.
+template <typename T>
+__global__ void __launch_bounds__(256) rownorm_full_kernel(const NlbArgs p) {
+  constexpr int ACH = 16 / sizeof(T);
+  const int nrb = (p.n + 3) / 4;
+  const int b = blockIdx.x / nrb, rb = blockIdx.x % nrb;
+  const int lane = threadIdx.x & 63, i = rb * 4 + (threadIdx.x >> 6);
+  if (i >= p.n) return;
+  const int n = p.n;
+  const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
+  const T* __restrict__ row = A + (long long)i * p.lda;
+  const bool va = (p.lda % ACH) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  float s = 0.f, m = 0.f;
+  int j0 = 0;
+  if (va) {
+    const int nv = n / ACH;
+    for (int c = lane; c < nv; c += 64) {
+      const uint4 u = reinterpret_cast<const uint4*>(row)[c];
+      const T* t = reinterpret_cast<const T*>(&u);
+#pragma unroll
+      for (int e = 0; e < ACH; ++e) {
+        float v = to_f32<T>(t[e]);
+        if (p.sign < 0 && c * ACH + e == i) v = 0.f;
+        s += v * v;
+        m = fmaxf(m, fabsf(v));
+      }
+    }
+    j0 = nv * ACH;
+  }
+  for (int j = j0 + lane; j < n; j += 64) {
+    float v = to_f32<T>(row[j]);
+    if (p.sign < 0 && j == i) v = 0.f;
+    s += v * v;
+    m = fmaxf(m, fabsf(v));
+  }
+  s = wave_sum(s);
+  m = wave_max(m);
+  if (lane == 0) {
+    p.rn2[b][i] = s;
+    p.rpart[b][i] = m;
+    p.cpart[b][i] = to_f32<T>(row[i]);
+  }
+}
+
+// One workgroup per (matrix, row r of V): argmax of rn2 (first maximum), nf = max diagonal (SPD) or max |A|
+// (skew) + smallest normal, then V0[r] = a_j + sgn(<a_j, V_r>) V_r with a_j = row j of A / nf (psgd_pro.py:25-33,
+// :49-57). Workgroup r = 0 also publishes nf and j.
+template <typename T>
+__global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
+  __shared__ float red[4];
+  __shared__ float sval[4];
+  __shared__ int sidx[4];
+  __shared__ float snf;
+  __shared__ int sj;
+  const int b = blockIdx.x / NLB_K, r = blockIdx.x % NLB_K;
+  const int tid = threadIdx.x, n = p.n;
+  const float* __restrict__ rn2 = p.rn2[b];
+  float best = -1.f, am = 0.f, dm = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < n; i += 256) {
+    const float s = rn2[i];
+    if (s > best) { best = s; bi = i; }
+    am = fmaxf(am, p.rpart[b][i]);
+    dm = fmaxf(dm, p.cpart[b][i]);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { sval[tid >> 6] = best; sidx[tid >> 6] = bi; }
+  am = block_max(am, red);
+  dm = block_max(dm, red);
+  if (tid == 0) {
+    float bv = sval[0];
+    int bj = sidx[0];
+    for (int w = 1; w < 4; ++w)
+      if (sval[w] > bv || (sval[w] == bv && sidx[w] < bj)) { bv = sval[w]; bj = sidx[w]; }
+    sj = bj < n ? bj : 0;
+    const float nf = (p.sign > 0 ? dm : am) + kSmallestNormal;
+    snf = nf;
+    if (r == 0) {
+      p.scal[b][NLB_NF] = nf;
+      p.scal[b][NLB_J] = (float)sj;
+    }
+  }
+  __syncthreads();
+  const T* __restrict__ arow = reinterpret_cast<const T*>(p.A[b]) + (long long)sj * p.lda;
+  const int j = sj;
+  const float nf = snf;
+  const float* __restrict__ vr = p.Vin[b] + (long long)r * n;
+  T* __restrict__ v0 = reinterpret_cast<T*>(p.Vout[b]) + (long long)r * n;
+  float d = 0.f;
+  for (int k = tid; k < n; k += 256) d += (p.sign < 0 && k == j ? 0.f : to_f32<T>(arow[k])) / nf * vr[k];
+  d = block_sum(d, red);
+  const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
+  for (int k = tid; k < n; k += 256)
+    v0[k] = from_f32<T>((p.sign < 0 && k == j ? 0.f : to_f32<T>(arow[k])) / nf + sg * vr[k]);
+}
+
+// W = V A^T * (1 / nf) * (normalize ? 1 / (|V_r| + smallest normal) : 1) for symmetric or skew A read in full;
+// A^T = +-A, and a sign flip of every product leaves every row norm of the iteration, hence the bound, unchanged.
+// Reading A^T makes both operands k-contiguous: rows c of A for output columns c, rows r of V.
+// Workgroup: 32 rows x 128 columns x one k slice (kslice, a multiple of 64), 4 waves of 32 columns (2 x 2 MFMA
+// tiles of 16 x 16). Every operand element is used by one wave only (V rows are shared through the caches), so the
+// lanes load their MFMA fragments as 16-byte pieces straight from memory, 4 k steps at a time: no LDS staging and
+// no barriers, and the loads in flight are bounded by registers only. V is stored in A's type T (the init kernel
+// and the epilogues write it so): bf16 with v_mfma_f32_16x16x32_bf16, fp32 with v_mfma_f32_16x16x4_f32.
+// ksplit > 1: each workgroup stores its 32 x 128 partial in part[b][s] and vmm_reduce_kernel sums the slices in
+// order s = 0, 1, ... and runs the epilogue. A single-workgroup handshake (a device-scope fence and an arrival
+// counter) would need an L2 write-back and invalidate per workgroup on this multi-XCD part, which costs more than
+// the separate launch. Epilogue: W, and ssout[r][cb] = sum over the block's columns of W[r][c]^2.
+// grid: nb * ceil(n / 128) * ksplit, the k slice fastest.
+constexpr int VMM_C = 128;
+
+// 1 / nf, times 1 / (|W_r| + smallest normal) of the previous product when normalize (psgd_pro.py:36-38).
+__device__ __forceinline__ float vmm_row_scale(const NlbArgs& p, int b, int r, int nbk, int normalize) {
+  float sc = 1.f / p.scal[b][NLB_NF];
+  if (normalize) {
+    const float* ss = p.ssin[b];
+    float s = 0.f;
+    for (int q = 0; q < nbk; ++q) s += ss[r * nbk + q];
+    sc = sc / (sqrtf(s) + kSmallestNormal);
+  }
+  return sc;
+}
+
+template <typename T, int U>  // U: MFMA steps whose loads are issued together
+__global__ void __launch_bounds__(256) vmm_full_kernel(const NlbArgs p, int normalize) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int ACH = 16 / sizeof(T);  // elements per 16-byte piece
+  constexpr int KS = 4 * ACH;          // k per MFMA step: lane group g holds pieces at k + g ACH
+  __shared__ float rs[NLB_K];
+  __shared__ float ssw[4][NLB_K];
+  const int nbk = (p.n + VMM_C - 1) / VMM_C;
+  const int ks = blockIdx.x % p.ksplit, bc = blockIdx.x / p.ksplit;
+  const int b = bc / nbk, cb = bc % nbk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n = p.n, c0 = cb * VMM_C;
+  const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
+  const T* __restrict__ V = reinterpret_cast<const T*>(p.Vin[b]);
+  if (tid < NLB_K) rs[tid] = vmm_row_scale(p, b, tid, nbk, normalize);
+  // 16-byte buffer loads (out-of-range lanes read zero, no branches) where every row start is 16-byte aligned and
+  // both matrices span < 2^31 bytes (uniform per launch); element loads otherwise
+  const bool va = (p.lda % ACH) == 0 && (n % ACH) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(V) & 15) == 0 && (long long)n * p.lda * sizeof(T) < kOob &&
+                  (long long)NLB_K * n * sizeof(T) < kOob;
+  // MFMA operands straight from memory: V rows i*16 + r16 (A operand), A rows = output columns (B operand)
+  int cj[2];
+  bool aok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cj[j] = c0 + wave * 32 + j * 16 + r16;
+    aok[j] = cj[j] < n;
+  }
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const uint4 (&vf)[2], const uint4 (&af)[2]) {
+    if constexpr (BF) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vf[i]),
+                                                              __builtin_bit_cast(bf16x8_t, af[j]), acc[i][j], 0, 0, 0);
+    } else {  // element s of every lane's piece: k = kk + 4 g + s, the same map for both operands
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float((&vf[i].x)[s4]),
+                                                             __uint_as_float((&af[j].x)[s4]), acc[i][j], 0, 0, 0);
+    }
+  };
+  const int kbeg = ks * p.kslice, kend = min(n, kbeg + p.kslice);
+  if (va) {
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * n * sizeof(T));
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * sizeof(T));
+    int vo[2], ao[2];  // byte offsets of this lane's pieces at k = 0
+#pragma unroll
+    for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * n + g * ACH) * (int)sizeof(T);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) ao[j] = (int)(((long long)cj[j] * p.lda + g * ACH) * sizeof(T));
+    for (int k0 = kbeg; k0 < kend; k0 += U * KS) {
+      uint4 vf[U][2], af[U][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kk = k0 + u * KS, so = kk * (int)sizeof(T);
+        const bool in = kk + g * ACH < kend;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          vf[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, in ? vo[i] : kOob, so, 0));
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          af[u][j] = __builtin_bit_cast(uint4,
+                                        __builtin_amdgcn_raw_buffer_load_b128(ra, in && aok[j] ? ao[j] : kOob, so, 0));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep all U steps' loads ahead of the first MFMA
+#pragma unroll
+      for (int u = 0; u < U; ++u) mma(vf[u], af[u]);
+    }
+  } else {
+    for (int k0 = kbeg; k0 < kend; k0 += KS) {
+      uint4 vf[2], af[2];
+      const int kl = k0 + g * ACH;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        T t[ACH];
+        const T* src = V + (long long)(i * 16 + r16) * n + kl;
+#pragma unroll
+        for (int e = 0; e < ACH; ++e) t[e] = kl + e < kend ? src[e] : T(0);
+        vf[i] = *reinterpret_cast<const uint4*>(t);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        T t[ACH];
+        const T* src = A + (long long)(aok[j] ? cj[j] : 0) * p.lda + kl;
+#pragma unroll
+        for (int e = 0; e < ACH; ++e) t[e] = aok[j] && kl + e < kend ? src[e] : T(0);
+        af[j] = *reinterpret_cast<const uint4*>(t);
+      }
+      mma(vf, af);
+    }
+  }
+  __syncthreads();  // rs
+  // lane holds rows i*16 + 4g + e of column wave*32 + j*16 + r16
+  if (p.ksplit > 1) {  // partial product of this k slice; vmm_reduce_kernel finishes the column block
+    float* __restrict__ P = p.part[b];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = c0 + wave * 32 + j * 16 + r16;
+      if (col < n) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) P[((long long)ks * NLB_K + i * 16 + g * 4 + e) * n + col] = acc[i][j][e];
+      }
+    }
+    return;
+  }
+  T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]);
+  float sq[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sq[i][e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = c0 + wave * 32 + j * 16 + r16;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = i * 16 + g * 4 + e;
+        const float w = acc[i][j][e] * rs[row];
+        if (col < n) {
+          W[(long long)row * n + col] = from_f32<T>(w);
+          sq[i][e] += w * w;
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = sq[i][e];
+      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+      sq[i][e] = v;
+    }
+  if (r16 == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ssw[wave][i * 16 + g * 4 + e] = sq[i][e];
+  }
+  __syncthreads();
+  if (tid < NLB_K) p.ssout[b][tid * nbk + cb] = ssw[0][tid] + ssw[1][tid] + ssw[2][tid] + ssw[3][tid];
+}
+
+// Sum of the ksplit (<= VMM_MAXS) partial products of 8 rows x 128 columns in slice order, then the epilogue of
+// vmm_full_kernel (row scale, W in the storage type T, per-row sums of squares of the fp32 values over the block's
+// columns). Thread (rg, c) owns rows r0 + rg + 2t (t < 4) of column c and issues the loads of all slices and rows
+// at once (slices >= ksplit read zero through the buffer range check; adding zeros keeps the sum). grid: nb *
+// ceil(n / 128) * 4.
+constexpr int VMM_MAXS = 8;
+
+template <typename T>
+__global__ void __launch_bounds__(256) vmm_reduce_kernel(const NlbArgs p, int normalize) {
+  __shared__ float rs[8];
+  __shared__ float ssw[4][4];
+  const int nbk = (p.n + VMM_C - 1) / VMM_C;
+  const int b = blockIdx.x / (nbk * 4), cb = (blockIdx.x / 4) % nbk, r0 = (blockIdx.x % 4) * 8;
+  const int tid = threadIdx.x, n = p.n;
+  if (tid < 8) rs[tid] = vmm_row_scale(p, b, r0 + tid, nbk, normalize);
+  const int col = cb * VMM_C + (tid & 127), rg = tid >> 7;
+  const bool ok = col < n;
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part[b], (long long)p.ksplit * NLB_K * n * 4);
+  const int vo = ok ? ((r0 + rg) * n + col) * 4 : kOob;
+  float x[VMM_MAXS][4];
+#pragma unroll
+  for (int q = 0; q < VMM_MAXS; ++q)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      x[q][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rp, q < p.ksplit ? vo : kOob, (q * NLB_K + 2 * t) * n * 4, 0));
+  float w[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    w[t] = x[0][t];
+#pragma unroll
+    for (int q = 1; q < VMM_MAXS; ++q) w[t] += x[q][t];
+  }
+  __syncthreads();
+  T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int lr = rg + 2 * t;
+    const float v = ok ? w[t] * rs[lr] : 0.f;
+    if (ok) W[(long long)(r0 + lr) * n + col] = from_f32<T>(v);
+    const float sq = wave_sum(v * v);
+    if ((tid & 63) == 0) ssw[tid >> 6][t] = sq;
+  }
+  __syncthreads();
+  if (tid < 8) {
+    const int g = tid & 1, t = tid >> 1;  // local row tid = g + 2 t: waves 2g and 2g + 1
+    p.ssout[b][(r0 + tid) * nbk + cb] = ssw[2 * g][t] + ssw[2 * g + 1][t];
+  }
+}
+
+hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st) {
+  if (stage == 0) {
+    const int nrb = (a.n + 3) / 4;
+    if (a_bf16) hipLaunchKernelGGL(rownorm_full_kernel<bf16_t>, dim3(nrb * a.nb), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(rownorm_full_kernel<float>, dim3(nrb * a.nb), dim3(256), 0, st, a);
+  } else if (stage == 1) {
+    if (a_bf16) hipLaunchKernelGGL(nlb_init_full_kernel<bf16_t>, dim3(a.nb * NLB_K), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(nlb_init_full_kernel<float>, dim3(a.nb * NLB_K), dim3(256), 0, st, a);
+  } else {
+    const int nbk = (a.n + VMM_C - 1) / VMM_C;
+    if (a.ksplit < 1 || a.ksplit > VMM_MAXS || a.kslice % 64 != 0 || (long long)a.ksplit * a.kslice < a.n)
+      return hipErrorInvalidValue;
+    const dim3 grid(nbk * a.nb * a.ksplit);
+    if (a_bf16) {
+      if (a.vmm_u == 8) hipLaunchKernelGGL((vmm_full_kernel<bf16_t, 8>), grid, dim3(256), 0, st, a, normalize);
+      else if (a.vmm_u == 2) hipLaunchKernelGGL((vmm_full_kernel<bf16_t, 2>), grid, dim3(256), 0, st, a, normalize);
+      else hipLaunchKernelGGL((vmm_full_kernel<bf16_t, 4>), grid, dim3(256), 0, st, a, normalize);
+      if (a.ksplit > 1) hipLaunchKernelGGL(vmm_reduce_kernel<bf16_t>, dim3(nbk * a.nb * 4), dim3(256), 0, st, a, normalize);
+    } else {
+      if (a.vmm_u == 8) hipLaunchKernelGGL((vmm_full_kernel<float, 8>), grid, dim3(256), 0, st, a, normalize);
+      else if (a.vmm_u == 2) hipLaunchKernelGGL((vmm_full_kernel<float, 2>), grid, dim3(256), 0, st, a, normalize);
+      else hipLaunchKernelGGL((vmm_full_kernel<float, 4>), grid, dim3(256), 0, st, a, normalize);
+      if (a.ksplit > 1) hipLaunchKernelGGL(vmm_reduce_kernel<float>, dim3(nbk * a.nb * 4), dim3(256), 0, st, a, normalize);
+    }
+  }
   return hipGetLastError();
 }
 

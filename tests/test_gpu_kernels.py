@@ -189,6 +189,65 @@ def test_norm_lower_bound_matches_oracle(hip, n, sign):
     assert got <= top * (1 + 1e-5)
 
 
+_NLB_CASES = {}
+
+
+def _nlb_case(n, sign):
+    """SPD X X^T (rank n/2 + 1) or skew Y - Y^T, fixed per (n, sign)."""
+    if (n, sign) not in _NLB_CASES:
+        if sign > 0:
+            X = rnd(n, n // 2 + 1, seed=n + 2)
+            S = X @ X.T
+        else:
+            Y = rnd(n, n, seed=n + 3)
+            S = Y - Y.T
+        _NLB_CASES[(n, sign)] = S
+    return _NLB_CASES[(n, sign)]
+
+
+def nlb_full(As, Vs, sign):
+    n = As[0].shape[0]
+    outs = [torch.empty((), device=DEV, dtype=torch.float32) for _ in As]
+    L.call_ws(L.lib().psgdk_norm_lower_bound_full, n, sign, len(As), L.ptrs(As), As[0].stride(0),
+              L.dtype_code(As[0].dtype), L.ptrs(Vs), L.ptrs(outs), ws=K._WS, device=As[0].device,
+              stream=L.stream_of(As[0]))
+    return [float(o) for o in outs]
+
+
+@pytest.mark.parametrize("n,pad", [(1, 0), (37, 0), (100, 0), (100, 4), (100, 3), (130, 6), (768, 0), (1000, 8),
+                                   (3072, 0)])
+@pytest.mark.parametrize("sign", [1, -1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("target", [1, 1024, 1 << 20])
+def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, target):
+    """Full-storage bound (psgd_pro.py:19-65) of two matrices in one call, against the float64 oracle on the same
+    (storage-rounded) matrices. target sets the split-K workgroup target: 1 gives one k slice, 2^20 the most
+    slices, 1024 the default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load
+    path). fp32: rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
+    from oracle.psgd_oracle import norm_lower_bound
+    S = _nlb_case(n, sign)
+    S2 = 0.5 * S.flip(0).flip(1)  # another matrix of the same kind
+    mats = [S.to(dtype), S2.to(dtype)]
+    Vs = [rnd(32, n, seed=11), rnd(32, n, seed=12)]
+    dev_mats = []
+    for M in mats:
+        buf = torch.zeros(n, n + pad, dtype=dtype)
+        buf[:, :n] = M
+        dev_mats.append(buf.to(DEV)[:, :n])
+    lib = L.lib()
+    assert lib.psgdk_set_option(2, target) == 0
+    try:
+        got = nlb_full(dev_mats, [v.to(DEV) for v in Vs], sign)
+    finally:
+        lib.psgdk_set_option(2, 1024)
+    rel = 1e-5 if dtype == torch.float32 else 2e-2
+    for M, V, g in zip(mats, Vs, got):
+        ref = float(norm_lower_bound(M.double(), V.double(), skew=sign < 0))
+        assert g == pytest.approx(ref, rel=rel, abs=1e-30)
+        top = float(torch.linalg.matrix_norm(M.double(), 2))
+        assert g <= top * (1 + rel)
+
+
 def test_hip_ops_plugin_methods(hip):
     """The ops class methods (psgd_pro_fast.EagerOps interface) against their eager definitions."""
     ops = K.make_ops(())
