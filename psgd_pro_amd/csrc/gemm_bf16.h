@@ -27,7 +27,7 @@ struct GB16Args {
   float* part[MAXB];
 };
 
-// cfg 0: 256 x 256 tiles, cfg 1: 128 x 128 tiles
+// cfg 0: 256 x 256 tiles (8 waves), cfg 1: 128 x 128 tiles (4 waves), cfg 2: 256 x 256 tiles (4 waves)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg);
 

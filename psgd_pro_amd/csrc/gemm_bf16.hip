@@ -2,8 +2,10 @@
 //
 // Every operand arrives in HBM as bf16 rows with k contiguous (producers write transposed copies where a consumer
 // needs one), so the main loop is only 16-byte global loads, 16-byte LDS stores and 16-byte LDS fragment reads: no
-// conversion, no in-register transposes. Macro tile BM x BN x 64 with 4 waves (2 x 2), each wave owning a
-// (BM/2) x (BN/2) block of v_mfma_f32_16x16x32_bf16 tiles (8 x 8 for 256 x 256: 256 fp32 accumulators per lane).
+// conversion, no in-register transposes. Macro tile BM x BN x 64 with WGM x WGN waves, each wave owning a
+// (BM/WGM) x (BN/WGN) block of v_mfma_f32_16x16x32_bf16 tiles. The large configuration runs 8 waves of 128 x 64
+// (128 fp32 accumulators per lane, two waves per SIMD): while one wave waits on LDS, a barrier or the epilogue's
+// memory traffic, the other keeps the SIMD's MFMA pipe busy.
 // LDS holds two stages of A and B, rows padded to 144 bytes (64 bf16 + 8): 16 lanes reading 16 consecutive rows
 // at the same k hit 16 distinct 16-byte bank groups. Global loads for tile k+1 are in flight while tile k is
 // multiplied; one barrier per k tile. The (problem, tile) list is dealt out so each XCD gets a contiguous run.
@@ -15,7 +17,7 @@ namespace psgdk {
 
 namespace {
 
-constexpr int BK = 64, KP = 72, NT = 256;
+constexpr int BK = 64, KP = 72;
 
 __device__ __forceinline__ int remap_xcd(int w, int G) {
   const int cnt = G / 8, rem = G % 8, xcd = w % 8, slot = w / 8;
@@ -28,7 +30,7 @@ __device__ __forceinline__ int remap_xcd(int w, int G) {
 // group and the tile's k origin are the scalar offset. A lane whose row is past the operand or whose k chunk is
 // past K (K is a multiple of 8) gets an offset beyond the buffer extent: it reads zero (or, where the scalar part
 // wraps the 32-bit sum, some element of the same buffer), and either way only feeds outputs that are not stored.
-template <int ROWS>
+template <int ROWS, int NT>
 struct Ld {
   static constexpr int NV = ROWS * (BK / 8) / NT;  // 16-byte vectors per thread
   uint4 r[NV];
@@ -58,9 +60,12 @@ struct Ld {
 
 }  // namespace
 
-template <int BM, int BN, int EPI>
-__global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
-  constexpr int FM = BM / 32, FN = BN / 32;  // 16x16 tiles per wave along m, n (2 x 2 waves)
+// WGM x WGN waves, each owning a TM x TN block (TM = BM / WGM, TN = BN / WGN) of 16 x 16 MFMA tiles.
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Args p) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int TM = BM / WGM, TN = BN / WGN;
+  constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 tiles per wave along m, n
   extern __shared__ __align__(16) unsigned char smem[];
   bf16_t* const As0 = reinterpret_cast<bf16_t*>(smem);
   bf16_t* const Bs0 = As0 + 2 * BM * KP;
@@ -82,7 +87,7 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
   const bf16_t* __restrict__ Ap = p.A[b];
   const bf16_t* __restrict__ Bp = p.tri ? p.A[b] : p.B[b];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int r = lane & 15, g = lane >> 4;
 
   f32x4_t acc[FM][FN];
@@ -97,8 +102,8 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
   const int rowsB = p.tri ? p.M : p.N;
   const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * 8) * 2);
   const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * 8) * 2);
-  Ld<BM> la;
-  Ld<BN> lb;
+  Ld<BM, NT> la;
+  Ld<BN, NT> lb;
   la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K);
   lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K);
   la.store(As0);
@@ -119,13 +124,13 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
       bf16x8_t bfr[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * FN * 16 + j * 16 + r) * KP + ks * 32 + g * 8);
-      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * FM * 16 + r) * KP + ks * 32 + g * 8);
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ks * 32 + g * 8);
+      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + r) * KP + ks * 32 + g * 8);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         bf16x8_t a_nxt = a_cur;
         if (i + 1 < FM)
-          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * FM * 16 + (i + 1) * 16 + r) * KP + ks * 32 + g * 8);
+          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + (i + 1) * 16 + r) * KP + ks * 32 + g * 8);
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, bfr[j], acc[i][j], 0, 0, 0);
         a_cur = a_nxt;
@@ -138,13 +143,13 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
     __syncthreads();
   }
 
-  // Epilogue through LDS (idle after the main loop), in two halves of each wave's rows so that 4 waves x
-  // (BM/4 x BN/2) fp32 fit: (1) the wave parks half of its accumulators in its own LDS slot (static register
+  // Epilogue through LDS (idle after the main loop), in two halves of each wave's rows so that every wave's
+  // (TM/2 x TN) fp32 fit: (1) the wave parks half of its accumulators in its own LDS slot (static register
   // indices only); (2) row pass: each lane takes 4 consecutive columns of a row, applies the epilogue, writes the
   // value back to LDS and stores C / Cb rows (16- and 8-byte stores); (3) column pass: each lane takes 4
   // consecutive rows of a column for the transposed bf16 copy, the SYRK mirror and the Procrustes trace.
-  constexpr int HR = BM / 4;       // rows per wave per half
-  constexpr int WC = BN / 2;       // columns per wave
+  constexpr int HR = TM / 2;       // rows per wave per half
+  constexpr int WC = TN;           // columns per wave
   constexpr int EP = WC + 4;       // LDS row pitch (floats)
   float* const ep = reinterpret_cast<float*>(smem) + wave * HR * EP;
   float* __restrict__ C = p.C[b];
@@ -168,8 +173,8 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) ep[(ii * 16 + g * 4 + e) * EP + j * 16 + r] = acc[h * (FM / 2) + ii][j][e];
     __syncthreads();
-    const int grow0 = m0 + wm * (BM / 2) + h * HR;  // global row of local row 0
-    const int gcol0 = n0 + wn * WC;
+    const int grow0 = m0 + wm * TM + h * HR;  // global row of local row 0
+    const int gcol0 = n0 + wn * TN;
     // (2) row pass
     for (int idx = lane; idx < HR * (WC / 4); idx += 64) {
       const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
@@ -286,16 +291,17 @@ __global__ void __launch_bounds__(NT) gemm_bf16_kernel(const GB16Args p) {
 }
 
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
-  const int T = cfg ? 128 : 256;
+  const int T = cfg == 1 ? 128 : 256;
   const long long tm = (M + T - 1) / T, tn = (N + T - 1) / T;
   return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
-  constexpr int smem_main = 2 * (BM + BN) * KP * 2, smem_epi = 4 * (BM / 4) * (BN / 2 + 4) * 4;
+  constexpr int NW = WGM * WGN;
+  constexpr int smem_main = 2 * (BM + BN) * KP * 2, smem_epi = NW * (BM / WGM / 2) * (BN / WGN + 4) * 4;
   constexpr int smem = smem_main > smem_epi ? smem_main : smem_epi;
-  auto fn = gemm_bf16_kernel<BM, BN, EPI>;
+  auto fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
@@ -305,25 +311,28 @@ static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;
-  hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(NT), smem, st, a);
+  hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(64 * NW), smem, st, a);
   return hipGetLastError();
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WGM, int WGN>
 static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
   switch (a.epi) {
-    case EPI_FACTOR: return launch_b16<BM, BN, EPI_FACTOR>(a, st);
-    case EPI_PROC: return launch_b16<BM, BN, EPI_PROC>(a, st);
-    case EPI_SCALE: return launch_b16<BM, BN, EPI_SCALE>(a, st);
-    case EPI_RQ: return launch_b16<BM, BN, EPI_RQ>(a, st);
-    case EPI_SUMSQ: return launch_b16<BM, BN, EPI_SUMSQ>(a, st);
-    default: return launch_b16<BM, BN, EPI_STORE>(a, st);
+    case EPI_FACTOR: return launch_b16<BM, BN, WGM, WGN, EPI_FACTOR>(a, st);
+    case EPI_PROC: return launch_b16<BM, BN, WGM, WGN, EPI_PROC>(a, st);
+    case EPI_SCALE: return launch_b16<BM, BN, WGM, WGN, EPI_SCALE>(a, st);
+    case EPI_RQ: return launch_b16<BM, BN, WGM, WGN, EPI_RQ>(a, st);
+    case EPI_SUMSQ: return launch_b16<BM, BN, WGM, WGN, EPI_SUMSQ>(a, st);
+    default: return launch_b16<BM, BN, WGM, WGN, EPI_STORE>(a, st);
   }
 }
 
+// cfg 0: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64; cfg 1: 128 x 128 tiles, 4 waves of 64 x 64;
+// cfg 2: 256 x 256 tiles, 4 waves of 128 x 128 (one wave per SIMD)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st) {
-  if (cfg == 1) return launch_epi<128, 128>(a, st);
-  return launch_epi<256, 256>(a, st);
+  if (cfg == 1) return launch_epi<128, 128, 2, 2>(a, st);
+  if (cfg == 2) return launch_epi<256, 256, 2, 2>(a, st);
+  return launch_epi<256, 256, 2, 4>(a, st);
 }
 
 }  // namespace psgdk
