@@ -6,8 +6,8 @@
 // (BM/WGM) x (BN/WGN) block of v_mfma_f32_16x16x32_bf16 tiles. The large configuration runs 8 waves of 128 x 64
 // (128 fp32 accumulators per lane, two waves per SIMD): while one wave waits on LDS, a barrier or the epilogue's
 // memory traffic, the other keeps the SIMD's MFMA pipe busy.
-// LDS holds two stages of A and B, rows padded to 144 bytes (64 bf16 + 8): 16 lanes reading 16 consecutive rows
-// at the same k hit 16 distinct 16-byte bank groups. Global loads for tile k+1 are in flight while tile k is
+// LDS holds two stages of A and B in 128-byte rows with XOR-swizzled 16-byte chunks (conflict-free fragment
+// reads and row writes). Global loads for tile k+1 are in flight while tile k is
 // multiplied; one barrier per k tile. The (problem, tile) list is dealt out so each XCD gets a contiguous run.
 // Operands: K a multiple of 8, leading dimensions multiples of 8, 16-byte aligned bases, under 2 GiB each (the host
 // routes anything else to the general engine); ragged M, N and K edges read zeros through the buffer extent.
@@ -17,13 +17,19 @@ namespace psgdk {
 
 namespace {
 
-constexpr int BK = 64, KP = 72;
+constexpr int BK = 64, KP = 64;  // LDS rows of 128 bytes, 16-byte chunks XOR-swizzled by row (swz)
 
 __device__ __forceinline__ int remap_xcd(int w, int G) {
   const int cnt = G / 8, rem = G % 8, xcd = w % 8, slot = w / 8;
   return xcd < rem ? xcd * (cnt + 1) + slot : rem * (cnt + 1) + (xcd - rem) * cnt + slot;
 }
 
+
+// LDS slot of the 16-byte k chunk c (0..7) of tile row `row`. Rows are 128 bytes with no padding; the XOR spreads
+// the 16 rows of an MFMA fragment read (16 lanes, one chunk each) over 16 distinct 16-byte bank groups, which
+// the LDS serves without conflicts (measured: 4 cycles per ds_read_b128, against 8 with rows padded to 144
+// bytes); the 8 lanes that write one row still cover its 8 slots.
+__device__ __forceinline__ int swz(int row, int c) { return c ^ (row & 7); }
 
 // Global -> register -> LDS staging of one ROWS x 64 bf16 tile with buffer loads. Lane `tid` owns the 16-byte
 // k chunk tid % 8 of rows tid / 8 + 32 i (i < NV): the lane part of the byte offset is the VGPR offset, the row
@@ -35,10 +41,11 @@ struct Ld {
   static constexpr int NV = ROWS * (BK / 8) / NT;  // 16-byte vectors per thread
   uint4 r[NV];
 
+  // t: the thread's index among the NT threads that load this tile
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int voff, long long ld, int mn0, int rows, int k0,
-                                       int K) {
-    const int lrow = threadIdx.x >> 3;
-    const bool kok = k0 + (threadIdx.x & 7) * 8 < K;
+                                       int K, int t) {
+    const int lrow = t >> 3;
+    const bool kok = k0 + (t & 7) * 8 < K;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int base = mn0 + i * (NT / 8);
@@ -48,12 +55,11 @@ struct Ld {
     }
   }
 
-  __device__ __forceinline__ void store(bf16_t* lds) const {
-    const int tid = threadIdx.x;
+  __device__ __forceinline__ void store(bf16_t* lds, int t) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int v = tid + NT * i, row = v >> 3, kv = v & 7;
-      *reinterpret_cast<uint4*>(lds + row * KP + kv * 8) = r[i];
+      const int v = t + NT * i, row = v >> 3, kv = v & 7;
+      *reinterpret_cast<uint4*>(lds + row * KP + swz(row, kv) * 8) = r[i];
     }
   }
 };
@@ -65,6 +71,7 @@ template <int BM, int BN, int WGM, int WGN, int EPI>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Args p) {
   constexpr int NT = 64 * WGM * WGN;
   constexpr int TM = BM / WGM, TN = BN / WGN;
+  constexpr bool PP = WGM == 2 && WGN == 4;  // ping-pong main loop (8 waves, two groups of 4)
   constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 tiles per wave along m, n
   extern __shared__ __align__(16) unsigned char smem[];
   bf16_t* const As0 = reinterpret_cast<bf16_t*>(smem);
@@ -100,47 +107,130 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   const __amdgpu_buffer_rsrc_t rsA = make_rsrc(Ap, (long long)p.M * p.lda * 2);
   const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bp, (long long)(p.tri ? p.M : p.N) * p.ldb * 2);
   const int rowsB = p.tri ? p.M : p.N;
-  const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * 8) * 2);
-  const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * 8) * 2);
-  Ld<BM, NT> la;
-  Ld<BN, NT> lb;
-  la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K);
-  lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K);
-  la.store(As0);
-  lb.store(Bs0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      la.load(rsA, voffA, p.lda, m0, p.M, (kt + 1) * BK, p.K);
-      lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 1) * BK, p.K);
-    }
-    const bf16_t* As = As0 + cur * BM * KP;
-    const bf16_t* Bs = Bs0 + cur * BN * KP;
+  // 2 x 32-deep MFMA steps of one k tile from LDS (B fragments held, A fragments streamed one row ahead)
+  auto mma_tile = [&](const bf16_t* As, const bf16_t* Bs) {
 #pragma unroll 1
     for (int ks = 0; ks < BK / 32; ++ks) {
+      // fragment rows are 16-aligned plus r, so their swizzle is that of r
+      const int ko = swz(r, ks * 4 + g) * 8;
       bf16x8_t bfr[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ks * 32 + g * 8);
-      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + r) * KP + ks * 32 + g * 8);
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
+      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + r) * KP + ko);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         bf16x8_t a_nxt = a_cur;
         if (i + 1 < FM)
-          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + (i + 1) * 16 + r) * KP + ks * 32 + g * 8);
+          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + (i + 1) * 16 + r) * KP + ko);
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, bfr[j], acc[i][j], 0, 0, 0);
         a_cur = a_nxt;
       }
     }
-    if (more) {
-      la.store(As0 + (cur ^ 1) * BM * KP);
-      lb.store(Bs0 + (cur ^ 1) * BN * KP);
+  };
+  // Ping-pong compute phase: the other wave on the SIMD is moving data, so this wave alone must keep the MFMA
+  // pipe fed. All 2 x FM A rows of the tile are streamed 3 rows ahead of their MFMAs; the second step's B
+  // fragments are read during the first step. sched_group_barrier pins the order: reads go out ahead of the
+  // MFMAs that hide their latency.
+  auto mma_tile_pp = [&](const bf16_t* As, const bf16_t* Bs) {
+    constexpr int NQ = 2 * FM, LA = 3;
+    bf16x8_t bq[2][FN], aq[NQ];
+    auto rd_b = [&](int ks) {
+      const int ko = swz(r, ks * 4 + g) * 8;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bq[ks][j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
+    };
+    auto rd_a = [&](int q) {
+      const int ks = q / FM, i = q % FM;
+      aq[q] = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + i * 16 + r) * KP + swz(r, ks * 4 + g) * 8);
+    };
+    rd_b(0);
+#pragma unroll
+    for (int q = 0; q < LA; ++q) rd_a(q);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (q + LA < NQ) rd_a(q + LA);
+      if (q == FM / 2) rd_b(1);
+      const int ks = q / FM, i = q % FM;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q], bq[ks][j], acc[i][j], 0, 0, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, FN + LA, 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (q + LA < NQ && q == FM / 2) __builtin_amdgcn_sched_group_barrier(0x100, FN + 1, 0);
+      else if (q + LA < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      else if (q == FM / 2) __builtin_amdgcn_sched_group_barrier(0x100, FN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+    }
+  };
+  if constexpr (!PP) {
+    const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * 8) * 2);
+    const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * 8) * 2);
+    Ld<BM, NT> la;
+    Ld<BN, NT> lb;
+    la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K, tid);
+    lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K, tid);
+    la.store(As0, tid);
+    lb.store(Bs0, tid);
     __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        la.load(rsA, voffA, p.lda, m0, p.M, (kt + 1) * BK, p.K, tid);
+        lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 1) * BK, p.K, tid);
+      }
+      mma_tile(As0 + cur * BM * KP, Bs0 + cur * BN * KP);
+      if (more) {
+        la.store(As0 + (cur ^ 1) * BM * KP, tid);
+        lb.store(Bs0 + (cur ^ 1) * BN * KP, tid);
+      }
+      __syncthreads();
+    }
+  } else {
+    // Ping-pong: wave group h = wave / 4 (one wave of each group per SIMD) owns output rows 128 h .. 128 h + 127
+    // and loads rows 128 h .. of both operand tiles. The groups run half a tile apart:
+    //   group 0: compute(kt) | barrier | memory(kt) | barrier
+    //   group 1: memory(kt)  | barrier | compute(kt) | barrier
+    // memory(kt) writes the group's half of tile kt + 1 (in registers since two phases) into LDS stage
+    // (kt + 1) & 1 and requests its half of tile kt + 2. Between two barriers one group multiplies while the other
+    // moves data, so each SIMD's MFMA pipe has a wave with work; the stage being written is never the one read in
+    // the same phase. Past the last tile the loads read zeros and their LDS stage is not read again.
+    // The group's row offset rides in the lane index t (t / 8 is the tile row), not in the loads' scalar offset:
+    // h is uniform per wave but not provably so, and a scalar offset derived from it would be waterfalled.
+    const int h = wave >> 2, t = (tid & 255) + h * (NT / 2) * 4;  // rows h * 128 + (tid & 255) / 8 (+ 32 i)
+    static_assert(BM == BN && (NT / 2) * 4 == (BM / 2) * 8, "ping-pong loader: one group loads half the rows");
+    const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * 8) * 2);
+    const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * 8) * 2);
+    Ld<BM / 2, NT / 2> la;
+    Ld<BN / 2, NT / 2> lb;
+    la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K, t);
+    lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K, t);
+    la.store(As0, t);
+    lb.store(Bs0, t);
+    la.load(rsA, voffA, p.lda, m0, p.M, BK, p.K, t);
+    lb.load(rsB, voffB, p.ldb, n0, rowsB, BK, p.K, t);
+    __syncthreads();
+    auto memory = [&](int kt) {
+      const int nxt = (kt + 1) & 1;
+      la.store(As0 + nxt * BM * KP, t);
+      lb.store(Bs0 + nxt * BN * KP, t);
+      la.load(rsA, voffA, p.lda, m0, p.M, (kt + 2) * BK, p.K, t);
+      lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 2) * BK, p.K, t);
+    };
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (h == 0) mma_tile_pp(As0 + cur * BM * KP, Bs0 + cur * BN * KP);
+      else memory(kt);
+      __syncthreads();
+      if (h == 0) memory(kt);
+      else mma_tile_pp(As0 + cur * BM * KP, Bs0 + cur * BN * KP);
+      __syncthreads();
+    }
   }
 
   // Epilogue through LDS (idle after the main loop), in two halves of each wave's rows so that every wave's
