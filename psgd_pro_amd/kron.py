@@ -30,6 +30,13 @@ def _is_dense(size, numel, max_size, max_skew):
     return not (size <= 1 or size > max_size or size ** 2 > max_skew * numel)
 
 
+class _Lane:
+    """A side stream (None: the caller's stream) with the workspaces of the groups it runs."""
+
+    def __init__(self, stream, ws_upd, ws_app, ws_bal):
+        self.stream, self.ws_upd, self.ws_app, self.ws_bal = stream, ws_upd, ws_app, ws_bal
+
+
 class _Param:
     __slots__ = ("index", "shape", "m", "n", "kind", "Q", "P", "L", "group", "slot", "scalar")
 
@@ -68,7 +75,8 @@ class KronWhiten:
                  precision=None,
                  draws="device",
                  seed=None,
-                 tri=None):
+                 tri=None,
+                 streams=4):
         self.lr_params = lr_params
         self.lr_preconditioner = lr_preconditioner
         self.betaL = betaL
@@ -106,6 +114,9 @@ class KronWhiten:
         self._groups = None
         self._ms, self._counter_m = None, 0
         self._ws_upd, self._ws_app, self._ws_bal = L.Workspace(), L.Workspace(), L.Workspace()
+        if int(streams) < 0:
+            raise ValueError("streams: a count >= 0")
+        self._nstreams, self._lanes = int(streams), None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
             self._init([p.squeeze() for p in self._params_with_grad], preconditioner_init_scale)
@@ -250,36 +261,72 @@ class KronWhiten:
             off += a + b
         return noise, V, coins
 
+    # Groups share no state (each owns its factors, shadows and parameters), so their update and apply chains
+    # run on side streams of default priority, each with its own workspaces: one group's memory-bound epilogues
+    # and small kernels overlap another's GEMMs. The side streams start after the caller's stream reaches the
+    # step and the caller's stream waits for all of them before it continues; results do not depend on the
+    # number of streams.
+    def _lanes_for(self, dev):
+        if self._nstreams == 0 or len(self._groups) < 2:
+            return [_Lane(None, self._ws_upd, self._ws_app, self._ws_bal)]
+        if self._lanes is None:
+            self._lanes = [_Lane(torch.cuda.Stream(device=dev), L.Workspace(), L.Workspace(), L.Workspace())
+                           for _ in range(min(self._nstreams, len(self._groups)))]
+        return self._lanes
+
+    def _fork(self, dev):
+        lanes = self._lanes_for(dev)
+        cur = torch.cuda.current_stream(dev)
+        for ln in lanes:
+            if ln.stream is not None:
+                ln.stream.wait_stream(cur)
+        return cur, lanes
+
+    @staticmethod
+    def _join(cur, lanes):
+        for ln in lanes:
+            if ln.stream is not None:
+                cur.wait_stream(ln.stream)
+
     def _update(self, srcs):
         noise, V, coins = self._draw_update(srcs)
         o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, 0)
-        for grp in self._groups:
-            s = grp.struct
-            gdt = self._bind_sources(grp, srcs)
-            o.grad_eps = torch.finfo(gdt).eps
-            nz = L.ptrs([noise[p.index] for p in grp.members])
-            vv = L.ptrs([V[p.index] for p in grp.members])
-            L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=self._ws_upd, device=srcs[0].device,
-                      stream=L.stream_of(srcs[0]))
-        for grp in self._groups:
-            flags = [int(coins[p.index]) for p in grp.members]
-            if any(flags):
-                fl = (ctypes.c_int32 * len(flags))(*flags)
-                L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=self._ws_bal,
-                          device=srcs[0].device, stream=L.stream_of(srcs[0]))
+        dev = srcs[0].device
+        cur, lanes = self._fork(dev)
+        for gi, grp in enumerate(self._groups):
+            ln = lanes[gi % len(lanes)]
+            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                s = grp.struct
+                gdt = self._bind_sources(grp, srcs)
+                o.grad_eps = torch.finfo(gdt).eps
+                nz = L.ptrs([noise[p.index] for p in grp.members])
+                vv = L.ptrs([V[p.index] for p in grp.members])
+                L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=ln.ws_upd, device=dev,
+                          stream=L.stream_of(srcs[0]))
+                flags = [int(coins[p.index]) for p in grp.members]
+                if any(flags):
+                    fl = (ctypes.c_int32 * len(flags))(*flags)
+                    L.call_ws(L.lib().psgdk_kron2d_balance, s, fl, self._tri, ws=ln.ws_bal, device=dev,
+                              stream=L.stream_of(srcs[0]))
+        self._join(cur, lanes)
 
     def _apply(self, srcs):
         max_avg, max_el = self.grad_clip_max_amps
         o = L.ApplyOpts(self.lr_params, max_avg, max_el, self._tri)
-        pre = [torch.empty(p.m, p.n, device=srcs[0].device, dtype=torch.float32) for p in self._params] \
+        dev = srcs[0].device
+        pre = [torch.empty(p.m, p.n, device=dev, dtype=torch.float32) for p in self._params] \
             if self.capture else None
-        for grp in self._groups:
-            s = grp.struct
-            self._bind_sources(grp, srcs)
-            prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
-            po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
-            L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=self._ws_app, device=srcs[0].device,
-                      stream=L.stream_of(srcs[0]))
+        cur, lanes = self._fork(dev)
+        for gi, grp in enumerate(self._groups):
+            ln = lanes[gi % len(lanes)]
+            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                s = grp.struct
+                self._bind_sources(grp, srcs)
+                prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
+                po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
+                L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=ln.ws_app, device=dev,
+                          stream=L.stream_of(srcs[0]))
+        self._join(cur, lanes)
         if pre is not None:
             self.pre = [t.view(p.shape) for t, p in zip(pre, self._params)]
 

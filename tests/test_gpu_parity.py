@@ -165,6 +165,25 @@ def test_state_dict_round_trip(hip):
         assert torch.equal(a, b.detach())
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_side_streams_bitwise_identical(hip, prec):
+    """Weight groups on side streams (streams=4) give bit-identical factors and parameters to one stream
+    (streams=0): the groups share no state and every kernel reduces in a fixed order."""
+    shapes = [(64, 96), (96, 64), (128, 128), (32,), (64, 96)]
+    runs = []
+    for ns in (0, 4):
+        W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
+        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=7,
+                         momentum=0.9, precision=prec, streams=ns)
+        for t in range(4):
+            opt.step_math([g.to(DEV) for g in grads_for(shapes, t)])
+        torch.cuda.synchronize()
+        qs = [q.detach().clone() for i in range(len(shapes)) for q in opt.factors(i)[0]]
+        runs.append(([w.detach().clone() for w in W], qs))
+    for a, b in zip(runs[0][0] + runs[0][1], runs[1][0] + runs[1][1]):
+        assert torch.equal(a, b)
+
+
 def test_step_closure_and_loss_curve(hip):
     """A least-squares model trained 100 steps through step(closure): the GPU optimizer (float32 model and
     gradients) and the float64 oracle (float64 model and gradients, same draws) give matching loss curves. The
