@@ -181,7 +181,9 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
 /* Launch profiling (diagnostic, single host thread): after psgdk_profile_start every MFMA-engine launch is
  * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
  * waits for the recorded events and fills one record per launch: the kernel instantiation id
- * (cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype; cfg 0 = 128 x 128 tiles, 1 = 32 x 128), whether it was a
+ * (general engine: cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype, cfg 0 = 128 x 128 tiles, 1 = 32 x 128;
+ * bf16 engine: 5000 + cfg * 10 + epilogue, cfg 0 = 256 x 256 tiles on 8 waves, 1 = 128 x 128 on 4, 2 = 256 x 256
+ * on 4), whether it was a
  * SYRK (triangular grid), the problems in the launch, its device time and its algorithmic flop count
  * (SYRK n(n+1)k, TRMM n(n+1)p, GEMM 2mnk, per problem). With out NULL only *n_records is set (records kept). */
 typedef struct psgdk_prof_record {

@@ -137,9 +137,10 @@ class Workspace:
 
 def kernel_name(kernel_id):
     """Kernel template name of a profiling kernel id."""
-    if kernel_id >= 5000:
-        t = 128 if kernel_id % 10 else 256
-        return f"gemm_bf16_kernel<{t}, {t}>"
+    if kernel_id >= 5000:  # 5000 + 10 cfg + epilogue
+        cfg, epi = divmod(kernel_id - 5000, 10)
+        tile = {0: "256, 256, 2, 4", 1: "128, 128, 2, 2", 2: "256, 256, 2, 2"}[cfg]
+        return f"gemm_bf16_kernel<{tile}, {epi}>"
     cfg, rest = divmod(kernel_id, 1000)
     prec, rest = divmod(rest, 100)
     adt, bdt = divmod(rest, 10)

@@ -239,7 +239,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   if (ntiles) *ntiles = gemm_bf16_tiles(M, N, tri, cfg);
   if (!g_prof.on) return hip_check(gemm_bf16_launch(a, cfg, st), "bf16 gemm launch");
   ProfRec r;
-  r.kernel_id = 5000 + cfg;
+  r.kernel_id = 5000 + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
   r.flops = tri ? (double)M * (M + 1) * K * nb : 2.0 * M * N * K * nb;
