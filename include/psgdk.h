@@ -124,8 +124,10 @@ typedef struct psgdk_kron2d {
   float* P[2][PSGDK_MAXB];   /* Q^T Q (dense: full symmetric, or upper triangle with tri bit 1) or q * q */
   float* L[2][PSGDK_MAXB];   /* one float each: the factor's Lipschitz smoothness EMA */
   /* bf16 shadows of dense factors for prec = PSGDK_PREC_BF16 (optional: NULL selects the general path): Qt16 is
-   * Q^T and P16 is P in bfloat16, d x d row-major. The library keeps them in step with Q and P (update, refresh,
-   * balance); psgdk_kron2d_refresh_p rebuilds both from the fp32 state. */
+   * Q^T and P16 is P in bfloat16, d x d row-major. The library keeps them in step with Q (update, refresh,
+   * balance); psgdk_kron2d_refresh_p rebuilds both from the fp32 state. With shadows (and tri = 0) the update
+   * refreshes only P16, the copy its readers use; fp32 P is current after psgdk_kron2d_refresh_p and
+   * psgdk_kron2d_balance, so a caller that reads P between them calls psgdk_kron2d_refresh_p first. */
   void* Qt16[2][PSGDK_MAXB];
   void* P16[2][PSGDK_MAXB];
 } psgdk_kron2d_t;

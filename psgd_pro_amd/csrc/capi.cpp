@@ -509,8 +509,9 @@ bool b16_group(const psgdk_kron2d_t* g, int tri) {
   for (int f = 0; f < 2; ++f)
     for (int b = 0; b < g->nb; ++b)
       if (!g->Qt16[f][b] || !g->P16[f][b] || !aligned16(g->Qt16[f][b]) || !aligned16(g->P16[f][b])) return false;
-  for (int b = 0; b < g->nb; ++b)
-    if (!aligned16(g->G[b])) return false;
+  // G's alignment does not matter: the update reads G through the noise kernel and the apply copies a misaligned
+  // bf16 G into aligned workspace, so a group's path depends on its own storage only (the bf16 path keeps fp32 P
+  // current at refresh points only, and no other path may run on the group in between)
   const int64_t big = std::max(g->m, g->n);
   if (big * big * 2 >= ((int64_t)1 << 31) || g->m * g->n * 2 >= ((int64_t)1 << 31)) return false;
   return true;
@@ -704,13 +705,13 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
   }
-  for (int f = 0; f < 2; ++f) {  // P = Q^T Q from the fresh Q^T shadow
+  for (int f = 0; f < 2; ++f) {  // P16 = bf16(Q^T Q) from the fresh Q^T shadow (its only per-step reader reads bf16;
+                                 // fp32 P is written by psgdk_kron2d_refresh_p / _balance from the same shadow)
     const int64_t d = dims[f];
     B16Out out;
-    out.ldc = d; out.ldcb = d;
+    out.ldcb = d;
     for (int b = 0; b < nb; ++b) {
       A[b] = g->Qt16[f][b];
-      out.C[b] = g->P[f][b];
       out.Cb[b] = reinterpret_cast<bf16_t*>(g->P16[f][b]);
     }
     EpiSpec e;
@@ -729,7 +730,8 @@ int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const*
   bf16_t *Gb[MAXB], *YTb[MAXB];
   float *pre[MAXB], *part[MAXB];
   const int np_max = gemm_bf16_tiles(m, n, 0, 1);
-  const bool conv = g->g_dtype != PSGDK_BF16;
+  bool conv = g->g_dtype != PSGDK_BF16;  // fp32 G, or a bf16 G the kernel cannot read in place: copy to bf16
+  for (int b = 0; b < nb; ++b) conv = conv || !aligned16(g->G[b]);
   for (int b = 0; b < nb; ++b) {
     Gb[b] = conv ? w.take<bf16_t>(mn) : nullptr;
     YTb[b] = w.take<bf16_t>(mn);

@@ -409,6 +409,8 @@ class KronWhiten:
                   momentum_buffers=[m.clone() for m in self._ms] if self._ms is not None else None,
                   generator=self._gen.get_state() if self._gen is not None else None)
         if self._params is not None:
+            for grp in self._groups:  # the bf16 path keeps only P's bf16 copy current between refreshes
+                self._refresh_p(grp)
             st["params"] = []
             for p in self._params:
                 ent = dict(shape=p.shape, kind=tuple(p.kind), Q=[], P=[], L=[])
@@ -446,6 +448,9 @@ class KronWhiten:
                 p.group.Ls[f][p.slot].copy_(ent["L"][j])
                 if ent.get("P"):
                     p.group.Ps[f][p.slot].copy_(ent["P"][j])
-        if not all(ent.get("P") for ent in st["params"]):
-            for grp in self._groups:
+        have_p = all(ent.get("P") for ent in st["params"])
+        for grp in self._groups:
+            # bf16 shadows (Q^T, P) are derived state: rebuild them from the loaded Q (their fp32 P is what
+            # state_dict saved, since it refreshes P first); other groups keep the saved P unless it is absent
+            if not have_p or any(x is not None for x in grp.P16):
                 self._refresh_p(grp)

@@ -145,20 +145,27 @@ def test_balance_matches_oracle(hip):
     assert rel_err_norm(P, Q[0].double().cpu().T @ Q[0].double().cpu()) < 1e-6
 
 
-def test_state_dict_round_trip(hip):
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_state_dict_round_trip(hip, prec):
+    """A state_dict taken mid-run and loaded into a fresh optimizer continues bit-identically. On the bf16 path the
+    update keeps only P's bf16 copy current, so state_dict refreshes P first: the saved P is Q^T Q of the
+    bf16-rounded Q (fp32 accumulation of bf16 products)."""
     shapes = [(64, 96), (32,)]
     W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
     opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=5,
-                     momentum=0.9)
+                     momentum=0.9, precision=prec)
     for t in range(3):
         opt.step_math([g.to(DEV) for g in grads_for(shapes, t)])
     st = opt.state_dict()
+    Q0, P0 = st["params"][0]["Q"][0].double().cpu(), st["params"][0]["P"][0].double().cpu()
+    Qr = Q0.to(torch.bfloat16).double() if prec == "bf16" else Q0
+    assert rel_err_norm(P0, Qr.T @ Qr) < 1e-6
     W0 = [w.detach().clone() for w in W]
     opt.step_math([g.to(DEV) for g in grads_for(shapes, 3)])
     after = [w.detach().clone() for w in W]
     W2 = [w0.clone().requires_grad_(True) for w0 in W0]
     opt2 = KronWhiten(W2, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=99,
-                      momentum=0.9)
+                      momentum=0.9, precision=prec)
     opt2.load_state_dict(st)
     opt2.step_math([g.to(DEV) for g in grads_for(shapes, 3)])
     for a, b in zip(after, W2):
