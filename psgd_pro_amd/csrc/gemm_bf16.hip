@@ -11,6 +11,8 @@
 // multiplied; one barrier per k tile. The (problem, tile) list is dealt out so each XCD gets a contiguous run.
 // Operands: K a multiple of 8, leading dimensions multiples of 8, 16-byte aligned bases, under 2 GiB each (the host
 // routes anything else to the general engine); ragged M, N and K edges read zeros through the buffer extent.
+#include <type_traits>
+
 #include "gemm_bf16.h"
 
 namespace psgdk {
@@ -252,6 +254,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) s1 = p.s[b][1];
   const bool mirror = p.tri && p.out_mode == 1;
   const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ;
+  auto al = [](const void* q, int bytes) { return (reinterpret_cast<uintptr_t>(q) & (bytes - 1)) == 0; };
+  const bool fast = m0 + BM <= p.M && n0 + BN <= p.N && (!p.tri || ti < tj) &&
+                    (!C || ((p.ldc & 3) == 0 && al(C, 16))) && (!Cb || ((p.ldcb & 3) == 0 && al(Cb, 8))) &&
+                    (!CTb || ((p.ldct & 3) == 0 && al(CTb, 8))) && (p.ldx & 3) == 0 &&
+                    (!X1 || al(X1, EPI == EPI_RQ ? 8 : 16)) && (!X2 || al(X2, 16));
   float t1 = 0.f, t2 = 0.f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -265,54 +272,85 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     __syncthreads();
     const int grow0 = m0 + wm * TM + h * HR;  // global row of local row 0
     const int gcol0 = n0 + wn * TN;
-    // (2) row pass
-    for (int idx = lane; idx < HR * (WC / 4); idx += 64) {
-      const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
-      const int row = grow0 + lr, col = gcol0 + lc;
-      float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
-      float v[4] = {a.x, a.y, a.z, a.w};
-      bool ok[4];
+    // (2) row pass, (3) column pass. An interior tile (fast: inside M and N, strictly above the diagonal for a
+    // SYRK, every leading dimension and base 16-byte compatible) needs no per-element checks, so its loads and
+    // stores are whole vectors and its unrolled loop keeps several iterations' loads in flight; edge tiles check
+    // each element.
+    auto row_pass = [&](auto fast_c) {
+      constexpr bool FAST = decltype(fast_c)::value;
+      constexpr int IT = HR * (WC / 4) / 64;
+      static_assert(IT * 64 == HR * (WC / 4), "row pass: whole iterations");
+#pragma unroll 4
+      for (int it = 0; it < IT; ++it) {
+        const int idx = lane + 64 * it;
+        const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
+        const int row = grow0 + lr, col = gcol0 + lc;
+        const float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
+        float v[4] = {a.x, a.y, a.z, a.w};
+        bool ok[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ok[e] = row < p.M && col + e < p.N && !(p.tri && row > col + e);
-      const long long xo = (long long)row * p.ldx + col;
+        for (int e = 0; e < 4; ++e) ok[e] = FAST || (row < p.M && col + e < p.N && !(p.tri && row > col + e));
+        const long long xo = (long long)row * p.ldx + col;
+        float q1[4] = {0.f, 0.f, 0.f, 0.f}, q2[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) {
+          if constexpr (FAST) {
+            const float4 t = *reinterpret_cast<const float4*>(X1 + xo);
+            q1[0] = t.x; q1[1] = t.y; q1[2] = t.z; q1[3] = t.w;
+          } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (EPI == EPI_FACTOR) {
-          const float q = ok[e] ? X1[xo + e] : 0.f;
-          v[e] = q - s0 * (v[e] - s1 * q);
-        } else if constexpr (EPI == EPI_PROC) {
-          v[e] = ok[e] ? X1[xo + e] + s0 * X2[xo + e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
-        } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
-          v[e] = s0 * v[e];
-          if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
-        } else {
-          v[e] = p.alpha * v[e];
-          if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
+            for (int e = 0; e < 4; ++e) q1[e] = ok[e] ? X1[xo + e] : 0.f;
+          }
+        }
+        if constexpr (EPI == EPI_PROC) {
+          if constexpr (FAST) {
+            const float4 t = *reinterpret_cast<const float4*>(X2 + xo);
+            q2[0] = t.x; q2[1] = t.y; q2[2] = t.z; q2[3] = t.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? X2[xo + e] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (EPI == EPI_FACTOR) {
+            v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
+          } else if constexpr (EPI == EPI_PROC) {
+            v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
+          } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
+            v[e] = s0 * v[e];
+            if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
+          } else {
+            v[e] = p.alpha * v[e];
+            if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
+          }
+        }
+        *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
+        const bool all = ok[0] && ok[1] && ok[2] && ok[3];
+        if (C) {
+          float* dst = C + (long long)row * p.ldc + col;
+          if (FAST || (all && (p.ldc & 3) == 0)) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          else
+#pragma unroll
+            for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = v[e];
+        }
+        if (Cb) {
+          bf16_t* dst = Cb + (long long)row * p.ldcb + col;
+          if (FAST || (all && (p.ldcb & 3) == 0))
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                         pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+          else
+#pragma unroll
+            for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
         }
       }
-      *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
-      const bool all = ok[0] && ok[1] && ok[2] && ok[3];
-      if (C) {
-        float* dst = C + (long long)row * p.ldc + col;
-        if (all && (p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        else
-#pragma unroll
-          for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = v[e];
-      }
-      if (Cb) {
-        bf16_t* dst = Cb + (long long)row * p.ldcb + col;
-        if (all && (p.ldcb & 3) == 0)
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
-                                                       pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
-        else
-#pragma unroll
-          for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
-      }
-    }
-    __syncthreads();
-    // (3) column pass
-    if (colpass) {
-      for (int idx = lane; idx < WC * (HR / 4); idx += 64) {
+    };
+    auto col_pass = [&](auto fast_c) {
+      constexpr bool FAST = decltype(fast_c)::value;
+      constexpr int IT = WC * (HR / 4) / 64;
+      static_assert(IT * 64 == WC * (HR / 4), "column pass: whole iterations");
+#pragma unroll 4
+      for (int it = 0; it < IT; ++it) {
+        const int idx = lane + 64 * it;
         const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
         const int col = gcol0 + lc, row = grow0 + lr;
         float v[4];
@@ -320,18 +358,24 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           v[e] = ep[(lr + e) * EP + lc];
-          ok[e] = row + e < p.M && col < p.N && !(p.tri && row + e > col);
+          ok[e] = FAST || (row + e < p.M && col < p.N && !(p.tri && row + e > col));
         }
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
         if constexpr (EPI == EPI_RQ) {  // X1: R in bf16, read at (col, row..row+3)
           const bf16_t* x = reinterpret_cast<const bf16_t*>(X1) + (long long)col * p.ldx + row;
+          if constexpr (FAST) {
+            const uint2 t = *reinterpret_cast<const uint2*>(x);
+            t2 += s0 * (bf16_to_f32((bf16_t)(t.x & 0xffff)) * v[0] + bf16_to_f32((bf16_t)(t.x >> 16)) * v[1] +
+                        bf16_to_f32((bf16_t)(t.y & 0xffff)) * v[2] + bf16_to_f32((bf16_t)(t.y >> 16)) * v[3]);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (ok[e]) t2 += s0 * bf16_to_f32(x[e]) * v[e];
+            for (int e = 0; e < 4; ++e)
+              if (ok[e]) t2 += s0 * bf16_to_f32(x[e]) * v[e];
+          }
         }
         if (CTb) {
           bf16_t* dst = CTb + (long long)col * p.ldct + row;
-          if (all && (p.ldct & 3) == 0)
+          if (FAST || (all && (p.ldct & 3) == 0))
             *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
                                                          pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
           else
@@ -339,17 +383,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
             for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
         }
         if (mirror) {  // element (row, col) with row < col also at (col, row): rows row..row+3 are contiguous there
-          if (all && row + 3 < col) {
+          if (FAST || (all && row + 3 < col)) {
             if (C) {
               float* dst = C + (long long)col * p.ldc + row;
-              if ((p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+              if (FAST || (p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
               else
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dst[e] = v[e];
             }
             if (Cb) {
               bf16_t* dst = Cb + (long long)col * p.ldcb + row;
-              if ((p.ldcb & 3) == 0)
+              if (FAST || (p.ldcb & 3) == 0)
                 *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
                                                              pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
               else
@@ -366,6 +410,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
           }
         }
       }
+    };
+    if (fast) row_pass(std::true_type{});
+    else row_pass(std::false_type{});
+    __syncthreads();
+    if (colpass) {
+      if (fast) col_pass(std::true_type{});
+      else col_pass(std::false_type{});
       __syncthreads();
     }
   }
