@@ -274,8 +274,9 @@ def test_hip_ops_plugin_methods(hip):
 # -------------------------------------------------------------------------------------------------------------- bf16
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 768, 320), (768, 768, 2304), (100, 70, 33), (1, 50, 77),
                                    (264, 520, 72), (3072, 768, 768), (4096, 4096, 256)])
-def test_gemm_bf16_k_contiguous(hip, m, n, k):
-    """A (m x k) B^T (B given n x k), both bf16 k-contiguous: the dedicated bf16 kernel (256 or 128 tiles)."""
+def test_gemm_bf16_k_contiguous(hip, b16cfg, m, n, k):
+    """A (m x k) B^T (B given n x k), both bf16 k-contiguous: the dedicated bf16 kernel in every tile
+    configuration (interior tiles take the unchecked epilogue, ragged ones the checked one)."""
     A = rnd(m, k, seed=m).to(torch.bfloat16)
     B = rnd(n, k, seed=n + 1).to(torch.bfloat16)
     C = K.gemm(A.to(DEV), B.to(DEV), False, True, True)
@@ -283,7 +284,7 @@ def test_gemm_bf16_k_contiguous(hip, m, n, k):
 
 
 @pytest.mark.parametrize("nb,m,n,k", [(12, 768, 768, 768), (12, 1024, 1024, 512)])
-def test_gemm_bf16_grouped(hip, nb, m, n, k):
+def test_gemm_bf16_grouped(hip, b16cfg, nb, m, n, k):
     As = [rnd(m, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     Bs = [rnd(n, k, seed=50 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     Cs = [torch.empty(m, n, device=DEV) for _ in range(nb)]
@@ -294,7 +295,7 @@ def test_gemm_bf16_grouped(hip, nb, m, n, k):
 
 
 @pytest.mark.parametrize("nb,n,k", [(1, 768, 2304), (1, 3072, 768), (16, 1024, 256), (1, 200, 72)])
-def test_syrk_bf16_k_contiguous(hip, nb, n, k):
+def test_syrk_bf16_k_contiguous(hip, b16cfg, nb, n, k):
     As = [rnd(n, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     Cs = [torch.full((n, n), float("nan"), device=DEV) for _ in range(nb)]
     L.check(hip.psgdk_syrk(1, 0, L.OUT_UPPER, n, k, 1, nb, L.ptrs(As), k, L.ptrs(Cs), n, L.stream_of(As[0])))

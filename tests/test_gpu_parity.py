@@ -104,10 +104,12 @@ def test_fp32_parity_1024_weight(hip):
     assert_fp32(worst, base)
 
 
-def test_bf16_parity(hip):
+def test_bf16_parity(hip, b16cfg):
     """bf16 gradients and bf16 MFMA inputs against the float32 oracle on the same gradients upcast: per-element
     2e-2 on Q (floor 1e-3 max); normwise 2e-2 on the preconditioned gradient and the parameters (a per-element
-    floor of 1e-3 max sits below bfloat16's rounding noise (2^-9) of a sum with cancellation)."""
+    floor of 1e-3 max sits below bfloat16's rounding noise (2^-9) of a sum with cancellation). Run in every tile
+    configuration of the bf16 kernel: 384 = 256 + 128 gives the 256-tile ones interior and ragged tiles, so every
+    fused epilogue (factor update, RQ with traces, Q update, SYRK mirror) runs on both of its paths."""
     eps16 = torch.finfo(torch.bfloat16).eps
     worst, _ = run_pair([(256, 384), (384, 256)], steps=8, skew=math.inf, prec="bf16", gdt=torch.bfloat16,
                         grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
