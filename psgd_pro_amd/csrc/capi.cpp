@@ -198,7 +198,7 @@ struct B16Out {
   int64_t ldc = 0, ldcb = 0, ldct = 0;
 };
 
-int g_tile_order = 0;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous runs
+int g_tile_order = 2;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous runs, 2 runs + grouped rows
 int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's tile config
 int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
 int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)

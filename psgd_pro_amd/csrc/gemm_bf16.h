@@ -15,7 +15,8 @@ struct GB16Args {
   int epi;
   int tri, out_mode;  // tri: SYRK (B is A); out_mode 0 upper, 1 mirrored
   int tiles_m, tiles_n, ntiles, nb;
-  int vec;            // 1: deal tiles to XCDs in contiguous runs; 0: problem-major order (WG id = tile)
+  int vec;            // 0: problem-major order (WG id = tile); 1: tiles dealt to XCDs in contiguous runs; 2: as 1,
+                      // with tile rows grouped by 4 inside each problem
   const bf16_t* A[MAXB];
   const bf16_t* B[MAXB];
   float* C[MAXB];

@@ -88,6 +88,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     int rem = tile, rowlen = p.tiles_m;
     while (rem >= rowlen) { rem -= rowlen; ++ti; --rowlen; }
     tj = ti + rem;
+  } else if (p.vec == 2) {
+    // groups of GM tile rows, column-major inside a group: the 32 workgroups an XCD runs at once cover a
+    // GM x 8 block of tiles, so each k step fetches GM + 8 operand panel slices into that XCD's L2
+    constexpr int GM = 4;
+    const int grp = tile / (GM * p.tiles_n), r0 = grp * GM;
+    const int gm = min(GM, p.tiles_m - r0), idx = tile - r0 * p.tiles_n;
+    ti = r0 + idx % gm;
+    tj = idx / gm;
   } else {
     ti = tile / p.tiles_n;
     tj = tile % p.tiles_n;

@@ -283,13 +283,18 @@ def test_gemm_bf16_k_contiguous(hip, b16cfg, m, n, k):
     check_gemm_bound(C, A.double(), B.double().T)
 
 
-@pytest.mark.parametrize("nb,m,n,k", [(12, 768, 768, 768), (12, 1024, 1024, 512)])
-def test_gemm_bf16_grouped(hip, b16cfg, nb, m, n, k):
+@pytest.mark.parametrize("order", [0, 1, 2])
+@pytest.mark.parametrize("nb,m,n,k", [(12, 768, 768, 768), (12, 1024, 1024, 512), (5, 1300, 520, 264)])
+def test_gemm_bf16_grouped(hip, b16cfg, order, nb, m, n, k):
+    """Grouped launches under every tile order (problem-major; contiguous runs per XCD; runs with tile rows grouped
+    by 4, where the last group of a problem may be shorter): each maps the grid onto every tile exactly once."""
+    assert hip.psgdk_set_option(0, order) == 0
     As = [rnd(m, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     Bs = [rnd(n, k, seed=50 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     Cs = [torch.empty(m, n, device=DEV) for _ in range(nb)]
     L.check(hip.psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(As), k, L.ptrs(Bs), k, 0.0, L.ptrs(Cs), n,
                            L.stream_of(As[0])))
+    hip.psgdk_set_option(0, 2)
     for A, B, C in zip(As, Bs, Cs):
         check_gemm_bound(C, A.double().cpu(), B.double().cpu().T)
 
