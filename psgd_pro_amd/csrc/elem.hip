@@ -51,11 +51,13 @@ hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // R[i][j] = sign * (Q[j][i] - Q[i][j]) and R[j][i] = -R[i][j] from one read of each 64 x 64 tile pair (I <= J):
-// both tiles are staged in LDS, each output tile is written row-major from there. Outputs: R fp32 (out, optional)
-// and R bf16 (out2, optional). grid: nb * T (T + 1) / 2, T = ceil(d / 64).
+// both tiles are staged in LDS (16-byte loads when rows are 16-byte aligned), each output tile is written
+// row-major from there, 4 consecutive columns per thread (16-byte fp32 / 8-byte bf16 stores). Outputs: R fp32
+// (out, optional) and R bf16 (out2, optional). grid: nb * T (T + 1) / 2, T = ceil(d / 64).
 __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
-  __shared__ float qa[64][65];  // Q[I block][J block]
-  __shared__ float qb[64][65];  // Q[J block][I block]
+  constexpr int TP = 65;        // LDS pitch (floats): column reads of the transposed tile are conflict-free
+  __shared__ float qa[64 * TP];  // Q[I block][J block]
+  __shared__ float qb[64 * TP];  // Q[J block][I block]
   const int d = (int)a.m, T = (d + 63) / 64, np = T * (T + 1) / 2;
   const int b = blockIdx.x / np;
   int t = blockIdx.x % np, I = 0;
@@ -66,31 +68,55 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
   const long long ld = a.ld;
   const float sg = (float)a.i0;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const int i = I * 64 + r, j = J * 64 + tx, i2 = J * 64 + r, j2 = I * 64 + tx;
-    qa[r][tx] = (i < d && j < d) ? Q[(long long)i * ld + j] : 0.f;
-    qb[r][tx] = (i2 < d && j2 < d) ? Q[(long long)i2 * ld + j2] : 0.f;
-  }
+  const int tid = threadIdx.x, c4 = (tid & 15) * 4, r0 = tid >> 4;  // 4 columns, rows r0 + 16 k
+  const bool full = (I + 1) * 64 <= d && (J + 1) * 64 <= d;
+  const bool vec = full && (ld & 3) == 0 && (reinterpret_cast<uintptr_t>(Q) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(R) & 15) == 0 && (reinterpret_cast<uintptr_t>(Rb) & 7) == 0;
+  auto stage = [&](float* dst, int rb, int cb) {  // Q[rb block][cb block] -> dst
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
+      float v[4];
+      if (vec) {
+        const float4 q = *reinterpret_cast<const float4*>(Q + (long long)gi * ld + gj);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (gi < d && gj + e < d) ? Q[(long long)gi * ld + gj + e] : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[r * TP + c4 + e] = v[e];
+    }
+  };
+  stage(qa, I, J);
+  stage(qb, J, I);
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    {  // R[I*64 + r][J*64 + tx] = sg (Q[J*64 + tx][I*64 + r] - Q[I*64 + r][J*64 + tx])
-      const int i = I * 64 + r, j = J * 64 + tx;
-      if (i < d && j < d) {
-        const float v = sg * (qb[tx][r] - qa[r][tx]);
-        if (R) R[(long long)i * ld + j] = v;
-        if (Rb) Rb[(long long)i * ld + j] = f32_to_bf16(v);
+  // out(rb, cb)[r][c] = sg (src_t[c][r] - src[r][c]): (I, J) from (qb, qa), (J, I) from (qa, qb)
+  auto emit = [&](const float* src, const float* srct, int rb, int cb) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
+      const long long o = (long long)gi * ld + gj;
+      if (vec) {
+        if (R) *reinterpret_cast<float4*>(R + o) = make_float4(v[0], v[1], v[2], v[3]);
+        if (Rb)
+          *reinterpret_cast<uint2*>(Rb + o) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                        pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+      } else if (gi < d) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gj + e < d) {
+            if (R) R[o + e] = v[e];
+            if (Rb) Rb[o + e] = f32_to_bf16(v[e]);
+          }
       }
     }
-    if (I != J) {  // R[J*64 + r][I*64 + tx] = sg (Q[I*64 + tx][J*64 + r] - Q[J*64 + r][I*64 + tx])
-      const int i = J * 64 + r, j = I * 64 + tx;
-      if (i < d && j < d) {
-        const float v = sg * (qa[tx][r] - qb[r][tx]);
-        if (R) R[(long long)i * ld + j] = v;
-        if (Rb) Rb[(long long)i * ld + j] = f32_to_bf16(v);
-      }
-    }
-  }
+  };
+  emit(qa, qb, I, J);
+  if (I != J) emit(qb, qa, J, I);
 }
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
   const long long T = (a.m + 63) / 64;
