@@ -40,7 +40,7 @@ def parse_args():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--skew", default="inf")
     ap.add_argument("--blocks", type=int, default=12)
-    ap.add_argument("--config", choices=["vitb", "syrk", "copy"], default="vitb")
+    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
@@ -254,6 +254,46 @@ def bench_syrk(args):
     return lines
 
 
+def bench_llama(args):
+    """Llama-class shapes: one 4096 x 4096 and one 4096 x 14336 weight, bf16 gradients, every factor dense
+    (max_size 16384, max_skew inf), fp32 factors, bf16 MFMA path, update every step."""
+    import torch
+    from oracle.psgd_oracle import flops_2d
+    from psgd_pro_amd import KronWhiten
+    from psgd_pro_amd import _lib as L
+    dev = torch.device("cuda:0")
+    shapes = [(4096, 4096), (4096, 14336)]
+    gen = torch.Generator().manual_seed(0)
+    params = [(0.02 * torch.randn(s, generator=gen)).to(dev).requires_grad_(True) for s in shapes]
+    grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
+    opt = KronWhiten(params, preconditioner_max_size=16384, preconditioner_max_skew=math.inf,
+                     preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0,
+                     streams=args.streams)
+    flops_step = sum(flops_2d(m, n, True, True) for m, n in shapes)
+    steps, warmup = min(args.steps, 10), min(args.warmup, 3)
+    for _ in range(warmup):
+        opt.step_math(grads)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step_math(grads)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    opt._nstreams = 0
+    L.profile_start()
+    for _ in range(2):
+        opt.step_math(grads)
+    torch.cuda.synchronize()
+    recs = L.profile_stop()
+    return {"metric": "Kron update+apply ms/step at Llama shapes (4096x4096 + 4096x14336), 1 GPU", "value": round(ms, 3),
+            "unit": "ms/step", "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": args.precision,
+            "data": "synthetic", "config": {"workload": "llama-4096x4096+4096x14336-kron-update-apply",
+                                            "max_size": 16384, "max_skew": "inf", "streams": args.streams},
+            "algorithmic_tflop_per_step": round(flops_step / 1e12, 3),
+            "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2),
+            "launch_classes": launch_classes(recs, 2, top=8)}
+
+
 def bench_copy(args):
     """Calibration for the HBM counters: one device-to-device copy of 256 MiB (read 256 MiB, write 256 MiB)."""
     import torch
@@ -279,6 +319,9 @@ def main():
         sys.exit(1)
     if args.config == "copy":
         print(json.dumps(bench_copy(args)), flush=True)
+        return
+    if args.config == "llama":
+        print(json.dumps(bench_llama(args)), flush=True)
         return
     if args.config == "syrk":
         for ln in bench_syrk(args):
