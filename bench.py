@@ -40,7 +40,7 @@ def parse_args():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--skew", default="inf")
     ap.add_argument("--blocks", type=int, default=12)
-    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama"], default="vitb")
+    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
@@ -294,6 +294,104 @@ def bench_llama(args):
             "launch_classes": launch_classes(recs, 2, top=8)}
 
 
+def _vit(dim=512, depth=6, heads=8, dim_head=64, mlp=1024, patch=4, image=32, classes=10):
+    """A ViT of vit_pro.py's architecture (vit_pro.py:76-226: pre-norm attention and MLP blocks, patch embedding
+    with LayerNorms, class token, learned positions, final LayerNorm, class-token head). The attention products
+    run in float32 on contiguous operands outside autocast; the Linear layers run under bf16 autocast."""
+    import torch
+    from torch import nn
+
+    class Attention(nn.Module):
+        def __init__(self):
+            super().__init__()
+            inner = heads * dim_head
+            self.norm = nn.LayerNorm(dim)
+            self.to_qkv = nn.Linear(dim, 3 * inner, bias=False)
+            self.to_out = nn.Linear(inner, dim)
+
+        def forward(self, x):
+            b, n, _ = x.shape
+            qkv = self.to_qkv(self.norm(x)).reshape(b, n, 3, heads, dim_head).permute(2, 0, 3, 1, 4)
+            with torch.autocast("cuda", enabled=False):
+                q, k, v = (t.float().contiguous() for t in qkv)
+                att = torch.matmul(q, k.transpose(-1, -2).contiguous()) * dim_head ** -0.5
+                out = torch.matmul(att.softmax(dim=-1), v)
+            return self.to_out(out.permute(0, 2, 1, 3).reshape(b, n, heads * dim_head))
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = Attention()
+            self.ff = nn.Sequential(nn.LayerNorm(dim), nn.Linear(dim, mlp), nn.GELU(), nn.Linear(mlp, dim))
+
+        def forward(self, x):
+            x = self.attn(x) + x
+            return self.ff(x) + x
+
+    class ViT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            pdim = 3 * patch * patch
+            self.np = (image // patch) ** 2
+            self.embed = nn.Sequential(nn.LayerNorm(pdim), nn.Linear(pdim, dim), nn.LayerNorm(dim))
+            self.pos = nn.Parameter(torch.randn(1, self.np + 1, dim))
+            self.cls = nn.Parameter(torch.randn(1, 1, dim))
+            self.blocks = nn.ModuleList([Block() for _ in range(depth)])
+            self.norm = nn.LayerNorm(dim)
+            self.head = nn.Linear(dim, classes)
+
+        def forward(self, img):
+            b, h = img.shape[0], image // patch
+            x = img.reshape(b, 3, h, patch, h, patch).permute(0, 2, 4, 3, 5, 1).reshape(b, h * h, -1)
+            x = self.embed(x)
+            x = torch.cat([self.cls.expand(b, 1, dim), x], dim=1) + self.pos
+            for blk in self.blocks:
+                x = blk(x)
+            return self.head(self.norm(x)[:, 0])
+
+    return ViT()
+
+
+def bench_e2e(args):
+    """Optimizer share of an end-to-end training step: the ViT above, batch 512 of synthetic 32 x 32 images and
+    labels, bf16 autocast, KronWhiten with vit_pro.py's settings (max_skew 2, momentum 0.9, lr 1e-3, update every
+    step). t_step = forward + backward + optimizer, t_opt = optimizer; medians of 50 steps after 10 warmup."""
+    import statistics
+    import torch
+    from psgd_pro_amd import KronWhiten
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = _vit().to(dev)
+    params = [p for p in model.parameters() if p.requires_grad]
+    x = torch.randn(512, 3, 32, 32, device=dev)
+    y = torch.randint(0, 10, (512,), device=dev)
+    opt = KronWhiten(params, preconditioner_max_skew=2, lr_params=1e-3, preconditioner_update_probability=1.0,
+                     momentum=0.9, precision=args.precision, streams=args.streams)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(60)]
+    losses = []
+    for i in range(60):
+        e = ev[i]
+        e[0].record()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = torch.nn.functional.cross_entropy(model(x).float(), y)
+        grads = torch.autograd.grad(loss, params)
+        e[1].record()
+        opt.step_math(grads)
+        e[2].record()
+        losses.append(loss.detach())
+    torch.cuda.synchronize()
+    t_step = [ev[i][0].elapsed_time(ev[i][2]) for i in range(10, 60)]
+    t_opt = [ev[i][1].elapsed_time(ev[i][2]) for i in range(10, 60)]
+    ms_step, ms_opt = statistics.median(t_step), statistics.median(t_opt)
+    return {"metric": "optimizer share of an end-to-end ViT training step (t_opt / t_step), 1 GPU",
+            "value": round(ms_opt / ms_step, 4), "unit": "fraction", "higher_is_better": False,
+            "ms_step": round(ms_step, 3), "ms_opt": round(ms_opt, 3), "ms_fwd_bwd": round(ms_step - ms_opt, 3),
+            "loss_first_last": [round(float(losses[0]), 4), round(float(losses[-1]), 4)],
+            "dtype": args.precision, "data": "synthetic",
+            "config": {"workload": "vit-dim512-depth6-heads8-mlp1024-patch4-batch512-e2e", "params": len(params),
+                       "max_skew": 2, "momentum": 0.9, "streams": args.streams}}
+
+
 def bench_copy(args):
     """Calibration for the HBM counters: one device-to-device copy of 256 MiB (read 256 MiB, write 256 MiB)."""
     import torch
@@ -319,6 +417,9 @@ def main():
         sys.exit(1)
     if args.config == "copy":
         print(json.dumps(bench_copy(args)), flush=True)
+        return
+    if args.config == "e2e":
+        print(json.dumps(bench_e2e(args)), flush=True)
         return
     if args.config == "llama":
         print(json.dumps(bench_llama(args)), flush=True)
