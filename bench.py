@@ -44,6 +44,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
+    ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
     return ap.parse_args()
 
 
@@ -135,7 +136,7 @@ def bench_vitb(args):
     grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
     opt = KronWhiten(params, preconditioner_max_size=8192, preconditioner_max_skew=skew,
                      preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0,
-                     streams=args.streams)
+                     streams=args.streams, graphs=bool(args.graphs))
     flops_step = sum(flops_2d(m, n, is_dense(m, m * n, 8192, skew), is_dense(n, m * n, 8192, skew))
                      for m, n in shapes)
     for _ in range(args.warmup):
@@ -153,9 +154,9 @@ def bench_vitb(args):
     t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3 / args.steps
     ev_ms = e0.elapsed_time(e1) / args.steps
-    # Per-launch figures come from a second pass on one stream, so that each kernel's HIP-event duration is its
-    # own and not shared with another group's kernels.
-    opt._nstreams = 0
+    # Per-launch figures come from a second pass on one stream, eager, so that each kernel's HIP-event duration is
+    # its own and not shared with another group's kernels.
+    opt._nstreams, opt._use_graphs = 0, False
     opt.step_math(grads)
     torch.cuda.synchronize()
     L.profile_start()
@@ -194,6 +195,7 @@ def bench_vitb(args):
                    "max_skew": args.skew, "update_probability": 1.0, "parallelism": "none"},
         "gpu_ms_per_step": round(ev_ms, 3),
         "streams": args.streams,
+        "graphs": bool(args.graphs),
         "profile_pass": "per-launch figures (roofline, kernels, launch_classes) from a separate single-stream pass",
         "algorithmic_tflop_per_step": round(flops_step / 1e12, 4),
         "tflops": round(flops_step / (wall_ms * 1e-3) / 1e12, 2),
@@ -268,7 +270,7 @@ def bench_llama(args):
     grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
     opt = KronWhiten(params, preconditioner_max_size=16384, preconditioner_max_skew=math.inf,
                      preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0,
-                     streams=args.streams)
+                     streams=args.streams, graphs=bool(args.graphs))
     flops_step = sum(flops_2d(m, n, True, True) for m, n in shapes)
     steps, warmup = min(args.steps, 10), min(args.warmup, 3)
     for _ in range(warmup):
@@ -279,7 +281,7 @@ def bench_llama(args):
         opt.step_math(grads)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    opt._nstreams = 0
+    opt._nstreams, opt._use_graphs = 0, False
     L.profile_start()
     for _ in range(2):
         opt.step_math(grads)
@@ -366,7 +368,7 @@ def bench_e2e(args):
     x = torch.randn(512, 3, 32, 32, device=dev)
     y = torch.randint(0, 10, (512,), device=dev)
     opt = KronWhiten(params, preconditioner_max_skew=2, lr_params=1e-3, preconditioner_update_probability=1.0,
-                     momentum=0.9, precision=args.precision, streams=args.streams)
+                     momentum=0.9, precision=args.precision, streams=args.streams, graphs=bool(args.graphs))
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(60)]
     losses = []
     for i in range(60):
@@ -389,7 +391,7 @@ def bench_e2e(args):
             "loss_first_last": [round(float(losses[0]), 4), round(float(losses[-1]), 4)],
             "dtype": args.precision, "data": "synthetic",
             "config": {"workload": "vit-dim512-depth6-heads8-mlp1024-patch4-batch512-e2e", "params": len(params),
-                       "max_skew": 2, "momentum": 0.9, "streams": args.streams}}
+                       "max_skew": 2, "momentum": 0.9, "streams": args.streams, "graphs": bool(args.graphs)}}
 
 
 def bench_copy(args):

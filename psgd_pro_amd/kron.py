@@ -76,7 +76,8 @@ class KronWhiten:
                  draws="device",
                  seed=None,
                  tri=None,
-                 streams=4):
+                 streams=4,
+                 graphs=False):
         self.lr_params = lr_params
         self.lr_preconditioner = lr_preconditioner
         self.betaL = betaL
@@ -117,6 +118,9 @@ class KronWhiten:
         if int(streams) < 0:
             raise ValueError("streams: a count >= 0")
         self._nstreams, self._lanes = int(streams), None
+        self._use_graphs = bool(graphs)
+        self._graphs, self._seen = {}, set()
+        self._draw_buf = None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
             self._init([p.squeeze() for p in self._params_with_grad], preconditioner_init_scale)
@@ -242,6 +246,10 @@ class KronWhiten:
         total = sum(a + b for a, b in sizes)
         dev = srcs[0].device
         coins = []
+        # one persistent device buffer (fixed address: captured graphs read it), refilled before the step's work
+        if self._draw_buf is None or self._draw_buf.numel() < max(1, total):
+            self._draw_buf = torch.empty(max(1, total), device=dev, dtype=torch.float32)
+        flat = self._draw_buf[:total]
         if self._draws == "host":
             parts = []
             for p, (a, b) in zip(self._params, sizes):
@@ -250,10 +258,12 @@ class KronWhiten:
                     parts.append(torch.randn(_K * d, generator=self._gen))
                     parts.append(torch.randn(_K * d, generator=self._gen))
                 coins.append(self._rand() < 0.01)
-            flat = torch.cat(parts).pin_memory().to(dev, non_blocking=True) if total else None
+            if total:
+                flat.copy_(torch.cat(parts).pin_memory(), non_blocking=True)
         else:
             coins = (torch.rand(len(self._params), generator=self._gen) < 0.01).tolist()
-            flat = torch.randn(total, device=dev, dtype=torch.float32)
+            if total:
+                torch.randn(total, device=dev, dtype=torch.float32, out=flat)
         noise, V, off = [], [], 0
         for a, b in sizes:
             noise.append(flat[off:off + a])
@@ -288,8 +298,7 @@ class KronWhiten:
             if ln.stream is not None:
                 cur.wait_stream(ln.stream)
 
-    def _update(self, srcs):
-        noise, V, coins = self._draw_update(srcs)
+    def _update(self, srcs, noise, V):
         o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, 0)
         dev = srcs[0].device
         cur, lanes = self._fork(dev)
@@ -303,11 +312,20 @@ class KronWhiten:
                 vv = L.ptrs([V[p.index] for p in grp.members])
                 L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=ln.ws_upd, device=dev,
                           stream=L.stream_of(srcs[0]))
-                flags = [int(coins[p.index]) for p in grp.members]
-                if any(flags):
-                    fl = (ctypes.c_int32 * len(flags))(*flags)
-                    L.call_ws(L.lib().psgdk_kron2d_balance, s, fl, self._tri, ws=ln.ws_bal, device=dev,
-                              stream=L.stream_of(srcs[0]))
+        self._join(cur, lanes)
+
+    def _balance(self, coins, dev):
+        """psgd_pro.py:138-139: balance the factors of every parameter whose coin came up (eager, rare)."""
+        cur, lanes = self._fork(dev)
+        for gi, grp in enumerate(self._groups):
+            flags = [int(coins[p.index]) for p in grp.members]
+            if not any(flags):
+                continue
+            ln = lanes[gi % len(lanes)]
+            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                fl = (ctypes.c_int32 * len(flags))(*flags)
+                L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=ln.ws_bal, device=dev,
+                          stream=torch.cuda.current_stream(dev).cuda_stream)
         self._join(cur, lanes)
 
     def _apply(self, srcs):
@@ -347,30 +365,92 @@ class KronWhiten:
             # psgd_pro.py:329-332: scale = (max_p mean|g|^4 + damping^4)^(-1/8) (one host read at initialisation)
             m4 = max(float(torch.mean(g.float().abs() ** 4)) for g in grads)
             self._init(grads, (m4 + self.damping ** 4) ** (-1.0 / 8))
+        dev = grads[0].device
+        beta = None
         if self.momentum > 0:
             beta = min(self._counter_m / (1 + self._counter_m), self.momentum)
             self._counter_m += 1
             if self._ms is None:
                 self._ms = [torch.zeros(g.shape, device=g.device, dtype=torch.float32) for g in grads]
+        else:
+            self._ms, self._counter_m = None, 0
+        update = self._rand() < self.preconditioner_update_probability
+        noise = V = coins = None
+        if update:
+            noise, V, coins = self._draw_update(grads)
+        # device work in segments; the balancing coins act between them, as in psgd_pro.py:138-139 (inside the
+        # update, so before the apply when the update comes first)
+        first = update and self.update_preconditioner_first
+        self._segment("pre", grads, beta, first, not first, noise, V)
+        if first and any(coins):
+            self._balance(coins, dev)
+        if first:
+            self._segment("apply", grads, None, False, True, None, None)
+        elif update:
+            self._segment("update", grads, None, True, False, noise, V)
+            if any(coins):
+                self._balance(coins, dev)
+
+    def _device_work(self, grads, beta, do_update, do_apply, noise, V):
+        """Momentum (when beta is given), preconditioner update, apply: kernel launches only (capturable)."""
+        if beta is not None:
             for dt in (torch.float32, torch.bfloat16):
                 idx = [i for i, g in enumerate(grads) if g.dtype == dt]
                 for c in range(0, len(idx), L.MAXB):
                     ch = idx[c:c + L.MAXB]
-                    sizes = {grads[i].numel() for i in ch}
-                    for sz in sizes:
+                    for sz in {grads[i].numel() for i in ch}:
                         sel = [i for i in ch if grads[i].numel() == sz]
                         L.check(L.lib().psgdk_momentum(sz, beta, L.dtype_code(dt), len(sel),
                                                        L.ptrs([self._ms[i] for i in sel]),
                                                        L.ptrs([grads[i] for i in sel]), L.stream_of(grads[0])))
-        else:
-            self._ms, self._counter_m = None, 0
-        update = self._rand() < self.preconditioner_update_probability
         src = grads if self._whiten_grad else self._ms
-        if update and self.update_preconditioner_first:
-            self._update(src)
-        self._apply(self._ms if self.momentum > 0 else grads)
-        if update and not self.update_preconditioner_first:
-            self._update(src)
+        if do_update and self.update_preconditioner_first:
+            self._update(src, noise, V)
+        if do_apply:
+            self._apply(self._ms if self.momentum > 0 else grads)
+        if do_update and not self.update_preconditioner_first:
+            self._update(src, noise, V)
+
+    def _segment(self, kind, grads, beta, do_update, do_apply, noise, V):
+        """Runs one segment of device work eagerly, or (graphs=True) replays a captured HIP graph of it. A
+        graph bakes in its launch arguments, so it is keyed by every host value they take (segment, momentum
+        beta, learning rates, betaL, damping, clip amplitudes); a key is captured the second time it is seen
+        (the first run is eager and sizes the workspaces), and a new value simply captures a new graph."""
+        if not self._use_graphs:
+            self._device_work(grads, beta, do_update, do_apply, noise, V)
+            return
+        key = (kind, beta, do_update, do_apply, self.lr_params, self.lr_preconditioner, self.betaL, self.damping,
+               tuple(self.grad_clip_max_amps), tuple((g.dtype, tuple(g.shape)) for g in grads))
+        rec = self._graphs.get(key)
+        if rec is None and key not in self._seen:
+            self._seen.add(key)
+            self._device_work(grads, beta, do_update, do_apply, noise, V)
+            return
+        if rec is None:
+            rec = self._capture(key, grads, beta, do_update, do_apply, noise, V)
+        for s_g, g in zip(rec["grads"], grads):
+            s_g.copy_(g)
+        rec["graph"].replay()
+
+    def _capture(self, key, grads, beta, do_update, do_apply, noise, V):
+        dev = grads[0].device
+        static = [g.clone() for g in grads]
+        # the graph owns workspaces allocated during its capture (fixed addresses, never freed while it lives)
+        saved = (self._ws_upd, self._ws_app, self._ws_bal, self._lanes)
+        self._ws_upd, self._ws_app, self._ws_bal = L.Workspace(), L.Workspace(), L.Workspace()
+        if self._lanes is not None:
+            self._lanes = [_Lane(ln.stream, L.Workspace(), L.Workspace(), L.Workspace()) for ln in self._lanes]
+        lanes_used = self._lanes
+        torch.cuda.synchronize(dev)
+        g = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(g):
+                self._device_work(static, beta, do_update, do_apply, noise, V)
+            rec = {"graph": g, "grads": static, "ws": (self._ws_upd, self._ws_app, self._ws_bal, lanes_used)}
+        finally:
+            self._ws_upd, self._ws_app, self._ws_bal, self._lanes = saved
+        self._graphs[key] = rec
+        return rec
 
     @torch.no_grad()
     def step(self, closure):

@@ -193,6 +193,45 @@ def test_side_streams_bitwise_identical(hip, prec):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("first", [True, False])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_graph_replay_matches_eager(hip, prec, first):
+    """graphs=True replays captured HIP graphs of the step's device segments; every step must equal the eager
+    optimizer bit for bit. 16 steps: momentum's beta settles after 9 (new graph keys until then), the update coin
+    (p = 0.5) makes both the update and the apply-only segments replay, and balancing coins forced on steps 11 and
+    13 (on both optimizers) run between segments. Between replays the test synchronizes and compares on the
+    device (eager work of its own)."""
+    shapes = [(64, 96), (96, 64), (128, 128), (32,), (64, 96)]
+    opts, Ws = [], []
+    for graphs in (False, True):
+        W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
+        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=11,
+                         momentum=0.9, precision=prec, preconditioner_update_probability=0.5,
+                         update_preconditioner_first=first, graphs=graphs)
+        real = opt._draw_update
+
+        def forced(srcs, real=real, opt=opt):
+            noise, V, coins = real(srcs)
+            if opt._step_no in (11, 13):
+                coins = [True] + coins[1:]
+            return noise, V, coins
+        opt._draw_update = forced
+        opts.append(opt)
+        Ws.append(W)
+    for t in range(16):
+        gs = grads_for(shapes, t)
+        for opt in opts:
+            opt._step_no = t
+            opt.step_math([g.to(DEV) for g in gs])
+        torch.cuda.synchronize()
+        for a, b in zip(Ws[0], Ws[1]):
+            assert torch.equal(a, b), f"step {t}"
+        for i in range(len(shapes)):
+            for qa, qb in zip(opts[0].factors(i)[0], opts[1].factors(i)[0]):
+                assert torch.equal(qa, qb), f"step {t}, parameter {i}"
+    assert len(opts[1]._graphs) >= 2
+
+
 def test_step_closure_and_loss_curve(hip):
     """A least-squares model trained 100 steps through step(closure): the GPU optimizer (float32 model and
     gradients) and the float64 oracle (float64 model and gradients, same draws) give matching loss curves. The
