@@ -165,6 +165,25 @@ int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, voi
                        float* const* pre_out, float* const* clipped_out, void* ws, size_t* ws_bytes,
                        psgdk_stream_t stream);
 
+/* One dense factor update per problem given its term1 (full symmetric d x d fp32, or its upper triangle with
+ * term1_tri): ell = norm_lower_bound_spd(term1, V) + term2, L = max(betaL L + (1 - betaL) ell, ell) (L: one
+ * device float each, updated), Q_out = Q - lr/L (term1 Q - term2 Q), Q_out not aliasing Q. prec PSGDK_PREC_F32
+ * or _BF16 (MFMA inputs). Replaces the factor update of update_precond_kron_whiten_q0p5eq1p5 (psgd_pro.py:132-135,
+ * psgd_pro_fast.py:186-189). */
+int psgdk_factor_update(int prec, int64_t d, int nb, const float* const* term1, int term1_tri,
+                        const float* const* Q, float* const* Q_out, float* const* L, const float* const* V, float lr,
+                        float betaL, float term2, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* Q_out = procrustes_step2(Q) (psgd_pro.py:71-94; psgd_pro_fast.py:129-138): R = Q^T - Q normalized by
+ * norm_lower_bound_skh(R, V) + smallest normal, a = min(-tr(RQ)/tr(RRQ), 1/8) when tr(RRQ) < 0 else 1/8,
+ * Q_out = Q + a (RQ + a/2 RRQ), all on the device. Q_out must not alias Q (the reference updates in place). */
+int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out, const float* const* V,
+                     void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* apply_2d + clip + update (psgd_pro_fast.py:156-161,426-438): the same operation as psgdk_kron2d_apply. */
+int psgdk_apply2d(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params, float* const* pre_out,
+                  float* const* clipped_out, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
 /* P = Q^T Q (dense) or q * q (diagonal) for the factors selected by factor_mask (bit f = factor f):
  * gram_2d (psgd_pro_fast.py:164-165,191-192,447-449). tri bit 1: P written as its upper triangle. With bf16
  * shadows, Qt16 = bf16(Q^T) is rebuilt first and P16 written with P. */

@@ -778,6 +778,95 @@ int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const*
   return hip_check(clip_update_launch(a, st), "clip + update");
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Dense factor steps of the general engine, shared by psgdk_kron2d_update and the per-factor entry points.
+
+struct FacWs {
+  float *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
+  NlbWs nw;
+};
+
+void fac_take(Ws& w, int64_t d, int nb, FacWs& o) {
+  const int tp = gemm_tiles(d, d, 0);
+  for (int b = 0; b < nb; ++b) {
+    o.R[b] = w.take<float>(d * d);
+    o.RQ[b] = w.take<float>(d * d);
+    o.coef[b] = w.take<float>(4);
+    o.rs[b] = w.take<float>(4);
+    o.pc[b] = w.take<float>(4);
+    o.tpart[b] = w.take<float>(2 * (size_t)tp);
+  }
+  nlb_take(w, d, nb, o.nw);
+}
+
+// ell = nlb_spd(term1, V) + term2; L = max(betaL L + (1 - betaL) ell, ell); Qout = Q - lr/L (term1 Q - term2 Q)
+// (psgd_pro.py:132-135). term1: full symmetric, or its upper triangle when t1_tri. Qout must not alias Q.
+int factor_update_run(int prec, int nb, int64_t d, const float* const* T1, int t1_tri, const float* const* Q,
+                      float* const* Qout, float* const* Lv, const float* const* V, float lr, float betaL, float term2,
+                      const FacWs& w, hipStream_t st) {
+  {
+    NlbFinal fin;
+    std::memset(&fin, 0, sizeof fin);
+    fin.mode = NLB_FINAL_FACTOR; fin.lr = lr; fin.beta = betaL; fin.term2 = term2;
+    for (int b = 0; b < nb; ++b) { fin.L[b] = Lv[b]; fin.coef[b] = w.coef[b]; }
+    if (t1_tri) PSGDK_TRY(run_nlb(d, 1, nb, T1, d, false, V, fin, w.nw, st));
+    else PSGDK_TRY(run_nlb_full(d, 1, nb, reinterpret_cast<const void* const*>(T1), d, 0, V, fin, w.nw, st));
+  }
+  Opnd a, bq;
+  if (t1_tri) { a.mode = SYM; a.sign = 1; } else { a.mode = KC; }
+  a.ld = d;
+  bq.mode = MC; bq.ld = d;
+  EpiSpec e;
+  e.epi = EPI_FACTOR; e.ldx = d;
+  for (int b = 0; b < nb; ++b) { a.p[b] = T1[b]; bq.p[b] = Q[b]; e.X1[b] = Q[b]; e.s[b] = w.coef[b]; }
+  return run_gemm(prec, nb, d, d, d, a, bq, Qout, d, e, 0, 0, 0, 1, 0, st);
+}
+
+// Qout = procrustes_step2(Q) (psgd_pro.py:71-94): R = Q^T - Q, R /= nlb_skh(R, V) + sn, RQ = R Q, RRQ = R RQ,
+// a = min(-tr(RQ)/tr(RRQ), 1/8) if tr(RRQ) < 0 else 1/8, Qout = Q + a (RQ + a/2 RRQ). Qout must not alias Q.
+int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* const* Qout, const float* const* V,
+                   const FacWs& w, hipStream_t st) {
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
+    for (int b = 0; b < nb; ++b) { a.in[b] = Q[b]; a.out[b] = w.R[b]; }
+    PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
+  }
+  {
+    NlbFinal fin;
+    std::memset(&fin, 0, sizeof fin);
+    fin.mode = NLB_FINAL_SCALE;
+    for (int b = 0; b < nb; ++b) fin.coef[b] = w.rs[b];
+    const void* Rc[MAXB];
+    for (int b = 0; b < nb; ++b) Rc[b] = w.R[b];
+    PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 0, V, fin, w.nw, st));
+  }
+  {
+    Opnd a, bq;
+    a.mode = KC; a.ld = d;
+    bq.mode = MC; bq.ld = d;
+    EpiSpec e;
+    e.epi = EPI_RQ; e.ldx = d;
+    for (int b = 0; b < nb; ++b) { a.p[b] = w.R[b]; bq.p[b] = Q[b]; e.X1[b] = w.R[b]; e.s[b] = w.rs[b]; e.part[b] = w.tpart[b]; }
+    PSGDK_TRY(run_gemm(prec, nb, d, d, d, a, bq, w.RQ, d, e, 0, 0, 0, 1, 0, st));
+  }
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.i0 = gemm_tiles(d, d, 0); a.f0 = 0.125f;
+    for (int b = 0; b < nb; ++b) { a.in2[b] = w.tpart[b]; a.sc[b] = w.rs[b]; a.out[b] = w.pc[b]; }
+    PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
+  }
+  Opnd a, bq;
+  a.mode = KC; a.ld = d;
+  bq.mode = MC; bq.ld = d;
+  EpiSpec e;
+  e.epi = EPI_PROC; e.ldx = d;
+  for (int b = 0; b < nb; ++b) { a.p[b] = w.R[b]; bq.p[b] = w.RQ[b]; e.X1[b] = Q[b]; e.X2[b] = w.RQ[b]; e.s[b] = w.pc[b]; }
+  return run_gemm(prec, nb, d, d, d, a, bq, Qout, d, e, 0, 0, 0, 1, 0, st);
+}
+
 }  // namespace
 
 // ==============================================================================================================
@@ -1015,25 +1104,17 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
   const int64_t m = g->m, n = g->n, mn = m * n, dmx = dense_max(g);
   const int64_t dims[2] = {m, n};
   Ws w(ws);
-  float *X[MAXB], *Y[MAXB], *Pg[MAXB], *T1[MAXB], *Qn[MAXB], *R[MAXB], *RQ[MAXB];
-  float *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *dterm[MAXB];
-  const int tp = dmx ? gemm_tiles(dmx, dmx, 0) : 1;
+  float *X[MAXB], *Y[MAXB], *Pg[MAXB], *T1[MAXB], *Qn[MAXB], *dterm[MAXB];
   for (int b = 0; b < nb; ++b) {
     X[b] = w.take<float>(mn);
     Y[b] = w.take<float>(mn);
     Pg[b] = w.take<float>(mn);
     T1[b] = w.take<float>(dmx * dmx);
     Qn[b] = w.take<float>(dmx * dmx);
-    R[b] = w.take<float>(dmx * dmx);
-    RQ[b] = w.take<float>(dmx * dmx);
-    coef[b] = w.take<float>(4);
-    rs[b] = w.take<float>(4);
-    pc[b] = w.take<float>(4);
-    tpart[b] = w.take<float>(2 * (size_t)tp);
     dterm[b] = w.take<float>(std::max(m, n));
   }
-  NlbWs nw;
-  if (dmx) nlb_take(w, dmx, nb, nw);
+  FacWs fw;
+  if (dmx) fac_take(w, dmx, nb, fw);
   if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
   if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
   PSGDK_TRY(check_ptrs(noise, nb, "noise"));
@@ -1085,77 +1166,17 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
       PSGDK_TRY(run_gemm(g->prec, nb, d, d, other, a, a, T1, d, e, 1,
                          term_tri ? PSGDK_OUT_UPPER : PSGDK_OUT_MIRROR, 0, 1, 0, st));
     }
-    // ell = nlb(term1) + term2; L = max(beta L + (1 - beta) ell, ell)   (psgd_pro.py:132-134)
     const float* Vs[MAXB];
     const float* Vk[MAXB];
     for (int b = 0; b < nb; ++b) { Vs[b] = V[b] + voff; Vk[b] = V[b] + voff + NLB_K * d; }
     voff += 2 * NLB_K * d;
-    {
-      NlbFinal fin;
-      std::memset(&fin, 0, sizeof fin);
-      fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL; fin.term2 = term2;
-      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; }
-      const float* T1c[MAXB];
-      for (int b = 0; b < nb; ++b) T1c[b] = T1[b];
-      if (term_tri) PSGDK_TRY(run_nlb(d, 1, nb, T1c, d, false, Vs, fin, nw, st));
-      else PSGDK_TRY(run_nlb_full(d, 1, nb, reinterpret_cast<const void* const*>(T1c), d, 0, Vs, fin, nw, st));
-    }
-    // Qn = Q - lr/L (term1 Q - term2 Q)   (psgd_pro.py:135)
-    {
-      Opnd a, bq;
-      if (term_tri) { a.mode = SYM; a.sign = 1; } else { a.mode = KC; }
-      a.ld = d;
-      bq.mode = MC; bq.ld = d;
-      EpiSpec e;
-      e.epi = EPI_FACTOR; e.ldx = d;
-      for (int b = 0; b < nb; ++b) { a.p[b] = T1[b]; bq.p[b] = g->Q[f][b]; e.X1[b] = g->Q[f][b]; e.s[b] = coef[b]; }
-      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, Qn, d, e, 0, 0, 0, 1, 0, st));
-    }
-    // Procrustes step on Qn (psgd_pro.py:71-94): R = Qn^T - Qn, R /= nlb_skh(R) + sn, RQ = R Qn, RRQ = R RQ,
-    // a from the traces, Q = Qn + a (RQ + a/2 RRQ)
-    {
-      EwArgs a;
-      std::memset(&a, 0, sizeof a);
-      a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out[b] = R[b]; }
-      PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
-    }
-    {
-      NlbFinal fin;
-      std::memset(&fin, 0, sizeof fin);
-      fin.mode = NLB_FINAL_SCALE;
-      for (int b = 0; b < nb; ++b) fin.coef[b] = rs[b];
-      const void* Rc[MAXB];
-      for (int b = 0; b < nb; ++b) Rc[b] = R[b];
-      PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 0, Vk, fin, nw, st));
-    }
-    {
-      Opnd a, bq;
-      a.mode = KC; a.ld = d;
-      bq.mode = MC; bq.ld = d;
-      EpiSpec e;
-      e.epi = EPI_RQ; e.ldx = d;
-      for (int b = 0; b < nb; ++b) { a.p[b] = R[b]; bq.p[b] = Qn[b]; e.X1[b] = R[b]; e.s[b] = rs[b]; e.part[b] = tpart[b]; }
-      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, RQ, d, e, 0, 0, 0, 1, 0, st));
-    }
-    {
-      EwArgs a;
-      std::memset(&a, 0, sizeof a);
-      a.nb = nb; a.i0 = gemm_tiles(d, d, 0); a.f0 = 0.125f;
-      for (int b = 0; b < nb; ++b) { a.in2[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
-      PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
-    }
-    {
-      Opnd a, bq;
-      a.mode = KC; a.ld = d;
-      bq.mode = MC; bq.ld = d;
-      EpiSpec e;
-      e.epi = EPI_PROC; e.ldx = d;
-      for (int b = 0; b < nb; ++b) {
-        a.p[b] = R[b]; bq.p[b] = RQ[b]; e.X1[b] = Qn[b]; e.X2[b] = RQ[b]; e.s[b] = pc[b];
-      }
-      PSGDK_TRY(run_gemm(g->prec, nb, d, d, d, a, bq, g->Q[f], d, e, 0, 0, 0, 1, 0, st));
-    }
+    // Qn = Q - lr/L (term1 Q - term2 Q) with L's EMA (psgd_pro.py:132-135), then the Procrustes step on Qn into Q
+    const float* T1c[MAXB];
+    const float* Qc[MAXB];
+    const float* Qnc[MAXB];
+    for (int b = 0; b < nb; ++b) { T1c[b] = T1[b]; Qc[b] = g->Q[f][b]; Qnc[b] = Qn[b]; }
+    PSGDK_TRY(factor_update_run(g->prec, nb, d, T1c, term_tri, Qc, Qn, g->L[f], Vs, o->lr, o->betaL, term2, fw, st));
+    PSGDK_TRY(procrustes_run(g->prec, nb, d, Qnc, g->Q[f], Vk, fw, st));
   }
   // P refresh (psgd_pro_fast.py:191-192)
   int sel[MAXB];
@@ -1199,6 +1220,53 @@ int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, voi
     a.out2[b] = clipped_out ? clipped_out[b] : nullptr;
   }
   return hip_check(clip_update_launch(a, st), "clip + update");
+}
+
+int psgdk_factor_update(int prec, int64_t d, int nb, const float* const* term1, int term1_tri,
+                        const float* const* Q, float* const* Q_out, float* const* L, const float* const* V, float lr,
+                        float betaL, float term2, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(d, "d"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  Ws w(ws);
+  FacWs fw;
+  fac_take(w, d, nb, fw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(term1, nb, "term1"));
+  PSGDK_TRY(check_ptrs(Q, nb, "Q"));
+  PSGDK_TRY(check_ptrs(Q_out, nb, "Q_out"));
+  PSGDK_TRY(check_ptrs(L, nb, "L"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  for (int b = 0; b < nb; ++b)
+    if (Q_out[b] == Q[b]) return fail(PSGDK_EINVAL, "Q_out[%d] aliases Q[%d]", b, b);
+  return factor_update_run(prec, nb, d, term1, term1_tri ? 1 : 0, Q, Q_out, L, V, lr, betaL, term2, fw,
+                           (hipStream_t)stream);
+}
+
+int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out, const float* const* V,
+                     void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(d, "d"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  Ws w(ws);
+  FacWs fw;
+  fac_take(w, d, nb, fw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(Q, nb, "Q"));
+  PSGDK_TRY(check_ptrs(Q_out, nb, "Q_out"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  for (int b = 0; b < nb; ++b)
+    if (Q_out[b] == Q[b]) return fail(PSGDK_EINVAL, "Q_out[%d] aliases Q[%d]", b, b);
+  return procrustes_run(prec, nb, d, Q, Q_out, V, fw, (hipStream_t)stream);
+}
+
+int psgdk_apply2d(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params, float* const* pre_out,
+                  float* const* clipped_out, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  return psgdk_kron2d_apply(g, o, params, pre_out, clipped_out, ws, ws_bytes, stream);
 }
 
 int psgdk_kron2d_refresh_p(const psgdk_kron2d_t* g, int factor_mask, int tri, psgdk_stream_t stream) {

@@ -248,6 +248,53 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, target):
         assert g <= top * (1 + rel)
 
 
+@pytest.mark.parametrize("d,tri", [(64, 0), (130, 0), (256, 0), (130, 1)])
+@pytest.mark.parametrize("L0", [0.0, 7.5])
+def test_factor_update_matches_oracle(hip, d, tri, L0):
+    """psgdk_factor_update (psgd_pro.py:132-135) for two problems against the float64 formula with the oracle's
+    norm bound on the same V: Q_out rel 1e-5 normwise, L rel 1e-5. term1 full, or its upper triangle (tri)."""
+    from oracle.psgd_oracle import norm_lower_bound
+    lr, betaL, term2 = 0.1, 0.9, 3.0
+    T1s, Qs, Vs = [], [], []
+    for b in range(2):
+        X = rnd(d, d // 2 + 3, seed=d + b)
+        T1s.append(X @ X.T)
+        Qs.append(torch.eye(d) + 0.1 * rnd(d, d, seed=d + 10 + b))
+        Vs.append(rnd(32, d, seed=d + 20 + b))
+    T1d = [(poison_lower(t) if tri else t).to(DEV) for t in T1s]
+    Qd = [q.to(DEV) for q in Qs]
+    Qo = [torch.empty_like(q) for q in Qd]
+    Ld = [torch.full((1,), L0, device=DEV) for _ in range(2)]
+    Vd = [v.to(DEV) for v in Vs]
+    L.call_ws(L.lib().psgdk_factor_update, 0, d, 2, L.ptrs(T1d), tri, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Ld),
+              L.ptrs(Vd), lr, betaL, term2, ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+    for b in range(2):
+        T, Q = T1s[b].double(), Qs[b].double()
+        ell = float(norm_lower_bound(T, Vs[b].double(), skew=False)) + term2
+        Lr = max(betaL * L0 + (1 - betaL) * ell, ell)
+        ref = Q - lr / Lr * (T @ Q - term2 * Q)
+        assert float(Ld[b]) == pytest.approx(Lr, rel=1e-5)
+        assert rel_err_norm(Qo[b], ref) < 1e-5
+
+
+@pytest.mark.parametrize("d", [64, 130, 256])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_procrustes_matches_oracle(hip, d, prec):
+    """psgdk_procrustes against the oracle's procrustes_step2 (psgd_pro.py:71-94) in float64 on the same V (for
+    bf16 MFMA inputs, on the bf16-rounded Q): rel 1e-5 normwise for fp32, 5e-3 for bf16."""
+    from oracle.psgd_oracle import procrustes_step2
+    Qs = [torch.eye(d) + 0.05 * rnd(d, d, seed=d + b) for b in range(2)]
+    Vs = [rnd(32, d, seed=d + 5 + b) for b in range(2)]
+    Qd = [q.to(DEV) for q in Qs]
+    Qo = [torch.empty_like(q) for q in Qd]
+    L.call_ws(L.lib().psgdk_procrustes, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs([v.to(DEV) for v in Vs]),
+              ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+    for b in range(2):
+        ref = Qs[b].double().clone()
+        procrustes_step2(ref, Vs[b].double())
+        assert rel_err_norm(Qo[b], ref) < (1e-5 if prec == 0 else 5e-3)
+
+
 def test_hip_ops_plugin_methods(hip):
     """The ops class methods (psgd_pro_fast.EagerOps interface) against their eager definitions."""
     ops = K.make_ops(())

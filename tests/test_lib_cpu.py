@@ -64,6 +64,26 @@ def test_argument_validation():
     assert lib.psgdk_symm(0, 0, 3, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
 
 
+def test_factor_step_entry_points_reject_aliasing_without_device_work():
+    """psgdk_factor_update / psgdk_procrustes write Q_out from Q in one pass, so Q_out may not alias Q: refused
+    after the size query and before any launch (fake device addresses are never touched)."""
+    lib = L.lib()
+    sz = C.c_size_t(0)
+    assert lib.psgdk_procrustes(0, 256, 2, None, None, None, None, C.byref(sz), None) == L.OK and sz.value > 0
+    ws = C.c_void_p(0x100000)
+    q, other = L.ptrs([0x2000, 0x3000]), L.ptrs([0x4000, 0x5000])
+    big = C.c_size_t(sz.value)
+    assert lib.psgdk_procrustes(0, 256, 2, q, q, other, ws, C.byref(big), None) == L.EINVAL
+    assert "alias" in _err()
+    assert lib.psgdk_factor_update(0, 256, 2, None, 0, None, None, None, None, 0.1, 0.9, 1.0, None, C.byref(sz),
+                                   None) == L.OK
+    big = C.c_size_t(sz.value)
+    assert lib.psgdk_factor_update(0, 256, 2, other, 0, q, q, other, other, 0.1, 0.9, 1.0, ws, C.byref(big),
+                                   None) == L.EINVAL
+    assert "alias" in _err()
+    assert lib.psgdk_procrustes(3, 256, 2, q, other, other, ws, C.byref(big), None) == L.EINVAL
+
+
 def test_workspace_queries_need_no_device():
     lib = L.lib()
     sz = C.c_size_t(0)
