@@ -219,7 +219,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
 
 /* Tuning switches (process-wide): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
  * XCD, 2 = 1 with tile rows grouped by 4 so that the tiles an XCD runs at once share operand panels; default 2);
- * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256, 1 = 128 x 128); option 2 = workgroups
+ * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256 on 8 waves, 1 = 128 x 128, 2 = 256 x 256 on 4
+ * waves; other values are refused); option 2 = workgroups
  * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of that
  * kernel (2, 4 or 8; default 4). */
 int psgdk_set_option(int option, int value);

@@ -1351,7 +1351,11 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
 
 int psgdk_set_option(int option, int value) {
   if (option == 0) { g_tile_order = value; return PSGDK_OK; }
-  if (option == 1) { g_force_cfg = value; return PSGDK_OK; }
+  if (option == 1) {
+    if (value < -1 || value > 2) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 2");
+    g_force_cfg = value;
+    return PSGDK_OK;
+  }
   if (option == 2) {
     if (value < 1) return fail(PSGDK_EINVAL, "option 2 (V A workgroup target) must be >= 1");
     g_nlb_target = value;
