@@ -221,8 +221,10 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * XCD, 2 = 1 with tile rows grouped by 4 so that the tiles an XCD runs at once share operand panels; default 2);
  * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256 on 8 waves, 1 = 128 x 128, 2 = 256 x 256 on 4
  * waves; other values are refused); option 2 = workgroups
- * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of that
- * kernel (2, 4 or 8; default 4). */
+ * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of the V A
+ * kernels (2, 4 or 8; default 4; the column-block kernel takes 2 or 4); option 4 = the V A kernel of full-storage
+ * norm bounds (-1 by shape, 0 split-K products plus a reduce kernel, 1 one workgroup per 64 output columns over the
+ * whole k range; shapes the column kernel cannot read take the split-K kernel). */
 int psgdk_set_option(int option, int value);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,

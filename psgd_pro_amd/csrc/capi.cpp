@@ -202,6 +202,7 @@ int g_tile_order = 2;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous 
 int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's tile config
 int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
 int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
+int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape, 0 split-K + reduce, 1 column blocks
 
 int b16_cfg(int64_t M, int64_t N, int tri, int nb) {
   if (g_force_cfg >= 0) return g_force_cfg;
@@ -359,14 +360,26 @@ int run_nlb(int64_t n, int sign, int nb, const float* const* A, int64_t lda, boo
 
 // Norm lower bound of fully stored matrices (fp32 or bf16): row norms, init, 4 V A products with folded scaling,
 // final. 7 launches.
+// The column-block V A kernel needs the 16-byte operand layout (n and the row stride multiples of 16 bytes,
+// 16-byte aligned matrices and V buffers, each matrix < 2 GiB).
+bool vmm_cols_ok(int64_t n, int nb, const void* const* A, int64_t lda, int esz, const NlbWs& w) {
+  const int64_t ach = 16 / esz;
+  if (n % ach || lda % ach || n * lda * esz >= ((int64_t)1 << 31) || NLB_K * n * esz >= ((int64_t)1 << 31)) return false;
+  for (int b = 0; b < nb; ++b)
+    if (!aligned16(A[b]) || !aligned16(w.vb0[b]) || !aligned16(w.vb1[b])) return false;
+  return true;
+}
+
 int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_bf16, const float* const* V,
                  const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
   const float* Af[MAXB];
   for (int b = 0; b < nb; ++b) Af[b] = reinterpret_cast<const float*>(A[b]);
   NlbArgs a = nlb_args(n, sign, nb, Af, lda, w);
-  a.ssc = 128;
   nlb_full_plan(n, nb, w.part_cols, a.ksplit, a.kslice);
   a.vmm_u = g_vmm_u;
+  a.vmm_cols = g_vmm_cols != 0 && vmm_cols_ok(n, nb, A, lda, a_bf16 ? 2 : 4, w);
+  a.ssc = a.vmm_cols ? 64 : 128;
+  if (a.vmm_cols && a.vmm_u == 8) a.vmm_u = 4;
   PSGDK_HIP(nlb_full_launch(a, 0, a_bf16, 0, st), "row norms");
   for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
   PSGDK_HIP(nlb_full_launch(a, 1, a_bf16, 0, st), "nlb init");
@@ -1364,6 +1377,11 @@ int psgdk_set_option(int option, int value) {
   if (option == 3) {
     if (value != 2 && value != 4 && value != 8) return fail(PSGDK_EINVAL, "option 3 (V A load batch) must be 2, 4 or 8");
     g_vmm_u = value;
+    return PSGDK_OK;
+  }
+  if (option == 4) {
+    if (value < -1 || value > 1) return fail(PSGDK_EINVAL, "option 4 (V A kernel) must be -1, 0 or 1");
+    g_vmm_cols = value;
     return PSGDK_OK;
   }
   return fail(PSGDK_EINVAL, "unknown option %d", option);

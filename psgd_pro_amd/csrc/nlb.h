@@ -16,6 +16,8 @@ struct NlbArgs {
   int vmm_u;                // full path: MFMA steps per load batch of the V A kernel (2, 4 or 8)
   int ksplit, kslice;       // full path: k slices per V A product and their length (a multiple of 64); part holds
                             // ksplit x 32 x n partial products
+  int vmm_cols;             // full path: 1 = one workgroup per 64 output columns over the whole k range (no
+                            // partials, ssc = 64); 0 = split-K products plus a reduce kernel (ssc = 128)
   long long lda;
   const float* A[MAXB];     // n x n, upper triangle read
   const float* Vin[MAXB];   // init: the random start (32 x n)

@@ -281,9 +281,38 @@ __global__ void __launch_bounds__(256) rownorm_full_kernel(const NlbArgs p) {
   }
 }
 
+// Eight consecutive elements of T at a 16-byte aligned address, as floats.
+__device__ __forceinline__ void load8(const bf16_t* src, float (&x)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(src);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = __uint_as_float(w[e] << 16);
+    x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(src)[0], c = reinterpret_cast<const float4*>(src)[1];
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+}
+__device__ __forceinline__ void store8(bf16_t* dst, const float (&x)[8]) {
+  uint4 u;
+  u.x = pack2(f32_to_bf16(x[0]), f32_to_bf16(x[1]));
+  u.y = pack2(f32_to_bf16(x[2]), f32_to_bf16(x[3]));
+  u.z = pack2(f32_to_bf16(x[4]), f32_to_bf16(x[5]));
+  u.w = pack2(f32_to_bf16(x[6]), f32_to_bf16(x[7]));
+  *reinterpret_cast<uint4*>(dst) = u;
+}
+__device__ __forceinline__ void store8(float* dst, const float (&x)[8]) {
+  reinterpret_cast<float4*>(dst)[0] = make_float4(x[0], x[1], x[2], x[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4(x[4], x[5], x[6], x[7]);
+}
+
 // One workgroup per (matrix, row r of V): argmax of rn2 (first maximum), nf = max diagonal (SPD) or max |A|
 // (skew) + smallest normal, then V0[r] = a_j + sgn(<a_j, V_r>) V_r with a_j = row j of A / nf (psgd_pro.py:25-33,
-// :49-57). Workgroup r = 0 also publishes nf and j.
+// :49-57). Workgroup r = 0 also publishes nf and j. The scans read 4 (statistics) or 8 (rows) elements per thread
+// and step with the loads of several steps in flight; the rows take the element path unless n % 8 == 0, A's row
+// stride is a multiple of 16 bytes and the bases are 16-byte aligned.
 template <typename T>
 __global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
   __shared__ float red[4];
@@ -294,13 +323,31 @@ __global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
   const int b = blockIdx.x / NLB_K, r = blockIdx.x % NLB_K;
   const int tid = threadIdx.x, n = p.n;
   const float* __restrict__ rn2 = p.rn2[b];
+  const float* __restrict__ rmax = p.rpart[b];
+  const float* __restrict__ diag = p.cpart[b];
   float best = -1.f, am = 0.f, dm = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < n; i += 256) {
-    const float s = rn2[i];
-    if (s > best) { best = s; bi = i; }
-    am = fmaxf(am, p.rpart[b][i]);
-    dm = fmaxf(dm, p.cpart[b][i]);
+  if ((n & 3) == 0) {  // workspace arrays: 256-byte aligned bases
+    const int n4 = n >> 2;
+#pragma unroll 4
+    for (int i = tid; i < n4; i += 256) {
+      const float4 s = reinterpret_cast<const float4*>(rn2)[i];
+      const float4 a = reinterpret_cast<const float4*>(rmax)[i];
+      const float4 c = reinterpret_cast<const float4*>(diag)[i];
+      const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (sv[e] > best) { best = sv[e]; bi = 4 * i + e; }  // indices increase: first maximum per thread
+      am = fmaxf(am, fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)));
+      dm = fmaxf(dm, fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)));
+    }
+  } else {
+    for (int i = tid; i < n; i += 256) {
+      const float s = rn2[i];
+      if (s > best) { best = s; bi = i; }
+      am = fmaxf(am, rmax[i]);
+      dm = fmaxf(dm, diag[i]);
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o, 64);
@@ -329,12 +376,38 @@ __global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
   const float nf = snf;
   const float* __restrict__ vr = p.Vin[b] + (long long)r * n;
   T* __restrict__ v0 = reinterpret_cast<T*>(p.Vout[b]) + (long long)r * n;
+  const bool vec = (n & 7) == 0 && (p.lda * (long long)sizeof(T)) % 16 == 0 &&
+                   (reinterpret_cast<uintptr_t>(p.A[b]) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.Vin[b]) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(p.Vout[b]) & 15) == 0;
+  auto aval = [&](float a, int k) { return (p.sign < 0 && k == j ? 0.f : a) / nf; };
   float d = 0.f;
-  for (int k = tid; k < n; k += 256) d += (p.sign < 0 && k == j ? 0.f : to_f32<T>(arow[k])) / nf * vr[k];
+  if (vec) {
+#pragma unroll 2
+    for (int c = tid; c < (n >> 3); c += 256) {
+      float a[8], v[8];
+      load8(arow + 8 * c, a);
+      load8(vr + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d += aval(a[e], 8 * c + e) * v[e];
+    }
+  } else {
+    for (int k = tid; k < n; k += 256) d += aval(to_f32<T>(arow[k]), k) * vr[k];
+  }
   d = block_sum(d, red);
   const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
-  for (int k = tid; k < n; k += 256)
-    v0[k] = from_f32<T>((p.sign < 0 && k == j ? 0.f : to_f32<T>(arow[k])) / nf + sg * vr[k]);
+  if (vec) {
+#pragma unroll 2
+    for (int c = tid; c < (n >> 3); c += 256) {
+      float a[8], v[8];
+      load8(arow + 8 * c, a);
+      load8(vr + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = aval(a[e], 8 * c + e) + sg * v[e];
+      store8(v0 + 8 * c, a);
+    }
+  } else {
+    for (int k = tid; k < n; k += 256) v0[k] = from_f32<T>(aval(to_f32<T>(arow[k]), k) + sg * vr[k]);
+  }
 }
 
 // W = V A^T * (1 / nf) * (normalize ? 1 / (|V_r| + smallest normal) : 1) for symmetric or skew A read in full;
@@ -572,6 +645,129 @@ __global__ void __launch_bounds__(256) vmm_reduce_kernel(const NlbArgs p, int no
   }
 }
 
+// W = V A^T * row scale (the product of vmm_full_kernel) with one workgroup per 64 output columns of one matrix
+// over the whole k range, so that no partial products leave the workgroup and no reduce kernel follows. Wave w
+// multiplies the k quarter [w kq, (w + 1) kq) for all 32 x 64 outputs (2 x 4 MFMA tiles of 16 x 16, each V
+// fragment used by four A fragments); the four partial blocks are summed through LDS in the fixed order w = 0..3.
+// Operands come from 16-byte buffer loads straight into MFMA fragments, U steps issued together (the 16-byte layout
+// is required: n and the row stride multiples of 16 bytes, aligned bases, each matrix < 2 GiB; the host checks).
+// Epilogue: thread t owns row t / 8 and 8 consecutive columns: W in T (one 16- or 32-byte store) and
+// ssout[r][cb] = sum over the block's columns of W[r][c]^2, reduced over the row's 8 lanes in a fixed tree.
+// grid: nb * ceil(n / 64).
+constexpr int VMC = 64;     // output columns per workgroup
+constexpr int VMC_LD = 68;  // LDS row stride (floats) of the partial blocks
+
+template <typename T, int U>
+__global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int normalize) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int ACH = 16 / sizeof(T);  // elements per 16-byte piece
+  constexpr int KS = 4 * ACH;          // k per MFMA step: lane group g holds pieces at k + g ACH
+  __shared__ float rs[NLB_K];
+  __shared__ __attribute__((aligned(16))) float red[4][NLB_K][VMC_LD];
+  const int n = p.n, nbk = (n + VMC - 1) / VMC;
+  const int b = blockIdx.x / nbk, cb = blockIdx.x % nbk;
+  // the wave index sets the k range, hence the loads' scalar offset: readfirstlane makes it provably uniform
+  // (otherwise every load becomes a waterfall loop)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int c0 = cb * VMC;
+  const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
+  const T* __restrict__ V = reinterpret_cast<const T*>(p.Vin[b]);
+  if (tid < NLB_K) rs[tid] = vmm_row_scale(p, b, tid, nbk, normalize);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * n * sizeof(T));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * sizeof(T));
+  int vo[2], ao[4];  // byte offsets of this lane's pieces at k = 0 (kOob: a column past n reads zero)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * n + g * ACH) * (int)sizeof(T);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = c0 + j * 16 + r16;
+    ao[j] = c < n ? (int)(((long long)c * p.lda + g * ACH) * sizeof(T)) : kOob;
+  }
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int kq = ((n + 3) / 4 + KS - 1) / KS * KS;
+  const int kbeg = wave * kq, kend = min(n, kbeg + kq);
+  for (int k0 = kbeg; k0 < kend; k0 += U * KS) {
+    uint4 vf[U][2], af[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k0 + u * KS, so = kk * (int)sizeof(T);
+      const bool in = kk + g * ACH < kend;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        vf[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, in ? vo[i] : kOob, so, 0));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        af[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, in ? ao[j] : kOob, so, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep all U steps' loads ahead of the first MFMA
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if constexpr (BF) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vf[u][i]),
+                                                                __builtin_bit_cast(bf16x8_t, af[u][j]), acc[i][j], 0, 0, 0);
+      } else {  // element s of every lane's piece: k = kk + 4 g + s, the same map for both operands
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float((&vf[u][i].x)[s4]),
+                                                               __uint_as_float((&af[u][j].x)[s4]), acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+  // lane holds rows i*16 + 4g + e of columns j*16 + r16
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave][i * 16 + 4 * g + e][j * 16 + r16] = acc[i][j][e];
+  __syncthreads();
+  const int row = tid >> 3, cl = (tid & 7) * 8, col = c0 + cl;
+  float w[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4 x0 = *reinterpret_cast<const float4*>(&red[0][row][cl + 4 * h]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&red[1][row][cl + 4 * h]);
+    const float4 x2 = *reinterpret_cast<const float4*>(&red[2][row][cl + 4 * h]);
+    const float4 x3 = *reinterpret_cast<const float4*>(&red[3][row][cl + 4 * h]);
+    w[4 * h + 0] = ((x0.x + x1.x) + x2.x) + x3.x;
+    w[4 * h + 1] = ((x0.y + x1.y) + x2.y) + x3.y;
+    w[4 * h + 2] = ((x0.z + x1.z) + x2.z) + x3.z;
+    w[4 * h + 3] = ((x0.w + x1.w) + x2.w) + x3.w;
+  }
+  const float sc = rs[row];
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    w[e] *= sc;
+    if (col + e < n) sq += w[e] * w[e];
+  }
+  T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
+  if (col + 8 <= n) {
+    store8(W, w);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (col + e < n) W[e] = from_f32<T>(w[e]);
+  }
+  sq += __shfl_xor(sq, 1, 64);
+  sq += __shfl_xor(sq, 2, 64);
+  sq += __shfl_xor(sq, 4, 64);
+  if ((tid & 7) == 0) p.ssout[b][row * nbk + cb] = sq;
+}
+
 hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st) {
   if (stage == 0) {
     const int nrb = (a.n + 3) / 4;
@@ -580,6 +776,15 @@ hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normaliz
   } else if (stage == 1) {
     if (a_bf16) hipLaunchKernelGGL(nlb_init_full_kernel<bf16_t>, dim3(a.nb * NLB_K), dim3(256), 0, st, a);
     else hipLaunchKernelGGL(nlb_init_full_kernel<float>, dim3(a.nb * NLB_K), dim3(256), 0, st, a);
+  } else if (a.vmm_cols) {
+    const dim3 grid(((a.n + VMC - 1) / VMC) * a.nb);
+    if (a_bf16) {
+      if (a.vmm_u == 2) hipLaunchKernelGGL((vmm_cols_kernel<bf16_t, 2>), grid, dim3(256), 0, st, a, normalize);
+      else hipLaunchKernelGGL((vmm_cols_kernel<bf16_t, 4>), grid, dim3(256), 0, st, a, normalize);
+    } else {
+      if (a.vmm_u == 2) hipLaunchKernelGGL((vmm_cols_kernel<float, 2>), grid, dim3(256), 0, st, a, normalize);
+      else hipLaunchKernelGGL((vmm_cols_kernel<float, 4>), grid, dim3(256), 0, st, a, normalize);
+    }
   } else {
     const int nbk = (a.n + VMM_C - 1) / VMM_C;
     if (a.ksplit < 1 || a.ksplit > VMM_MAXS || a.kslice % 64 != 0 || (long long)a.ksplit * a.kslice < a.n)

@@ -218,12 +218,15 @@ def nlb_full(As, Vs, sign):
                                    (3072, 0)])
 @pytest.mark.parametrize("sign", [1, -1])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("target", [1, 1024, 1 << 20])
-def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, target):
+@pytest.mark.parametrize("cols,target", [(1, 1024), (0, 1), (0, 1024), (0, 1 << 20)],
+                         ids=["cols", "split1", "split1024", "splitmax"])
+def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, target):
     """Full-storage bound (psgd_pro.py:19-65) of two matrices in one call, against the float64 oracle on the same
-    (storage-rounded) matrices. target sets the split-K workgroup target: 1 gives one k slice, 2^20 the most
-    slices, 1024 the default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load
-    path). fp32: rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
+    (storage-rounded) matrices. cols = 1: the column-block V A kernel where the layout allows it (n and lda
+    multiples of 16 bytes: fp32 n = 100 with a ragged last block, 768, 1000, 3072), else the split-K kernel;
+    cols = 0: the split-K kernel, whose workgroup target 1 gives one k slice, 2^20 the most slices, 1024 the
+    default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path). fp32:
+    rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
     from oracle.psgd_oracle import norm_lower_bound
     S = _nlb_case(n, sign)
     S2 = 0.5 * S.flip(0).flip(1)  # another matrix of the same kind
@@ -236,16 +239,42 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, target):
         dev_mats.append(buf.to(DEV)[:, :n])
     lib = L.lib()
     assert lib.psgdk_set_option(2, target) == 0
+    assert lib.psgdk_set_option(4, -1 if cols else 0) == 0
     try:
         got = nlb_full(dev_mats, [v.to(DEV) for v in Vs], sign)
+        again = nlb_full(dev_mats, [v.to(DEV) for v in Vs], sign)
     finally:
         lib.psgdk_set_option(2, 1024)
+        lib.psgdk_set_option(4, -1)
+    assert got == again  # fixed reduction orders: bitwise repeatable
     rel = 1e-5 if dtype == torch.float32 else 2e-2
     for M, V, g in zip(mats, Vs, got):
         ref = float(norm_lower_bound(M.double(), V.double(), skew=sign < 0))
         assert g == pytest.approx(ref, rel=rel, abs=1e-30)
         top = float(torch.linalg.matrix_norm(M.double(), 2))
         assert g <= top * (1 + rel)
+
+
+@pytest.mark.parametrize("cols", [1, 0], ids=["cols", "split"])
+def test_norm_lower_bound_full_sixteen_matrices(hip, cols):
+    """A full group (16 matrices, the most one call takes) of 320 x 320 bf16 SPD matrices of different scales:
+    every matrix's bound against the float64 oracle (rel 2e-2), both V A kernels."""
+    from oracle.psgd_oracle import norm_lower_bound
+    n = 320
+    mats, Vs = [], []
+    for b in range(16):
+        X = rnd(n, 40 + 8 * b, seed=100 + b)
+        mats.append(((0.5 + b) * (X @ X.T)).to(torch.bfloat16))
+        Vs.append(rnd(32, n, seed=200 + b))
+    lib = L.lib()
+    assert lib.psgdk_set_option(4, -1 if cols else 0) == 0
+    try:
+        got = nlb_full([M.to(DEV) for M in mats], [v.to(DEV) for v in Vs], 1)
+    finally:
+        lib.psgdk_set_option(4, -1)
+    for M, V, g in zip(mats, Vs, got):
+        ref = float(norm_lower_bound(M.double(), V.double(), skew=False))
+        assert g == pytest.approx(ref, rel=2e-2)
 
 
 @pytest.mark.parametrize("d,tri", [(64, 0), (130, 0), (256, 0), (130, 1)])
