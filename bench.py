@@ -45,6 +45,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
+    ap.add_argument("--r2", type=int, default=0,
+                    help="1: the Procrustes step in the reference's r2 form (KronWhiten(r2=True), 3 d^3 instead of 4 d^3)")
     return ap.parse_args()
 
 
@@ -136,8 +138,8 @@ def bench_vitb(args):
     grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
     opt = KronWhiten(params, preconditioner_max_size=8192, preconditioner_max_skew=skew,
                      preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0,
-                     streams=args.streams, graphs=bool(args.graphs))
-    flops_step = sum(flops_2d(m, n, is_dense(m, m * n, 8192, skew), is_dense(n, m * n, 8192, skew))
+                     streams=args.streams, graphs=bool(args.graphs), r2=bool(args.r2))
+    flops_step = sum(flops_2d(m, n, is_dense(m, m * n, 8192, skew), is_dense(n, m * n, 8192, skew), r2=bool(args.r2))
                      for m, n in shapes)
     for _ in range(args.warmup):
         opt.step_math(grads)
@@ -192,7 +194,8 @@ def bench_vitb(args):
         "data": "synthetic",
         "config": {"workload": "vit-b16-kron-update-apply", "weights": "12 x {768x2304, 768x768, 768x3072, 3072x768}",
                    "blocks": args.blocks, "grad_dtype": "bf16", "factor_dtype": "fp32", "max_size": 8192,
-                   "max_skew": args.skew, "update_probability": 1.0, "parallelism": "none"},
+                   "max_skew": args.skew, "update_probability": 1.0, "procrustes": "r2" if args.r2 else "step2",
+                   "parallelism": "none"},
         "gpu_ms_per_step": round(ev_ms, 3),
         "streams": args.streams,
         "graphs": bool(args.graphs),

@@ -138,7 +138,7 @@ typedef struct psgdk_update_opts {
   float damping;
   float grad_eps; /* eps of the damping scale (torch.finfo(gradient dtype).eps in the reference) */
   int32_t tri;    /* bit 0: term1 kept as its upper triangle; bit 1: P kept as its upper triangle */
-  int32_t r2;     /* reserved: 0 (procrustes_step2 form) */
+  int32_t r2;     /* 0: procrustes_step2 (psgd_pro.py:71-94); 1: procrustes_step_r2 (psgd_pro_fast.py:141-153) */
 } psgdk_update_opts_t;
 
 typedef struct psgdk_apply_opts {
@@ -179,6 +179,12 @@ int psgdk_factor_update(int prec, int64_t d, int nb, const float* const* term1, 
  * Q_out = Q + a (RQ + a/2 RRQ), all on the device. Q_out must not alias Q (the reference updates in place). */
 int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out, const float* const* V,
                      void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
+/* Q_out = procrustes_step_r2(Q) (psgd_pro_fast.py:141-153): the same rotation with R R formed once by a symmetric
+ * rank-d product (3 d^3 flops instead of 4 d^3): Rn = Q - Q^T normalized by its skew norm bound, S = Rn^T Rn,
+ * tr(RQ) = sum(Rn * Q), tr(RRQ) = -sum(S * Q), Q_out = Q - (a Rn + a^2/2 S) Q. Arguments as psgdk_procrustes. */
+int psgdk_procrustes_r2(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out,
+                        const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
 
 /* apply_2d + clip + update (psgd_pro_fast.py:156-161,426-438): the same operation as psgdk_kron2d_apply. */
 int psgdk_apply2d(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params, float* const* pre_out,

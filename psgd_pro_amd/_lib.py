@@ -68,6 +68,7 @@ _SIGS = {
     "psgdk_factor_update": (_i32, [_i32, _i64, _i32, _vpa, _i32, _vpa, _vpa, _vpa, _vpa, C.c_float, C.c_float,
                                    C.c_float, _vp, _szp, _vp]),
     "psgdk_procrustes": (_i32, [_i32, _i64, _i32, _vpa, _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_procrustes_r2": (_i32, [_i32, _i64, _i32, _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_kron2d_refresh_p": (_i32, [C.POINTER(Kron2d), _i32, _i32, _vp]),
     "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
     "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),

@@ -257,6 +257,12 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
 // ------------------------------------------------------------------------------------------------------------
 // Norm lower bound pipeline (see nlb.hip). full = the matrix is stored in full (read by contiguous loads);
 // otherwise only its upper triangle is read.
+// tile pairs of rform (64 x 64 tiles, I <= J): its trace partials
+int64_t rform_pairs(int64_t d) {
+  const int64_t T = (d + 63) / 64;
+  return T * (T + 1) / 2;
+}
+
 struct NlbWs {
   float *vb0[MAXB], *vb1[MAXB], *part[MAXB], *ss0[MAXB], *ss1[MAXB];
   float *rpart[MAXB], *cpart[MAXB], *tmax[MAXB], *dmax[MAXB], *rn2[MAXB], *scal[MAXB];
@@ -593,7 +599,7 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
   const int64_t dims[2] = {m, n};
   Ws w(ws);
   bf16_t *Xb[MAXB], *YTb[MAXB], *Pgb[MAXB], *PgTb[MAXB], *T1b[MAXB], *QnTb[MAXB], *Rb[MAXB], *RQTb[MAXB];
-  float *Qn[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
+  float *Qn[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *rtp[MAXB];
   const int tp = gemm_bf16_tiles(dmx, dmx, 0, 1);
   for (int b = 0; b < nb; ++b) {
     Xb[b] = w.take<bf16_t>(mn);
@@ -608,8 +614,9 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
     RQ[b] = w.take<float>(dmx * dmx);
     coef[b] = w.take<float>(4);
     rs[b] = w.take<float>(4);
-    pc[b] = w.take<float>(4);
+    pc[b] = w.take<float>(8);
     tpart[b] = w.take<float>(2 * (size_t)tp);
+    rtp[b] = w.take<float>(rform_pairs(dmx));
   }
   NlbWs nw;
   nlb_take(w, dmx, nb, nw);
@@ -672,11 +679,11 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
-    {  // R = Qn^T - Qn -> bf16
+    {  // R = Qn^T - Qn -> bf16 (r2: and the partials of sum R * Qn)
       EwArgs a;
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out2[b] = Rb[b]; }
+      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out2[b] = Rb[b]; a.sc[b] = o->r2 ? rtp[b] : nullptr; }
       PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
     }
     {
@@ -686,6 +693,46 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       const void* Rc[MAXB];
       for (int b = 0; b < nb; ++b) { fin.coef[b] = rs[b]; Rc[b] = Rb[b]; }
       PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st));
+    }
+    if (o->r2) {  // procrustes_step_r2 (psgd_pro_fast.py:141-153)
+      bf16_t* Sb[MAXB];  // S = rs^2 R R^T, bf16, in the RQ^T buffer
+      bf16_t* Mb[MAXB];  // M = a rs R - a^2/2 S, bf16, in the (unused) fp32 RQ buffer
+      for (int b = 0; b < nb; ++b) { Sb[b] = RQTb[b]; Mb[b] = reinterpret_cast<bf16_t*>(RQ[b]); }
+      int nt = 0;
+      {  // S = rs^2 R R^T (SYRK of R's rows, scaled in the epilogue) -> bf16 mirrored, partials of sum S * Qn
+        B16Out out;
+        out.ldcb = d;
+        EpiSpec e;
+        e.epi = EPI_STRACE; e.ldx = d;
+        for (int b = 0; b < nb; ++b) { A[b] = Rb[b]; out.Cb[b] = Sb[b]; e.X1[b] = Qn[b]; e.s[b] = rs[b]; e.part[b] = tpart[b]; }
+        PSGDK_TRY(run_b16(nb, d, d, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, &nt, st));
+      }
+      {
+        EwArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.nb = nb; a.i0 = (int)rform_pairs(d); a.i1 = nt; a.f0 = 0.125f;
+        for (int b = 0; b < nb; ++b) { a.in2[b] = rtp[b]; a.in3[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
+        PSGDK_HIP(proc_scalar_r2_launch(a, st), "procrustes r2 step size");
+      }
+      {
+        EwArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.nb = nb; a.m = d; a.n = d; a.dt = PSGDK_BF16;
+        for (int b = 0; b < nb; ++b) { a.in[b] = Rb[b]; a.in2[b] = reinterpret_cast<const float*>(Sb[b]); a.out2[b] = Mb[b]; a.sc[b] = pc[b]; }
+        PSGDK_HIP(mform_launch(a, st), "M = a rs R - a^2/2 S");
+      }
+      {  // Q = Qn + M Qn -> Q fp32 + Q^T shadow
+        B16Out out;
+        out.ldc = d; out.ldct = d;
+        EpiSpec e;
+        e.epi = EPI_FACTOR; e.ldx = d;
+        for (int b = 0; b < nb; ++b) {
+          A[b] = Mb[b]; B[b] = QnTb[b]; out.C[b] = g->Q[f][b]; out.CTb[b] = reinterpret_cast<bf16_t*>(g->Qt16[f][b]);
+          e.X1[b] = Qn[b]; e.s[b] = pc[b] + 2;
+        }
+        PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+      }
+      continue;
     }
     int nt = 0;
     {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials (tr(R RQ) reads the bf16 R of the product)
@@ -795,7 +842,7 @@ int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const*
 // Dense factor steps of the general engine, shared by psgdk_kron2d_update and the per-factor entry points.
 
 struct FacWs {
-  float *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB];
+  float *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *rtp[MAXB];
   NlbWs nw;
 };
 
@@ -806,8 +853,9 @@ void fac_take(Ws& w, int64_t d, int nb, FacWs& o) {
     o.RQ[b] = w.take<float>(d * d);
     o.coef[b] = w.take<float>(4);
     o.rs[b] = w.take<float>(4);
-    o.pc[b] = w.take<float>(4);
+    o.pc[b] = w.take<float>(8);
     o.tpart[b] = w.take<float>(2 * (size_t)tp);
+    o.rtp[b] = w.take<float>(rform_pairs(d));
   }
   nlb_take(w, d, nb, o.nw);
 }
@@ -837,13 +885,49 @@ int factor_update_run(int prec, int nb, int64_t d, const float* const* T1, int t
 
 // Qout = procrustes_step2(Q) (psgd_pro.py:71-94): R = Q^T - Q, R /= nlb_skh(R, V) + sn, RQ = R Q, RRQ = R RQ,
 // a = min(-tr(RQ)/tr(RRQ), 1/8) if tr(RRQ) < 0 else 1/8, Qout = Q + a (RQ + a/2 RRQ). Qout must not alias Q.
+// procrustes_step_r2 (psgd_pro_fast.py:141-153) on the fp32 engine, after R = Q^T - Q (with the partials of
+// sum R * Q) and its norm bound: S = rs^2 R R^T (SYRK, mirrored, with the partials of sum S * Q), the step size and
+// M's coefficients, M = a rs R - a^2/2 S (in R's buffer), Qout = Q + M Q.
+int procrustes_r2_tail(int prec, int nb, int64_t d, const float* const* Q, float* const* Qout, const FacWs& w,
+                       hipStream_t st) {
+  {
+    Opnd a;
+    a.mode = KC; a.ld = d;
+    EpiSpec e;
+    e.epi = EPI_STRACE; e.ldx = d;
+    for (int b = 0; b < nb; ++b) { a.p[b] = w.R[b]; e.X1[b] = Q[b]; e.s[b] = w.rs[b]; e.part[b] = w.tpart[b]; }
+    PSGDK_TRY(run_gemm(prec, nb, d, d, d, a, a, w.RQ, d, e, 1, PSGDK_OUT_MIRROR, 0, 1, 0, st));
+  }
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.i0 = (int)rform_pairs(d); a.i1 = gemm_tiles(d, d, 1); a.f0 = 0.125f;
+    for (int b = 0; b < nb; ++b) { a.in2[b] = w.rtp[b]; a.in3[b] = w.tpart[b]; a.sc[b] = w.rs[b]; a.out[b] = w.pc[b]; }
+    PSGDK_HIP(proc_scalar_r2_launch(a, st), "procrustes r2 step size");
+  }
+  {
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = d; a.n = d; a.dt = PSGDK_F32;
+    for (int b = 0; b < nb; ++b) { a.in[b] = w.R[b]; a.in2[b] = w.RQ[b]; a.out2[b] = w.R[b]; a.sc[b] = w.pc[b]; }
+    PSGDK_HIP(mform_launch(a, st), "M = a rs R - a^2/2 S");
+  }
+  Opnd a, bq;
+  a.mode = KC; a.ld = d;
+  bq.mode = MC; bq.ld = d;
+  EpiSpec e;
+  e.epi = EPI_FACTOR; e.ldx = d;  // X1 - (-1) (acc - 0 X1) = Q + M Q
+  for (int b = 0; b < nb; ++b) { a.p[b] = w.R[b]; bq.p[b] = Q[b]; e.X1[b] = Q[b]; e.s[b] = w.pc[b] + 2; }
+  return run_gemm(prec, nb, d, d, d, a, bq, Qout, d, e, 0, 0, 0, 1, 0, st);
+}
+
 int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* const* Qout, const float* const* V,
-                   const FacWs& w, hipStream_t st) {
+                   const FacWs& w, hipStream_t st, bool r2 = false) {
   {
     EwArgs a;
     std::memset(&a, 0, sizeof a);
     a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-    for (int b = 0; b < nb; ++b) { a.in[b] = Q[b]; a.out[b] = w.R[b]; }
+    for (int b = 0; b < nb; ++b) { a.in[b] = Q[b]; a.out[b] = w.R[b]; a.sc[b] = r2 ? w.rtp[b] : nullptr; }
     PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
   }
   {
@@ -855,6 +939,7 @@ int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* co
     for (int b = 0; b < nb; ++b) Rc[b] = w.R[b];
     PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 0, V, fin, w.nw, st));
   }
+  if (r2) return procrustes_r2_tail(prec, nb, d, Q, Qout, w, st);
   {
     Opnd a, bq;
     a.mode = KC; a.ld = d;
@@ -1111,7 +1196,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
   PSGDK_TRY(check_group(g));
   if (!o) return fail(PSGDK_EINVAL, "null options");
   if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
-  if (o->r2) return fail(PSGDK_EINVAL, "r2 is not provided by this version");
+  if (o->r2 != 0 && o->r2 != 1) return fail(PSGDK_EINVAL, "r2 = %d (0: procrustes_step2, 1: procrustes_step_r2)", o->r2);
   if (b16_group(g, o->tri)) return b16_update(g, o, noise, V, ws, ws_bytes, (hipStream_t)stream);
   const int nb = g->nb;
   const int64_t m = g->m, n = g->n, mn = m * n, dmx = dense_max(g);
@@ -1189,7 +1274,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
     const float* Qnc[MAXB];
     for (int b = 0; b < nb; ++b) { T1c[b] = T1[b]; Qc[b] = g->Q[f][b]; Qnc[b] = Qn[b]; }
     PSGDK_TRY(factor_update_run(g->prec, nb, d, T1c, term_tri, Qc, Qn, g->L[f], Vs, o->lr, o->betaL, term2, fw, st));
-    PSGDK_TRY(procrustes_run(g->prec, nb, d, Qnc, g->Q[f], Vk, fw, st));
+    PSGDK_TRY(procrustes_run(g->prec, nb, d, Qnc, g->Q[f], Vk, fw, st, o->r2 != 0));
   }
   // P refresh (psgd_pro_fast.py:191-192)
   int sel[MAXB];
@@ -1258,8 +1343,8 @@ int psgdk_factor_update(int prec, int64_t d, int nb, const float* const* term1, 
                            (hipStream_t)stream);
 }
 
-int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out, const float* const* V,
-                     void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+static int procrustes_entry(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out,
+                            const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st, bool r2) {
   PSGDK_TRY(check_prec(prec));
   PSGDK_TRY(check_nb(nb));
   PSGDK_TRY(check_dims(d, "d"));
@@ -1274,7 +1359,17 @@ int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* 
   PSGDK_TRY(check_ptrs(V, nb, "V"));
   for (int b = 0; b < nb; ++b)
     if (Q_out[b] == Q[b]) return fail(PSGDK_EINVAL, "Q_out[%d] aliases Q[%d]", b, b);
-  return procrustes_run(prec, nb, d, Q, Q_out, V, fw, (hipStream_t)stream);
+  return procrustes_run(prec, nb, d, Q, Q_out, V, fw, st, r2);
+}
+
+int psgdk_procrustes_r2(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out,
+                        const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  return procrustes_entry(prec, d, nb, Q, Q_out, V, ws, ws_bytes, (hipStream_t)stream, true);
+}
+
+int psgdk_procrustes(int prec, int64_t d, int nb, const float* const* Q, float* const* Q_out, const float* const* V,
+                     void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  return procrustes_entry(prec, d, nb, Q, Q_out, V, ws, ws_bytes, (hipStream_t)stream, false);
 }
 
 int psgdk_apply2d(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params, float* const* pre_out,

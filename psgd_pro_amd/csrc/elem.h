@@ -27,6 +27,10 @@ hipError_t noise_launch(const EwArgs& a, hipStream_t st);
 hipError_t rform_launch(const EwArgs& a, hipStream_t st);
 // Procrustes step size from the trace partials     (psgd_pro.py:91-93)
 hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st);
+// procrustes_step_r2 step size and the coefficients of M = a Rn + a^2/2 S   (psgd_pro_fast.py:141-153)
+hipError_t proc_scalar_r2_launch(const EwArgs& a, hipStream_t st);
+// M = c0 R + c1 S (bf16 or fp32, elementwise)       (psgd_pro_fast.py:153)
+hipError_t mform_launch(const EwArgs& a, hipStream_t st);
 // out = in * p_row[i] * p_col[j] (diagonal factors' P = q * q; null pointer = 1)
 hipError_t diag_scale_launch(const EwArgs& a, hipStream_t st);
 // diagonal factor term1: sums of squares along rows (i0 = 0) or columns (i0 = 1) of Pg  (psgd_pro.py:125-126)

@@ -20,6 +20,31 @@ __device__ __forceinline__ void ew_range(long long total, int blocks_per, long l
   end = beg + chunk < total ? beg + chunk : total;
 }
 
+// Eight consecutive elements at a 16-byte aligned address, as floats / from floats.
+__device__ __forceinline__ void ew_load8(const bf16_t* src, float (&x)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(src);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = __uint_as_float(w[e] << 16);
+    x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void ew_load8(const float* src, float (&x)[8]) {
+  const float4 p = reinterpret_cast<const float4*>(src)[0], q = reinterpret_cast<const float4*>(src)[1];
+  x[0] = p.x; x[1] = p.y; x[2] = p.z; x[3] = p.w; x[4] = q.x; x[5] = q.y; x[6] = q.z; x[7] = q.w;
+}
+__device__ __forceinline__ void ew_store8(bf16_t* dst, const float (&x)[8]) {
+  *reinterpret_cast<uint4*>(dst) = make_uint4(pack2(f32_to_bf16(x[0]), f32_to_bf16(x[1])),
+                                              pack2(f32_to_bf16(x[2]), f32_to_bf16(x[3])),
+                                              pack2(f32_to_bf16(x[4]), f32_to_bf16(x[5])),
+                                              pack2(f32_to_bf16(x[6]), f32_to_bf16(x[7])));
+}
+__device__ __forceinline__ void ew_store8(float* dst, const float (&x)[8]) {
+  reinterpret_cast<float4*>(dst)[0] = make_float4(x[0], x[1], x[2], x[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4(x[4], x[5], x[6], x[7]);
+}
+
 static int ew_blocks(long long total) {
   long long b = (total + (long long)EW_THREADS * EW_PER_THREAD - 1) / ((long long)EW_THREADS * EW_PER_THREAD);
   if (b < 1) b = 1;
@@ -53,7 +78,9 @@ hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
 // R[i][j] = sign * (Q[j][i] - Q[i][j]) and R[j][i] = -R[i][j] from one read of each 64 x 64 tile pair (I <= J):
 // both tiles are staged in LDS (16-byte loads when rows are 16-byte aligned), each output tile is written
 // row-major from there, 4 consecutive columns per thread (16-byte fp32 / 8-byte bf16 stores). Outputs: R fp32
-// (out, optional) and R bf16 (out2, optional). grid: nb * T (T + 1) / 2, T = ceil(d / 64).
+// (out, optional) and R bf16 (out2, optional); with sc[b] set, sc[b][pair] = sum of R_ij Q_ij over the pair's
+// elements (fp32 values, a fixed-order block sum; the r2 Procrustes trace). grid: nb * T (T + 1) / 2,
+// T = ceil(d / 64).
 __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   constexpr int TP = 65;        // LDS pitch (floats): column reads of the transposed tile are conflict-free
   __shared__ float qa[64 * TP];  // Q[I block][J block]
@@ -63,6 +90,7 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   int t = blockIdx.x % np, I = 0;
   while (t >= T - I) { t -= T - I; ++I; }
   const int J = I + t;
+  const int pair = blockIdx.x % np;
   const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
   float* __restrict__ R = a.out[b];
   bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
@@ -92,13 +120,17 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   stage(qb, J, I);
   __syncthreads();
   // out(rb, cb)[r][c] = sg (src_t[c][r] - src[r][c]): (I, J) from (qb, qa), (J, I) from (qa, qb)
+  float tr = 0.f;  // sum of R_ij Q_ij (out-of-range elements are zero in both staged tiles)
   auto emit = [&](const float* src, const float* srct, int rb, int cb) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
       float v[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
+      for (int e = 0; e < 4; ++e) {
+        v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
+        tr += v[e] * src[r * TP + c4 + e];
+      }
       const long long o = (long long)gi * ld + gj;
       if (vec) {
         if (R) *reinterpret_cast<float4*>(R + o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -117,6 +149,11 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   };
   emit(qa, qb, I, J);
   if (I != J) emit(qb, qa, J, I);
+  if (a.sc[b]) {
+    __shared__ float red[16];
+    tr = block_sum(tr, red);
+    if (tid == 0) a.sc[b][pair] = tr;
+  }
 }
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
   const long long T = (a.m + 63) / 64;
@@ -149,6 +186,85 @@ __global__ void __launch_bounds__(256) proc_scalar_kernel(const EwArgs a) {
 }
 hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(proc_scalar_kernel, dim3(a.nb), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// Step size of procrustes_step_r2 (psgd_pro_fast.py:141-153) from R = Q^T - Q (unscaled; the reference's
+// Rn = Q - Q^T scaled by rs = sc[b][0] = 1 / (bound + smallest normal) is -rs R) and S = Rn^T Rn = rs^2 R R^T
+// (already scaled by the SYRK epilogue): in2[b] = the i0 partials of sum R_ij Q_ij, in3[b] = the i1 SYRK trace
+// partials (sum S_ij Q_ij at odd slots). tr(RQ) = sum(Rn * Q) = -rs sum(R * Q), tr(RRQ) = -sum(S * Q);
+// a = min(-tr(RQ) / tr(RRQ), f0) if tr(RRQ) < 0 else f0. Q - (a Rn + a^2/2 S) Q = Q + M Q with
+// M = a rs R - a^2/2 S: out[b] = {a rs, -a^2/2, -1, 0, a, tr(RQ), tr(RRQ)} (slots 2, 3: the coefficients that
+// turn the factor-update epilogue X1 - s0 (acc - s1 X1) into X1 + acc). rs^2 is never formed: R = 0 (a
+// symmetric Q, bound 0, rs = 1 / smallest normal) gives S = 0, tr = 0, M = 0 and Q unchanged, as in the
+// reference, where Rn is scaled before it is squared.
+__global__ void __launch_bounds__(256) proc_scalar_r2_kernel(const EwArgs a) {
+  __shared__ float red[16];
+  const int b = blockIdx.x;
+  float t1 = 0.f, t2 = 0.f;
+  for (int t = threadIdx.x; t < a.i0; t += blockDim.x) t1 += a.in2[b][t];
+  for (int t = threadIdx.x; t < a.i1; t += blockDim.x) t2 += a.in3[b][2 * t + 1];
+  t1 = block_sum(t1, red);
+  t2 = block_sum(t2, red);
+  if (threadIdx.x == 0) {
+    const float rs = a.sc[b][0];
+    const float trq = -rs * t1, trrq = -t2;
+    float step = a.f0;
+    if (trrq < 0.f) {
+      const float x = -trq / trrq;
+      step = x > a.f0 ? a.f0 : x;
+    }
+    float* o = a.out[b];
+    o[0] = step * rs;
+    o[1] = -0.5f * step * step;
+    o[2] = -1.f;
+    o[3] = 0.f;
+    o[4] = step;
+    o[5] = trq;
+    o[6] = trrq;
+  }
+}
+hipError_t proc_scalar_r2_launch(const EwArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(proc_scalar_r2_kernel, dim3(a.nb), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// M = c0 R + c1 S over m x n contiguous elements, c = sc[b][0..1]; R = in[b], S = in2 (as `in`'s dtype dt), M =
+// out2[b] in the same dtype (bf16 or fp32). 8 elements per thread and step (16-byte access when m n % 8 == 0 and
+// the bases are 16-byte aligned).
+template <typename T>
+__global__ void __launch_bounds__(EW_THREADS) mform_kernel(const EwArgs a, int blocks_per) {
+  const int b = blockIdx.x / blocks_per;
+  const long long total = a.m * a.n;
+  const T* __restrict__ R = reinterpret_cast<const T*>(a.in[b]);
+  const T* __restrict__ S = reinterpret_cast<const T*>(a.in2[b]);
+  T* __restrict__ M = reinterpret_cast<T*>(a.out2[b]);
+  const float c0 = a.sc[b][0], c1 = a.sc[b][1];
+  const bool vec = (total & 7) == 0 && ((reinterpret_cast<uintptr_t>(R) | reinterpret_cast<uintptr_t>(S) |
+                                         reinterpret_cast<uintptr_t>(M)) & 15) == 0;
+  if (vec) {
+    const long long nv = total >> 3;
+    const long long chunk = (nv + blocks_per - 1) / blocks_per;
+    const long long beg = (long long)(blockIdx.x % blocks_per) * chunk, end = min(nv, beg + chunk);
+    for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+      float r[8], s[8];
+      ew_load8(R + 8 * i, r);
+      ew_load8(S + 8 * i, s);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = c0 * r[e] + c1 * s[e];
+      ew_store8(M + 8 * i, r);
+    }
+  } else {
+    long long beg, end;
+    ew_range(total, blocks_per, beg, end);
+    for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS)
+      M[i] = from_f32<T>(c0 * to_f32<T>(R[i]) + c1 * to_f32<T>(S[i]));
+  }
+}
+hipError_t mform_launch(const EwArgs& a, hipStream_t st) {
+  const int bp = ew_blocks(a.m * a.n / 8 + 1);
+  if (a.dt) hipLaunchKernelGGL(mform_kernel<bf16_t>, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  else hipLaunchKernelGGL(mform_kernel<float>, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
   return hipGetLastError();
 }
 

@@ -345,6 +345,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
             break;
           }
           case EPI_SUMSQ: v = p.alpha * a; t1 += v * v; break;
+          case EPI_STRACE: {  // tri: element (row, col), row <= col, stands for (col, row) too
+            v = (s0 * a) * s0;
+            t2 += v * (X1[(long long)row * ldx + col] + (row != col ? X1[(long long)col * ldx + row] : 0.f));
+            break;
+          }
           default: v = p.beta != 0.f ? p.alpha * a + p.beta * C[off] : p.alpha * a; break;
         }
         if (p.tri) {
@@ -360,10 +365,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
       }
     }
   }
-  if (p.epi == EPI_RQ || p.epi == EPI_SUMSQ) {
+  if (p.epi == EPI_RQ || p.epi == EPI_SUMSQ || p.epi == EPI_STRACE) {
     __shared__ float red[16];
     t1 = block_sum(t1, red);
-    if (p.epi == EPI_RQ) t2 = block_sum(t2, red);
+    if (p.epi == EPI_RQ || p.epi == EPI_STRACE) t2 = block_sum(t2, red);
     if (tid == 0) {
       p.part[b][2 * tile] = t1;
       p.part[b][2 * tile + 1] = t2;

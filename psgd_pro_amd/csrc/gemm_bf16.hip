@@ -258,10 +258,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   const float* __restrict__ X1 = p.X1[b];
   const float* __restrict__ X2 = p.X2[b];
   float s0 = 0.f, s1 = 0.f;
-  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_SCALE || EPI == EPI_RQ) s0 = p.s[b][0];
+  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_SCALE || EPI == EPI_RQ || EPI == EPI_STRACE)
+    s0 = p.s[b][0];
   if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) s1 = p.s[b][1];
   const bool mirror = p.tri && p.out_mode == 1;
-  const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ;
+  const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ || EPI == EPI_STRACE;
   auto al = [](const void* q, int bytes) { return (reinterpret_cast<uintptr_t>(q) & (bytes - 1)) == 0; };
   const bool fast = m0 + BM <= p.M && n0 + BN <= p.N && (!p.tri || ti < tj) &&
                     (!C || ((p.ldc & 3) == 0 && al(C, 16))) && (!Cb || ((p.ldcb & 3) == 0 && al(Cb, 8))) &&
@@ -324,12 +325,24 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
             v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
           } else if constexpr (EPI == EPI_PROC) {
             v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
+          } else if constexpr (EPI == EPI_STRACE) {
+            v[e] = (s0 * v[e]) * s0;
           } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
             v[e] = s0 * v[e];
             if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
           } else {
             v[e] = p.alpha * v[e];
             if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
+          }
+        }
+        if constexpr (EPI == EPI_STRACE) {  // sum C_ij X1_ij over the stored (upper) elements, diagonal included
+          if constexpr (FAST) {
+            const float4 t = *reinterpret_cast<const float4*>(X1 + xo);
+            t2 += v[0] * t.x + v[1] * t.y + v[2] * t.z + v[3] * t.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (ok[e]) t2 += v[e] * X1[xo + e];
           }
         }
         *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
@@ -381,6 +394,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
               if (ok[e]) t2 += s0 * bf16_to_f32(x[e]) * v[e];
           }
         }
+        if constexpr (EPI == EPI_STRACE) {  // the mirrored elements (col, row + e), strictly below the diagonal
+          const float* x = X1 + (long long)col * p.ldx + row;
+          if constexpr (FAST) {
+            const float4 t = *reinterpret_cast<const float4*>(x);
+            t2 += v[0] * t.x + v[1] * t.y + v[2] * t.z + v[3] * t.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (ok[e] && row + e < col) t2 += v[e] * x[e];
+          }
+        }
         if (CTb) {
           bf16_t* dst = CTb + (long long)col * p.ldct + row;
           if (FAST || (all && (p.ldct & 3) == 0))
@@ -428,10 +452,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       __syncthreads();
     }
   }
-  if constexpr (EPI == EPI_RQ || EPI == EPI_SUMSQ) {
+  if constexpr (EPI == EPI_RQ || EPI == EPI_SUMSQ || EPI == EPI_STRACE) {
     __shared__ float red[16];
     t1 = block_sum(t1, red);
-    if constexpr (EPI == EPI_RQ) t2 = block_sum(t2, red);
+    if constexpr (EPI == EPI_RQ || EPI == EPI_STRACE) t2 = block_sum(t2, red);
     if (tid == 0) {
       p.part[b][2 * tile] = t1;
       p.part[b][2 * tile + 1] = t2;
@@ -472,6 +496,7 @@ static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
     case EPI_SCALE: return launch_b16<BM, BN, WGM, WGN, EPI_SCALE>(a, st);
     case EPI_RQ: return launch_b16<BM, BN, WGM, WGN, EPI_RQ>(a, st);
     case EPI_SUMSQ: return launch_b16<BM, BN, WGM, WGN, EPI_SUMSQ>(a, st);
+    case EPI_STRACE: return launch_b16<BM, BN, WGM, WGN, EPI_STRACE>(a, st);
     default: return launch_b16<BM, BN, WGM, WGN, EPI_STORE>(a, st);
   }
 }

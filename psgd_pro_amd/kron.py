@@ -96,8 +96,7 @@ class KronWhiten:
             assert self.momentum > 0, "Cannot whiten momentum if the momentum setting is invalid."
         if compile is not None:
             raise ValueError("compile: the HIP engine runs without torch.compile (pass compile=None)")
-        if r2:
-            raise NotImplementedError("r2 (procrustes_step_r2) is not provided by this version of the engine")
+        self._r2 = bool(r2)  # procrustes_step_r2 (psgd_pro_fast.py:141-153) instead of procrustes_step2
         flags = getattr(ops, "flags", frozenset()) if ops is not None else frozenset()
         self.ops = ops if ops is not None else make_ops(())
         if precision is None:
@@ -299,7 +298,7 @@ class KronWhiten:
                 cur.wait_stream(ln.stream)
 
     def _update(self, srcs, noise, V):
-        o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, 0)
+        o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))
         dev = srcs[0].device
         cur, lanes = self._fork(dev)
         for gi, grp in enumerate(self._groups):

@@ -316,12 +316,37 @@ def test_procrustes_matches_oracle(hip, d, prec):
     Vs = [rnd(32, d, seed=d + 5 + b) for b in range(2)]
     Qd = [q.to(DEV) for q in Qs]
     Qo = [torch.empty_like(q) for q in Qd]
-    L.call_ws(L.lib().psgdk_procrustes, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs([v.to(DEV) for v in Vs]),
+    Vd = [v.to(DEV) for v in Vs]  # held until the kernels have run (a freed block can become the workspace)
+    L.call_ws(L.lib().psgdk_procrustes, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Vd),
               ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
     for b in range(2):
         ref = Qs[b].double().clone()
         procrustes_step2(ref, Vs[b].double())
         assert rel_err_norm(Qo[b], ref) < (1e-5 if prec == 0 else 5e-3)
+
+
+@pytest.mark.parametrize("d", [64, 130, 256])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_procrustes_r2_matches_oracle(hip, d, prec):
+    """psgdk_procrustes_r2 against the oracle's procrustes_step_r2 (psgd_pro_fast.py:141-153) in float64 on the
+    same V: rel 1e-5 normwise for fp32, 5e-3 for bf16 MFMA inputs; and against procrustes_step2 (the same
+    rotation) at the same bars."""
+    from oracle.psgd_oracle import procrustes_step2, procrustes_step_r2
+    Qs = [torch.eye(d) + 0.05 * rnd(d, d, seed=d + b) for b in range(2)]
+    Vs = [rnd(32, d, seed=d + 5 + b) for b in range(2)]
+    Qd = [q.to(DEV) for q in Qs]
+    Qo = [torch.empty_like(q) for q in Qd]
+    Vd = [v.to(DEV) for v in Vs]  # held until the kernels have run (a freed block can become the workspace)
+    L.call_ws(L.lib().psgdk_procrustes_r2, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Vd),
+              ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+    tol = 1e-5 if prec == 0 else 5e-3
+    for b in range(2):
+        ref = Qs[b].double().clone()
+        procrustes_step_r2(ref, Vs[b].double())
+        assert rel_err_norm(Qo[b], ref) < tol
+        ref2 = Qs[b].double().clone()
+        procrustes_step2(ref2, Vs[b].double())
+        assert rel_err_norm(Qo[b], ref2) < tol
 
 
 def test_hip_ops_plugin_methods(hip):

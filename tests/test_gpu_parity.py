@@ -33,7 +33,8 @@ def _metrics(Qs, Ls, pre, W, ref):
         for q, qo in zip(Qs[i], ref.Q[i]):
             out["Q"] = max(out["Q"], rel_err_floor(q, qo))
         for l, lo in zip(Ls[i], ref.L[i]):
-            out["L"] = max(out["L"], abs(float(l) - float(lo)) / max(abs(float(lo)), 1e-30))
+            e = abs(float(l) - float(lo)) / max(abs(float(lo)), 1e-30)
+            out["L"] = max(out["L"], e if math.isfinite(e) else math.inf)
         out["pre"] = max(out["pre"], rel_err_floor(pre[i], ref.pre[i]))
         out["pre_norm"] = max(out["pre_norm"], rel_err_norm(pre[i], ref.pre[i]))
         out["W"] = max(out["W"], rel_err_norm(W[i], ref.params[i]))
@@ -41,19 +42,20 @@ def _metrics(Qs, Ls, pre, W, ref):
 
 
 def run_pair(shapes, steps, seed=0, skew=1.0, max_size=math.inf, prec="fp32", gdt=torch.float32, grad_eps=None,
-             momentum=0.0, update_first=True, tri=None, whiten_grad=True, ref_dtype=torch.float64, baseline=True):
+             momentum=0.0, update_first=True, tri=None, whiten_grad=True, ref_dtype=torch.float64, baseline=True,
+             r2=False):
     """Runs the GPU optimizer, the oracle in ref_dtype (the reference) and, with baseline, the oracle in float32 on
     the same gradients and draws. Returns the worst metrics of GPU vs reference and of float32 oracle vs reference
     over all steps."""
     Wg = [torch.zeros(s, device=DEV, dtype=torch.float32, requires_grad=True) for s in shapes]
     kw = dict(preconditioner_max_skew=skew, preconditioner_max_size=max_size, preconditioner_init_scale=1.0,
               momentum=momentum, update_preconditioner_first=update_first, whiten_grad=whiten_grad)
-    opt = KronWhiten(Wg, precision=prec, draws="host", seed=seed, tri=tri, **kw)
+    opt = KronWhiten(Wg, precision=prec, draws="host", seed=seed, tri=tri, r2=r2, **kw)
     opt.capture = True
     ref = O.OracleKron([torch.zeros(s, dtype=ref_dtype) for s in shapes], seed=seed, dtype=ref_dtype,
-                       grad_eps=grad_eps, **kw)
+                       grad_eps=grad_eps, r2=r2, **kw)
     o32 = O.OracleKron([torch.zeros(s, dtype=torch.float32) for s in shapes], seed=seed, dtype=torch.float32,
-                       grad_eps=grad_eps, **kw) if baseline else None
+                       grad_eps=grad_eps, r2=r2, **kw) if baseline else None
     worst = {}
     base = {}
     for t in range(steps):
@@ -115,6 +117,32 @@ def test_bf16_parity(hip, b16cfg):
     eps16 = torch.finfo(torch.bfloat16).eps
     worst, _ = run_pair([(256, 384), (384, 256)], steps=8, skew=math.inf, prec="bf16", gdt=torch.bfloat16,
                         grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
+    assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
+
+
+@pytest.mark.parametrize("shapes", [[(64, 96)], [(200, 136)], [(48, 64), (48, 64), (32,), (64, 48)]])
+def test_fp32_parity_r2(hip, shapes):
+    """r2=True (procrustes_step_r2, psgd_pro_fast.py:141-153) against the float64 oracle's r2 form at the fp32
+    bar: S = Rn^T Rn by the SYRK with its trace epilogue, tr(RQ) from the R-forming kernel, Q - M Q in one GEMM."""
+    assert_fp32(*run_pair(shapes, steps=6, skew=math.inf, r2=True))
+
+
+def test_fp32_r2_tracks_step2(hip):
+    """The two Procrustes forms are the same algebra: over 6 steps r2 and step2 on the GPU stay within the fp32
+    bar of each other (both against the float64 step2 oracle)."""
+    worst, base = run_pair([(96, 160)], steps=6, skew=math.inf, r2=True)  # vs float64 r2
+    w2, b2 = run_pair([(96, 160)], steps=6, skew=math.inf, r2=False)     # vs float64 step2
+    O.MAX_PROCRUSTES  # the oracle's step bound, 1/8, shared by both forms
+    for k in ("Q", "pre", "W"):
+        assert worst[k] < max(TOL32, 2 * base[k]) and w2[k] < max(TOL32, 2 * b2[k]), (k, worst, w2)
+
+
+def test_bf16_parity_r2(hip, b16cfg):
+    """r2 on the bf16 path (the SYRK of R with the trace epilogue on both of its tile paths in every tile
+    configuration) against the float32 oracle's r2 form, at the bf16 bar."""
+    eps16 = torch.finfo(torch.bfloat16).eps
+    worst, _ = run_pair([(256, 384), (384, 256)], steps=8, skew=math.inf, prec="bf16", gdt=torch.bfloat16,
+                        grad_eps=eps16, ref_dtype=torch.float32, baseline=False, r2=True)
     assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
 
 

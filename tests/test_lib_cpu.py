@@ -127,9 +127,12 @@ def test_group_validation():
     g.Q[0][0] = None
     assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.EINVAL
     assert "Q" in _err()
-    o.r2 = 1
     g.Q[0][0] = 0x1000
+    o.r2 = 1  # procrustes_step_r2: a valid choice (workspace query)
+    assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.OK
+    o.r2 = 2
     assert lib.psgdk_kron2d_update(g, o, None, None, None, C.byref(sz), None) == L.EINVAL
+    assert "r2" in _err()
 
 
 def test_python_surface_on_cpu():
