@@ -45,6 +45,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
+    ap.add_argument("--t1q-pg", type=int, default=1,
+                    help="0: form term1 Q as the reference writes it, never through Pg (library option 5)")
     ap.add_argument("--r2", type=int, default=0,
                     help="1: the Procrustes step in the reference's r2 form (KronWhiten(r2=True), 3 d^3 instead of 4 d^3)")
     return ap.parse_args()
@@ -131,6 +133,7 @@ def bench_vitb(args):
     from psgd_pro_amd import _lib as L
 
     dev = torch.device("cuda:0")
+    L.check(L.lib().psgdk_set_option(5, args.t1q_pg))
     skew = math.inf if args.skew == "inf" else float(args.skew)
     shapes = VIT_B * args.blocks
     gen = torch.Generator().manual_seed(0)
@@ -179,6 +182,7 @@ def bench_vitb(args):
     s_fl = sum(v[2] for v in syrk.values())
     syrk_tf = s_fl / (s_ms * 1e-3) / 1e12 if s_ms else 0.0
     mfma_ms = sum(v[1] for v in agg.values()) / args.steps
+    mfma_fl = sum(v[2] for v in agg.values()) / args.steps  # flops the MFMA launches execute (their own shapes)
     out = {
         "metric": METRIC,
         "value": round(wall_ms, 3),
@@ -195,6 +199,7 @@ def bench_vitb(args):
         "config": {"workload": "vit-b16-kron-update-apply", "weights": "12 x {768x2304, 768x768, 768x3072, 3072x768}",
                    "blocks": args.blocks, "grad_dtype": "bf16", "factor_dtype": "fp32", "max_size": 8192,
                    "max_skew": args.skew, "update_probability": 1.0, "procrustes": "r2" if args.r2 else "step2",
+                   "term1_q": "pg" if args.t1q_pg else "term1",
                    "parallelism": "none"},
         "gpu_ms_per_step": round(ev_ms, 3),
         "streams": args.streams,
@@ -203,6 +208,8 @@ def bench_vitb(args):
         "algorithmic_tflop_per_step": round(flops_step / 1e12, 4),
         "tflops": round(flops_step / (wall_ms * 1e-3) / 1e12, 2),
         "mfma_ms_per_step": round(mfma_ms, 3),
+        "executed_mfma_tflop_per_step": round(mfma_fl / 1e12, 4),
+        "executed_tflops": round(mfma_fl / (wall_ms * 1e-3) / 1e12, 2),
         "syrk": {"tflops": round(syrk_tf, 2), "frac": round(syrk_tf / PEAK[args.precision], 4),
                  "launches_per_step": s_l / args.steps, "ms_per_step": round(s_ms / args.steps, 3)},
         "roofline": {"bound": "mfma", "kernel": kname, "launches_per_step": n_l / args.steps,

@@ -203,6 +203,7 @@ int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's
 int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
 int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
 int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape, 0 split-K + reduce, 1 column blocks
+int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
 
 int b16_cfg(int64_t M, int64_t N, int tri, int nb) {
   if (g_force_cfg >= 0) return g_force_cfg;
@@ -588,10 +589,11 @@ int refresh_p_diag(const psgdk_kron2d_t* g, int f, const int* sel, int nsel, hip
 //   X  = G + (damping + eps |G|) N                      -> Xb
 //   Y  = X P2            (A = Xb,   B = P2 shadow)      -> Y^T bf16
 //   Pg = P1 Y            (A = P1 shadow, B = Y^T)       -> Pg bf16, Pg^T bf16
-//   per factor: term1 = SYRK (Pg or Pg^T) -> fp32 + bf16; bound, L, lr/L; Qn = Q - lr/L (term1 Q - term2 Q)
-//   (B = Q^T shadow) -> fp32 + Qn^T bf16; R = Qn^T - Qn -> fp32 + bf16; skew bound; RQ (B = Qn^T) -> fp32 +
-//   RQ^T bf16 + traces; step size; Q = Qn + a RQ + a^2/2 R RQ (B = RQ^T) -> Q fp32 + Q^T shadow
-//   P = Q^T Q (SYRK of the Q^T shadow) -> P fp32 + P shadow
+//   per factor: term1 = SYRK (Pg or Pg^T) -> bf16; bound, L, lr/L; Qn = Q - lr/L (term1 Q - term2 Q)
+//   (B = Q^T shadow; when the other side is under half of d, term1 Q is formed as Pg^T (Pg Q) or Pg (Pg^T Q))
+//   -> fp32 + Qn^T bf16; R = Qn^T - Qn -> bf16; skew bound; RQ (B = Qn^T) -> fp32 + RQ^T bf16 + traces; step
+//   size; Q = Qn + a RQ + a^2/2 R RQ (B = RQ^T) -> Q fp32 + Q^T shadow (r2: S = Rn^T Rn by SYRK, Q + M Q)
+//   P = Q^T Q (SYRK of the Q^T shadow) -> P shadow
 int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
                const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st) {
   const int nb = g->nb;
@@ -668,7 +670,33 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; T1c[b] = T1b[b]; }
       PSGDK_TRY(run_nlb_full(d, 1, nb, T1c, d, 1, Vs, fin, nw, st));
     }
-    {  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16
+    if (g_t1q_pg && 2 * other < d) {
+      // term1 Q = Pcol (Prow Q) with term1 = Pcol Prow (Pcol = Pg^T, Prow = Pg for f = 1; Pcol = Pg, Prow = Pg^T
+      // for f = 0): 4 other d^2 flops instead of 2 d^3, the same product associated the other way.
+      // Z = Prow Q (other x d; B = Q^T shadow) -> Z^T bf16 (d x other) in the RQ^T buffer, then
+      // Qn = Q - lr/L (Pcol Z - term2 Q) (A = Pcol, B = Z^T) -> fp32 + Qn^T bf16
+      {
+        B16Out out;
+        out.ldct = other;
+        for (int b = 0; b < nb; ++b) {
+          A[b] = f == 1 ? (const void*)Pgb[b] : (const void*)PgTb[b];
+          B[b] = g->Qt16[f][b];
+          out.CTb[b] = RQTb[b];
+        }
+        EpiSpec e;
+        PSGDK_TRY(run_b16(nb, other, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+      }
+      B16Out out;
+      out.ldc = d; out.ldct = d;
+      EpiSpec e;
+      e.epi = EPI_FACTOR; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        A[b] = f == 1 ? (const void*)PgTb[b] : (const void*)Pgb[b];
+        B[b] = RQTb[b]; out.C[b] = Qn[b]; out.CTb[b] = QnTb[b];
+        e.X1[b] = g->Q[f][b]; e.s[b] = coef[b];
+      }
+      PSGDK_TRY(run_b16(nb, d, d, other, A, other, B, other, out, e, 0, 0, nullptr, st));
+    } else {  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16
       B16Out out;
       out.ldc = d; out.ldct = d;
       EpiSpec e;
@@ -1477,6 +1505,11 @@ int psgdk_set_option(int option, int value) {
   if (option == 4) {
     if (value < -1 || value > 1) return fail(PSGDK_EINVAL, "option 4 (V A kernel) must be -1, 0 or 1");
     g_vmm_cols = value;
+    return PSGDK_OK;
+  }
+  if (option == 5) {
+    if (value != 0 && value != 1) return fail(PSGDK_EINVAL, "option 5 (term1 Q through Pg) must be 0 or 1");
+    g_t1q_pg = value;
     return PSGDK_OK;
   }
   return fail(PSGDK_EINVAL, "unknown option %d", option);

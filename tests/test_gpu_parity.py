@@ -120,6 +120,23 @@ def test_bf16_parity(hip, b16cfg):
     assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
 
 
+@pytest.mark.parametrize("via_pg", [1, 0], ids=["pg", "term1"])
+@pytest.mark.parametrize("r2", [False, True], ids=["step2", "r2"])
+def test_bf16_parity_thin_weights(hip, b16cfg, r2, via_pg):
+    """Weights whose other side is under half of a factor's side (128 x 384, 384 x 128, 96 x 264): the bf16 update
+    forms term1 Q as Pg^T (Pg Q) or Pg (Pg^T Q) for those factors (the same product associated the other way).
+    Against the float32 oracle on the same gradients upcast, at the bf16 bar, in every tile configuration (264 =
+    256 + 8: ragged tiles), with both Procrustes forms."""
+    eps16 = torch.finfo(torch.bfloat16).eps
+    assert hip.psgdk_set_option(5, via_pg) == 0
+    try:
+        worst, _ = run_pair([(128, 384), (384, 128), (96, 264)], steps=8, skew=math.inf, prec="bf16",
+                            gdt=torch.bfloat16, grad_eps=eps16, ref_dtype=torch.float32, baseline=False, r2=r2)
+    finally:
+        hip.psgdk_set_option(5, 1)
+    assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
+
+
 @pytest.mark.parametrize("shapes", [[(64, 96)], [(200, 136)], [(48, 64), (48, 64), (32,), (64, 48)]])
 def test_fp32_parity_r2(hip, shapes):
     """r2=True (procrustes_step_r2, psgd_pro_fast.py:141-153) against the float64 oracle's r2 form at the fp32
