@@ -53,14 +53,43 @@ static int ew_blocks(long long total) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// 8 consecutive elements of a bf16 (dt = 1) or fp32 buffer at element offset i (16-byte aligned), as floats
+__device__ __forceinline__ void ew_load8_dt(const void* p, int dt, long long i, float (&x)[8]) {
+  if (dt) ew_load8(reinterpret_cast<const bf16_t*>(p) + i, x);
+  else ew_load8(reinterpret_cast<const float*>(p) + i, x);
+}
+__device__ __forceinline__ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The elementwise kernels take 8 elements per thread and step (16- and 32-byte accesses) when the element count
+// is a multiple of 8 and every base is 16-byte aligned; each workgroup owns a contiguous range of 8-element groups.
+__device__ __forceinline__ void ew_range8(long long total, int blocks_per, long long& beg, long long& end) {
+  ew_range(total >> 3, blocks_per, beg, end);
+}
+
 __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int blocks_per) {
   const int b = blockIdx.x / blocks_per;
   long long beg, end;
-  ew_range(a.m * a.n, blocks_per, beg, end);
   const void* G = a.in[b];
   const float* N = a.in2[b];
   float* X = a.out[b];
   bf16_t* Xb = reinterpret_cast<bf16_t*>(a.out2[b]);
+  const long long total = a.m * a.n;
+  if ((total & 7) == 0 && al16(G) && (!N || al16(N)) && (!X || al16(X)) && (!Xb || al16(Xb))) {
+    ew_range8(total, blocks_per, beg, end);
+    for (long long v = beg + threadIdx.x; v < end; v += EW_THREADS) {
+      float g[8], nz[8];
+      ew_load8_dt(G, a.dt, 8 * v, g);
+      if (N) {
+        ew_load8(N + 8 * v, nz);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] = g[e] + (a.f0 + a.f1 * fabsf(g[e])) * nz[e];
+      }
+      if (X) ew_store8(X + 8 * v, g);
+      if (Xb) ew_store8(Xb + 8 * v, g);
+    }
+    return;
+  }
+  ew_range(total, blocks_per, beg, end);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     const float g = ldv(G, a.dt, i);
     const float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[i] : g;
@@ -376,10 +405,28 @@ __global__ void __launch_bounds__(EW_THREADS) clip_update_kernel(const EwArgs a,
   const bool scale = avg > a.f0;
   const float sc = a.f0 / avg;
   long long beg, end;
-  ew_range(total, blocks_per, beg, end);
   const float* pre = a.in2[b];
   void* prm = const_cast<void*>(a.in[b]);
   float* gout = reinterpret_cast<float*>(a.out2[b]);
+  if ((total & 7) == 0 && al16(pre) && al16(prm) && (!gout || al16(gout))) {
+    ew_range8(total, blocks_per, beg, end);
+    for (long long v = beg + threadIdx.x; v < end; v += EW_THREADS) {
+      float g[8], w[8];
+      ew_load8(pre + 8 * v, g);
+      ew_load8_dt(prm, a.dt, 8 * v, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (scale) g[e] *= sc;
+        g[e] = fminf(fmaxf(g[e], -a.f1), a.f1);
+        w[e] = w[e] - a.f2 * g[e];
+      }
+      if (gout) ew_store8(gout + 8 * v, g);
+      if (a.dt) ew_store8(reinterpret_cast<bf16_t*>(prm) + 8 * v, w);
+      else ew_store8(reinterpret_cast<float*>(prm) + 8 * v, w);
+    }
+    return;
+  }
+  ew_range(total, blocks_per, beg, end);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     float g = pre[i];
     if (scale) g *= sc;
