@@ -45,6 +45,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
+    ap.add_argument("--fuse", type=int, default=1,
+                    help="0: one update call per weight group instead of one call batching all groups' factor work")
+    ap.add_argument("--upd-streams", type=int, default=3,
+                    help="side streams of the grouped update inside the library (library option 6)")
     ap.add_argument("--t1q-pg", type=int, default=1,
                     help="0: form term1 Q as the reference writes it, never through Pg (library option 5)")
     ap.add_argument("--r2", type=int, default=0,
@@ -134,6 +138,7 @@ def bench_vitb(args):
 
     dev = torch.device("cuda:0")
     L.check(L.lib().psgdk_set_option(5, args.t1q_pg))
+    L.check(L.lib().psgdk_set_option(6, args.upd_streams))
     skew = math.inf if args.skew == "inf" else float(args.skew)
     shapes = VIT_B * args.blocks
     gen = torch.Generator().manual_seed(0)
@@ -141,7 +146,7 @@ def bench_vitb(args):
     grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).to(dev) for s in shapes]
     opt = KronWhiten(params, preconditioner_max_size=8192, preconditioner_max_skew=skew,
                      preconditioner_init_scale=1.0, precision=args.precision, draws="device", seed=0,
-                     streams=args.streams, graphs=bool(args.graphs), r2=bool(args.r2))
+                     streams=args.streams, graphs=bool(args.graphs), r2=bool(args.r2), fuse_groups=bool(args.fuse))
     flops_step = sum(flops_2d(m, n, is_dense(m, m * n, 8192, skew), is_dense(n, m * n, 8192, skew), r2=bool(args.r2))
                      for m, n in shapes)
     for _ in range(args.warmup):
@@ -162,6 +167,7 @@ def bench_vitb(args):
     # Per-launch figures come from a second pass on one stream, eager, so that each kernel's HIP-event duration is
     # its own and not shared with another group's kernels.
     opt._nstreams, opt._use_graphs = 0, False
+    L.check(L.lib().psgdk_set_option(6, 0))  # the grouped update's side streams too
     opt.step_math(grads)
     torch.cuda.synchronize()
     L.profile_start()
@@ -170,6 +176,7 @@ def bench_vitb(args):
     torch.cuda.synchronize()
     recs = L.profile_stop()
     opt._nstreams = args.streams
+    L.check(L.lib().psgdk_set_option(6, args.upd_streams))
     agg, syrk = aggregate(recs)
     kid = max(agg, key=lambda k: agg[k][1])
     n_l, ms_tot, fl_tot = agg[kid]
@@ -199,7 +206,8 @@ def bench_vitb(args):
         "config": {"workload": "vit-b16-kron-update-apply", "weights": "12 x {768x2304, 768x768, 768x3072, 3072x768}",
                    "blocks": args.blocks, "grad_dtype": "bf16", "factor_dtype": "fp32", "max_size": 8192,
                    "max_skew": args.skew, "update_probability": 1.0, "procrustes": "r2" if args.r2 else "step2",
-                   "term1_q": "pg" if args.t1q_pg else "term1",
+                   "term1_q": "pg" if args.t1q_pg else "term1", "fuse_groups": bool(args.fuse),
+                   "update_side_streams": args.upd_streams,
                    "parallelism": "none"},
         "gpu_ms_per_step": round(ev_ms, 3),
         "streams": args.streams,

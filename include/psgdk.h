@@ -28,6 +28,7 @@ typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
 
 #define PSGDK_VERSION 1
 #define PSGDK_MAXB 16 /* problems per grouped call */
+#define PSGDK_MAX_GROUPS 64 /* groups per psgdk_kron2d_update_groups call */
 #define PSGDK_NLB_K 32 /* rows of the random start of the norm lower bounds */
 
 enum { PSGDK_OK = 0, PSGDK_EINVAL = 1, PSGDK_ESHAPE = 2, PSGDK_EHIP = 3, PSGDK_EWORKSPACE = 4 };
@@ -157,6 +158,20 @@ typedef struct psgdk_apply_opts {
 int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
                         const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
 
+/* The update of several groups in one call: the same operation as psgdk_kron2d_update on each group, with the
+ * factor work of all groups batched by factor side (each launch covers up to 64 factors of one side, from any
+ * group and either dimension). Every group must be on the bf16 path (prec bf16, two dense factors with Qt16 / P16
+ * shadows, sides multiples of 8, tri = 0); lr, betaL, r2 and tri must agree across opts[]; damping and grad_eps
+ * are per group. noise[g] and V[g] are the group's arrays as in psgdk_kron2d_update. Results are bitwise those of
+ * one psgdk_kron2d_update per group. The work runs on side streams the library creates once per device (default
+ * priority; psgdk_set_option 6), forked from and joined back to `stream` with events; while `stream` is being
+ * captured into a HIP graph, everything runs on `stream` itself. Replaces the per-parameter
+ * loop of update_2d calls
+ * (psgd_pro_fast.py:351-368; the reference's batch=True stacks same-shape parameters, psgd_pro_fast.py:327-349). */
+int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
+                               const psgdk_update_opts_t* const* opts, const float* const* const* noise,
+                               const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+
 /* Precondition, clip and update: pre = P1 G P2 (apply_2d, psgd_pro_fast.py:156-161 = precond_grad_kron,
  * psgd_pro.py:107-112), clip to RMS <= max_avg_amp and |.| <= max_element_amp, param -= lr_params * clipped
  * (psgd_pro.py:371-381). pre_out[b] / clipped_out[b] (m x n fp32, optional: NULL array or NULL entries) receive
@@ -232,7 +247,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * norm bounds (-1 by shape, 0 split-K products plus a reduce kernel, 1 one workgroup per 64 output columns over the
  * whole k range; shapes the column kernel cannot read take the split-K kernel); option 5 = how the bf16 update
  * forms term1 Q for a factor whose other side m is under half of its side d (1, default: Pg^T (Pg Q) or Pg (Pg^T Q),
- * 4 m d^2 flops; 0: term1 Q, 2 d^3 flops). */
+ * 4 m d^2 flops; 0: term1 Q, 2 d^3 flops); option 6 = side streams of psgdk_kron2d_update_groups (default 3; 0 or
+ * 1: everything on the caller's stream). */
 int psgdk_set_option(int option, int value);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,

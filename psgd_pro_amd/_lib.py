@@ -12,6 +12,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("PSGDK_LIB", os.path.join(_HERE, "libpsgdk.so"))
 
 MAXB = 16
+MAX_GROUPS = 64
 NLB_K = 32
 OK, EINVAL, ESHAPE, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 F32, BF16 = 0, 1
@@ -63,6 +64,8 @@ _SIGS = {
     "psgdk_norm_lower_bound_full": (_i32, [_i64, _i32, _i32, _vpa, _i64, _i32, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_unpack": (_i32, [_i64, _i32, _vpa, _vpa, _i64, _vp]),
     "psgdk_kron2d_update": (_i32, [C.POINTER(Kron2d), C.POINTER(UpdateOpts), _vpa, _vpa, _vp, _szp, _vp]),
+    "psgdk_kron2d_update_groups": (_i32, [_i32, C.POINTER(C.POINTER(Kron2d)), C.POINTER(C.POINTER(UpdateOpts)),
+                                          C.POINTER(_vpa), C.POINTER(_vpa), _vp, _szp, _vp]),
     "psgdk_kron2d_apply": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_apply2d": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_factor_update": (_i32, [_i32, _i64, _i32, _vpa, _i32, _vpa, _vpa, _vpa, _vpa, C.c_float, C.c_float,

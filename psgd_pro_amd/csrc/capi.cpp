@@ -74,8 +74,8 @@ bool vec_ok(P const* ptrs, int nb, int64_t ld, int dt) {
   return true;
 }
 
-int check_nb(int nb) {
-  if (nb < 1 || nb > MAXB) return fail(PSGDK_EINVAL, "nb = %d: must be in 1..%d", nb, MAXB);
+int check_nb(int nb) {  // problems per public call (a launch may batch several calls' problems, up to MAXB)
+  if (nb < 1 || nb > PSGDK_MAXB) return fail(PSGDK_EINVAL, "nb = %d: must be in 1..%d", nb, PSGDK_MAXB);
   return PSGDK_OK;
 }
 int check_prec(int prec) {
@@ -204,6 +204,34 @@ int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A
 int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
 int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape, 0 split-K + reduce, 1 column blocks
 int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
+int g_upd_streams = 3;    // psgdk_set_option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
+
+// Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
+// until the process ends. A call forks from the caller's stream with an event and joins back with one event per
+// side stream, so it stays ordered with the caller's other work and can be captured into a HIP graph.
+struct SideStreams {
+  std::vector<hipStream_t> s;
+  std::vector<hipEvent_t> ev;  // 1 fork + per side stream 2 (phase join, final join)
+};
+int side_streams(int n, SideStreams** out) {
+  static std::vector<SideStreams> per_dev;
+  int dev = 0;
+  PSGDK_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
+  SideStreams& ss = per_dev[dev];
+  while ((int)ss.s.size() < n) {
+    hipStream_t t;
+    PSGDK_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking), "side stream");
+    ss.s.push_back(t);
+  }
+  while ((int)ss.ev.size() < 1 + 2 * n) {
+    hipEvent_t e;
+    PSGDK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "side stream event");
+    ss.ev.push_back(e);
+  }
+  *out = &ss;
+  return PSGDK_OK;
+}
 
 int b16_cfg(int64_t M, int64_t N, int tri, int nb) {
   if (g_force_cfg >= 0) return g_force_cfg;
@@ -584,184 +612,160 @@ int refresh_p_diag(const psgdk_kron2d_t* g, int f, const int* sel, int nsel, hip
   return hip_check(diag_scale_launch(a, st), "diag P refresh");
 }
 
-// One preconditioner update of a bf16-path group (b16_group): every contraction on gemm_bf16 with k-contiguous bf16
+// One preconditioner update of bf16-path groups (b16_group): every contraction on gemm_bf16 with k-contiguous bf16
 // operands; producers write the bf16 (and transposed) copies their consumers read.
-//   X  = G + (damping + eps |G|) N                      -> Xb
-//   Y  = X P2            (A = Xb,   B = P2 shadow)      -> Y^T bf16
-//   Pg = P1 Y            (A = P1 shadow, B = Y^T)       -> Pg bf16, Pg^T bf16
-//   per factor: term1 = SYRK (Pg or Pg^T) -> bf16; bound, L, lr/L; Qn = Q - lr/L (term1 Q - term2 Q)
-//   (B = Q^T shadow; when the other side is under half of d, term1 Q is formed as Pg^T (Pg Q) or Pg (Pg^T Q))
-//   -> fp32 + Qn^T bf16; R = Qn^T - Qn -> bf16; skew bound; RQ (B = Qn^T) -> fp32 + RQ^T bf16 + traces; step
-//   size; Q = Qn + a RQ + a^2/2 R RQ (B = RQ^T) -> Q fp32 + Q^T shadow (r2: S = Rn^T Rn by SYRK, Q + M Q)
-//   P = Q^T Q (SYRK of the Q^T shadow) -> P shadow
-int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
-               const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st) {
-  const int nb = g->nb;
-  const int64_t m = g->m, n = g->n, mn = m * n, dmx = std::max(m, n);
-  const int64_t dims[2] = {m, n};
-  Ws w(ws);
-  bf16_t *Xb[MAXB], *YTb[MAXB], *Pgb[MAXB], *PgTb[MAXB], *T1b[MAXB], *QnTb[MAXB], *Rb[MAXB], *RQTb[MAXB];
-  float *Qn[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *rtp[MAXB];
-  const int tp = gemm_bf16_tiles(dmx, dmx, 0, 1);
-  for (int b = 0; b < nb; ++b) {
-    Xb[b] = w.take<bf16_t>(mn);
-    YTb[b] = w.take<bf16_t>(mn);
-    Pgb[b] = w.take<bf16_t>(mn);
-    PgTb[b] = w.take<bf16_t>(mn);
-    T1b[b] = w.take<bf16_t>(dmx * dmx);
-    QnTb[b] = w.take<bf16_t>(dmx * dmx);
-    Rb[b] = w.take<bf16_t>(dmx * dmx);
-    RQTb[b] = w.take<bf16_t>(dmx * dmx);
-    Qn[b] = w.take<float>(dmx * dmx);
-    RQ[b] = w.take<float>(dmx * dmx);
-    coef[b] = w.take<float>(4);
-    rs[b] = w.take<float>(4);
-    pc[b] = w.take<float>(8);
-    tpart[b] = w.take<float>(2 * (size_t)tp);
-    rtp[b] = w.take<float>(rform_pairs(dmx));
+//   per group:  X  = G + (damping + eps |G|) N                      -> Xb
+//               Y  = X P2            (A = Xb,   B = P2 shadow)      -> Y^T bf16
+//               Pg = P1 Y            (A = P1 shadow, B = Y^T)       -> Pg bf16, Pg^T bf16
+//   per dense factor of every parameter (an item), batched over the items of one factor side d (all groups,
+//   both factors, up to MAXB items per launch): term1 = SYRK (Pg or Pg^T) -> bf16; bound, L, lr/L;
+//   Qn = Q - lr/L (term1 Q - term2 Q) (B = Q^T shadow; when the other side is under half of d, term1 Q is formed
+//   as Pg^T (Pg Q) or Pg (Pg^T Q)) -> fp32 + Qn^T bf16; R = Qn^T - Qn -> bf16; skew bound; RQ (B = Qn^T) -> fp32 +
+//   RQ^T bf16 + traces; step size; Q = Qn + a RQ + a^2/2 R RQ (B = RQ^T) -> Q fp32 + Q^T shadow (r2: S = Rn^T Rn
+//   by SYRK, Q + M Q); P = Q^T Q (SYRK of the Q^T shadow) -> P shadow.
+// The items are independent after Pg, and every kernel computes each problem of a launch on its own, so the
+// results do not depend on how the items are batched.
+struct B16Item {
+  int64_t d = 0, other = 0;
+  float term2 = 0.f;
+  const bf16_t* pcol = nullptr;  // d x other rows (k = other): term1 = pcol pcol^T
+  const bf16_t* prow = nullptr;  // other x d rows (k = d): term1 = pcol prow
+  float* Q = nullptr;
+  float* L = nullptr;
+  bf16_t* Qt16 = nullptr;
+  bf16_t* P16 = nullptr;
+  const float* Vs = nullptr;  // 32 x d starts of the SPD and the skew bound
+  const float* Vk = nullptr;
+  bf16_t *T1b = nullptr, *QnTb = nullptr, *Rb = nullptr, *RQTb = nullptr;
+  float *Qn = nullptr, *RQ = nullptr, *coef = nullptr, *rs = nullptr, *pc = nullptr, *tpart = nullptr,
+        *rtp = nullptr;
+};
+
+// Phases of one batch of items with a common side d (n <= MAXB).
+int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, const NlbWs& nw, hipStream_t st) {
+  const int nb = (int)it.size();
+  const int64_t d = it[0]->d;
+  const void *A[MAXB], *B[MAXB];
+  // term1 = pcol pcol^T, full symmetric bf16 (its only consumers read bf16): one launch per distinct other side
+  for (int i0 = 0; i0 < nb;) {
+    int k = 0;
+    int idx[MAXB];
+    const int64_t other = it[i0]->other;
+    for (int i = i0; i < nb; ++i)
+      if (it[i]->other == other) idx[k++] = i;
+    B16Out out;
+    out.ldcb = d;
+    for (int j = 0; j < k; ++j) { A[j] = it[idx[j]]->pcol; out.Cb[j] = it[idx[j]]->T1b; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(k, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
+    while (i0 < nb && it[i0]->other == other) ++i0;  // items arrive sorted by other side within a batch
   }
-  NlbWs nw;
-  nlb_take(w, dmx, nb, nw);
-  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
-  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
-  PSGDK_TRY(check_ptrs(noise, nb, "noise"));
-  PSGDK_TRY(check_ptrs(V, nb, "V"));
   {
+    NlbFinal fin;
+    std::memset(&fin, 0, sizeof fin);
+    fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL;
+    const void* T1c[MAXB];
+    const float* Vs[MAXB];
+    for (int b = 0; b < nb; ++b) {
+      fin.L[b] = it[b]->L; fin.coef[b] = it[b]->coef; fin.term2[b] = it[b]->term2;
+      T1c[b] = it[b]->T1b; Vs[b] = it[b]->Vs;
+    }
+    PSGDK_TRY(run_nlb_full(d, 1, nb, T1c, d, 1, Vs, fin, nw, st));
+  }
+  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16; items whose other side is under half of d form
+  // term1 Q = pcol (prow Q): 4 other d^2 flops instead of 2 d^3, the same product associated the other way
+  for (int i0 = 0; i0 < nb;) {
+    const int64_t other = it[i0]->other;
+    int k = 0;
+    int idx[MAXB];
+    for (int i = i0; i < nb; ++i)
+      if (it[i]->other == other) idx[k++] = i;
+    while (i0 < nb && it[i0]->other == other) ++i0;
+    B16Out out;
+    out.ldc = d; out.ldct = d;
+    EpiSpec e;
+    e.epi = EPI_FACTOR; e.ldx = d;
+    if (g_t1q_pg && 2 * other < d) {
+      {  // Z = prow Q (other x d; B = Q^T shadow) -> Z^T bf16 (d x other) in the RQ^T buffer
+        B16Out zo;
+        zo.ldct = other;
+        for (int j = 0; j < k; ++j) { A[j] = it[idx[j]]->prow; B[j] = it[idx[j]]->Qt16; zo.CTb[j] = it[idx[j]]->RQTb; }
+        EpiSpec ze;
+        PSGDK_TRY(run_b16(k, other, d, d, A, d, B, d, zo, ze, 0, 0, nullptr, st));
+      }
+      for (int j = 0; j < k; ++j) {
+        const B16Item* x = it[idx[j]];
+        A[j] = x->pcol; B[j] = x->RQTb; out.C[j] = x->Qn; out.CTb[j] = x->QnTb; e.X1[j] = x->Q; e.s[j] = x->coef;
+      }
+      PSGDK_TRY(run_b16(k, d, d, other, A, other, B, other, out, e, 0, 0, nullptr, st));
+    } else {
+      for (int j = 0; j < k; ++j) {
+        const B16Item* x = it[idx[j]];
+        A[j] = x->T1b; B[j] = x->Qt16; out.C[j] = x->Qn; out.CTb[j] = x->QnTb; e.X1[j] = x->Q; e.s[j] = x->coef;
+      }
+      PSGDK_TRY(run_b16(k, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+    }
+  }
+  {  // R = Qn^T - Qn -> bf16 (r2: and the partials of sum R * Qn)
     EwArgs a;
     std::memset(&a, 0, sizeof a);
-    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = o->damping; a.f1 = o->grad_eps;
-    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[b]; a.out2[b] = Xb[b]; }
-    PSGDK_HIP(noise_launch(a, st), "noise");
+    a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
+    for (int b = 0; b < nb; ++b) { a.in[b] = it[b]->Qn; a.out2[b] = it[b]->Rb; a.sc[b] = o->r2 ? it[b]->rtp : nullptr; }
+    PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
   }
-  const void *A[MAXB], *B[MAXB];
-  {  // Y = X P2 -> Y^T
-    B16Out out;
-    out.ldct = m;
-    for (int b = 0; b < nb; ++b) { A[b] = Xb[b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[b]; }
-    EpiSpec e;
-    PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+  {
+    NlbFinal fin;
+    std::memset(&fin, 0, sizeof fin);
+    fin.mode = NLB_FINAL_SCALE;
+    const void* Rc[MAXB];
+    const float* Vk[MAXB];
+    for (int b = 0; b < nb; ++b) { fin.coef[b] = it[b]->rs; Rc[b] = it[b]->Rb; Vk[b] = it[b]->Vk; }
+    PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st));
   }
-  {  // Pg = P1 Y -> Pg, Pg^T
-    B16Out out;
-    out.ldcb = n; out.ldct = m;
-    for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[b]; out.Cb[b] = Pgb[b]; out.CTb[b] = PgTb[b]; }
-    EpiSpec e;
-    PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, nullptr, st));
-  }
-  int64_t voff = 0;
-  for (int f = 0; f < 2; ++f) {
-    const int64_t d = dims[f], other = dims[1 - f];
-    const float term2 = (float)mn / (float)d;
-    {  // term1 = Pg Pg^T (f = 0) or Pg^T Pg (f = 1), full symmetric bf16 (its only consumers read bf16)
+  if (o->r2) {  // procrustes_step_r2 (psgd_pro_fast.py:141-153)
+    // S = rs^2 R R^T in the RQ^T buffer (bf16); M = a rs R - a^2/2 S in the (unused) fp32 RQ buffer, as bf16
+    int nt = 0;
+    {  // S = rs^2 R R^T (SYRK of R's rows, scaled in the epilogue) -> bf16 mirrored, partials of sum S * Qn
       B16Out out;
       out.ldcb = d;
-      for (int b = 0; b < nb; ++b) { A[b] = f == 0 ? (const void*)Pgb[b] : (const void*)PgTb[b]; out.Cb[b] = T1b[b]; }
       EpiSpec e;
-      PSGDK_TRY(run_b16(nb, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
+      e.epi = EPI_STRACE; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        A[b] = it[b]->Rb; out.Cb[b] = it[b]->RQTb; e.X1[b] = it[b]->Qn; e.s[b] = it[b]->rs; e.part[b] = it[b]->tpart;
+      }
+      PSGDK_TRY(run_b16(nb, d, d, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, &nt, st));
     }
-    const float *Vs[MAXB], *Vk[MAXB];
-    for (int b = 0; b < nb; ++b) { Vs[b] = V[b] + voff; Vk[b] = V[b] + voff + NLB_K * d; }
-    voff += 2 * NLB_K * d;
     {
-      NlbFinal fin;
-      std::memset(&fin, 0, sizeof fin);
-      fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL; fin.term2 = term2;
-      const void* T1c[MAXB];
-      for (int b = 0; b < nb; ++b) { fin.L[b] = g->L[f][b]; fin.coef[b] = coef[b]; T1c[b] = T1b[b]; }
-      PSGDK_TRY(run_nlb_full(d, 1, nb, T1c, d, 1, Vs, fin, nw, st));
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.i0 = (int)rform_pairs(d); a.i1 = nt; a.f0 = 0.125f;
+      for (int b = 0; b < nb; ++b) {
+        a.in2[b] = it[b]->rtp; a.in3[b] = it[b]->tpart; a.sc[b] = it[b]->rs; a.out[b] = it[b]->pc;
+      }
+      PSGDK_HIP(proc_scalar_r2_launch(a, st), "procrustes r2 step size");
     }
-    if (g_t1q_pg && 2 * other < d) {
-      // term1 Q = Pcol (Prow Q) with term1 = Pcol Prow (Pcol = Pg^T, Prow = Pg for f = 1; Pcol = Pg, Prow = Pg^T
-      // for f = 0): 4 other d^2 flops instead of 2 d^3, the same product associated the other way.
-      // Z = Prow Q (other x d; B = Q^T shadow) -> Z^T bf16 (d x other) in the RQ^T buffer, then
-      // Qn = Q - lr/L (Pcol Z - term2 Q) (A = Pcol, B = Z^T) -> fp32 + Qn^T bf16
-      {
-        B16Out out;
-        out.ldct = other;
-        for (int b = 0; b < nb; ++b) {
-          A[b] = f == 1 ? (const void*)Pgb[b] : (const void*)PgTb[b];
-          B[b] = g->Qt16[f][b];
-          out.CTb[b] = RQTb[b];
-        }
-        EpiSpec e;
-        PSGDK_TRY(run_b16(nb, other, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = d; a.n = d; a.dt = PSGDK_BF16;
+      for (int b = 0; b < nb; ++b) {
+        a.in[b] = it[b]->Rb; a.in2[b] = reinterpret_cast<const float*>(it[b]->RQTb); a.out2[b] = it[b]->RQ;
+        a.sc[b] = it[b]->pc;
       }
+      PSGDK_HIP(mform_launch(a, st), "M = a rs R - a^2/2 S");
+    }
+    {  // Q = Qn + M Qn -> Q fp32 + Q^T shadow
       B16Out out;
       out.ldc = d; out.ldct = d;
       EpiSpec e;
       e.epi = EPI_FACTOR; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
-        A[b] = f == 1 ? (const void*)PgTb[b] : (const void*)Pgb[b];
-        B[b] = RQTb[b]; out.C[b] = Qn[b]; out.CTb[b] = QnTb[b];
-        e.X1[b] = g->Q[f][b]; e.s[b] = coef[b];
-      }
-      PSGDK_TRY(run_b16(nb, d, d, other, A, other, B, other, out, e, 0, 0, nullptr, st));
-    } else {  // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16
-      B16Out out;
-      out.ldc = d; out.ldct = d;
-      EpiSpec e;
-      e.epi = EPI_FACTOR; e.ldx = d;
-      for (int b = 0; b < nb; ++b) {
-        A[b] = T1b[b]; B[b] = g->Qt16[f][b]; out.C[b] = Qn[b]; out.CTb[b] = QnTb[b];
-        e.X1[b] = g->Q[f][b]; e.s[b] = coef[b];
+        A[b] = it[b]->RQ; B[b] = it[b]->QnTb; out.C[b] = it[b]->Q; out.CTb[b] = it[b]->Qt16;
+        e.X1[b] = it[b]->Qn; e.s[b] = it[b]->pc + 2;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
-    {  // R = Qn^T - Qn -> bf16 (r2: and the partials of sum R * Qn)
-      EwArgs a;
-      std::memset(&a, 0, sizeof a);
-      a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-      for (int b = 0; b < nb; ++b) { a.in[b] = Qn[b]; a.out2[b] = Rb[b]; a.sc[b] = o->r2 ? rtp[b] : nullptr; }
-      PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
-    }
-    {
-      NlbFinal fin;
-      std::memset(&fin, 0, sizeof fin);
-      fin.mode = NLB_FINAL_SCALE;
-      const void* Rc[MAXB];
-      for (int b = 0; b < nb; ++b) { fin.coef[b] = rs[b]; Rc[b] = Rb[b]; }
-      PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st));
-    }
-    if (o->r2) {  // procrustes_step_r2 (psgd_pro_fast.py:141-153)
-      bf16_t* Sb[MAXB];  // S = rs^2 R R^T, bf16, in the RQ^T buffer
-      bf16_t* Mb[MAXB];  // M = a rs R - a^2/2 S, bf16, in the (unused) fp32 RQ buffer
-      for (int b = 0; b < nb; ++b) { Sb[b] = RQTb[b]; Mb[b] = reinterpret_cast<bf16_t*>(RQ[b]); }
-      int nt = 0;
-      {  // S = rs^2 R R^T (SYRK of R's rows, scaled in the epilogue) -> bf16 mirrored, partials of sum S * Qn
-        B16Out out;
-        out.ldcb = d;
-        EpiSpec e;
-        e.epi = EPI_STRACE; e.ldx = d;
-        for (int b = 0; b < nb; ++b) { A[b] = Rb[b]; out.Cb[b] = Sb[b]; e.X1[b] = Qn[b]; e.s[b] = rs[b]; e.part[b] = tpart[b]; }
-        PSGDK_TRY(run_b16(nb, d, d, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, &nt, st));
-      }
-      {
-        EwArgs a;
-        std::memset(&a, 0, sizeof a);
-        a.nb = nb; a.i0 = (int)rform_pairs(d); a.i1 = nt; a.f0 = 0.125f;
-        for (int b = 0; b < nb; ++b) { a.in2[b] = rtp[b]; a.in3[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
-        PSGDK_HIP(proc_scalar_r2_launch(a, st), "procrustes r2 step size");
-      }
-      {
-        EwArgs a;
-        std::memset(&a, 0, sizeof a);
-        a.nb = nb; a.m = d; a.n = d; a.dt = PSGDK_BF16;
-        for (int b = 0; b < nb; ++b) { a.in[b] = Rb[b]; a.in2[b] = reinterpret_cast<const float*>(Sb[b]); a.out2[b] = Mb[b]; a.sc[b] = pc[b]; }
-        PSGDK_HIP(mform_launch(a, st), "M = a rs R - a^2/2 S");
-      }
-      {  // Q = Qn + M Qn -> Q fp32 + Q^T shadow
-        B16Out out;
-        out.ldc = d; out.ldct = d;
-        EpiSpec e;
-        e.epi = EPI_FACTOR; e.ldx = d;
-        for (int b = 0; b < nb; ++b) {
-          A[b] = Mb[b]; B[b] = QnTb[b]; out.C[b] = g->Q[f][b]; out.CTb[b] = reinterpret_cast<bf16_t*>(g->Qt16[f][b]);
-          e.X1[b] = Qn[b]; e.s[b] = pc[b] + 2;
-        }
-        PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
-      }
-      continue;
-    }
+  } else {
     int nt = 0;
     {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials (tr(R RQ) reads the bf16 R of the product)
       B16Out out;
@@ -769,8 +773,8 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       EpiSpec e;
       e.epi = EPI_RQ; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
-        A[b] = Rb[b]; B[b] = QnTb[b]; out.C[b] = RQ[b]; out.CTb[b] = RQTb[b];
-        e.X1[b] = reinterpret_cast<const float*>(Rb[b]); e.s[b] = rs[b]; e.part[b] = tpart[b];
+        A[b] = it[b]->Rb; B[b] = it[b]->QnTb; out.C[b] = it[b]->RQ; out.CTb[b] = it[b]->RQTb;
+        e.X1[b] = reinterpret_cast<const float*>(it[b]->Rb); e.s[b] = it[b]->rs; e.part[b] = it[b]->tpart;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, &nt, st));
     }
@@ -778,7 +782,7 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       EwArgs a;
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.i0 = nt; a.f0 = 0.125f;
-      for (int b = 0; b < nb; ++b) { a.in2[b] = tpart[b]; a.sc[b] = rs[b]; a.out[b] = pc[b]; }
+      for (int b = 0; b < nb; ++b) { a.in2[b] = it[b]->tpart; a.sc[b] = it[b]->rs; a.out[b] = it[b]->pc; }
       PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
     }
     {  // Q = Qn + a RQ + a^2/2 R RQ -> Q fp32 + Q^T shadow
@@ -787,25 +791,145 @@ int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const floa
       EpiSpec e;
       e.epi = EPI_PROC; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
-        A[b] = Rb[b]; B[b] = RQTb[b]; out.C[b] = g->Q[f][b]; out.CTb[b] = reinterpret_cast<bf16_t*>(g->Qt16[f][b]);
-        e.X1[b] = Qn[b]; e.X2[b] = RQ[b]; e.s[b] = pc[b];
+        A[b] = it[b]->Rb; B[b] = it[b]->RQTb; out.C[b] = it[b]->Q; out.CTb[b] = it[b]->Qt16;
+        e.X1[b] = it[b]->Qn; e.X2[b] = it[b]->RQ; e.s[b] = it[b]->pc;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
   }
-  for (int f = 0; f < 2; ++f) {  // P16 = bf16(Q^T Q) from the fresh Q^T shadow (its only per-step reader reads bf16;
-                                 // fp32 P is written by psgdk_kron2d_refresh_p / _balance from the same shadow)
-    const int64_t d = dims[f];
+  {  // P16 = bf16(Q^T Q) from the fresh Q^T shadow (its only per-step reader reads bf16; fp32 P is written by
+     // psgdk_kron2d_refresh_p / _balance from the same shadow)
     B16Out out;
     out.ldcb = d;
-    for (int b = 0; b < nb; ++b) {
-      A[b] = g->Qt16[f][b];
-      out.Cb[b] = reinterpret_cast<bf16_t*>(g->P16[f][b]);
-    }
+    for (int b = 0; b < nb; ++b) { A[b] = it[b]->Qt16; out.Cb[b] = it[b]->P16; }
     EpiSpec e;
     PSGDK_TRY(run_b16(nb, d, d, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
   }
   return PSGDK_OK;
+}
+
+// The update of ng bf16-path groups: per-group noise, Y and Pg, then the items of every dense factor in batches of
+// one side d (largest first), the items of a batch ordered by their other side.
+int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_update_opts_t* const* os,
+                      const float* const* const* noise, const float* const* const* V, void* ws, size_t* ws_bytes,
+                      hipStream_t st) {
+  Ws w(ws);
+  std::vector<std::vector<bf16_t*>> Xb(ng), YTb(ng), Pgb(ng), PgTb(ng);
+  std::vector<B16Item> items;
+  for (int gi = 0; gi < ng; ++gi) {
+    const psgdk_kron2d_t* g = gs[gi];
+    const int64_t mn = g->m * g->n;
+    for (int b = 0; b < g->nb; ++b) {
+      Xb[gi].push_back(w.take<bf16_t>(mn));
+      YTb[gi].push_back(w.take<bf16_t>(mn));
+      Pgb[gi].push_back(w.take<bf16_t>(mn));
+      PgTb[gi].push_back(w.take<bf16_t>(mn));
+    }
+    for (int b = 0; b < g->nb; ++b) {
+      int64_t voff = 0;
+      for (int f = 0; f < 2; ++f) {
+        B16Item x;
+        x.d = f == 0 ? g->m : g->n;
+        x.other = f == 0 ? g->n : g->m;
+        x.term2 = (float)mn / (float)x.d;
+        x.pcol = f == 0 ? Pgb[gi][b] : PgTb[gi][b];
+        x.prow = f == 0 ? PgTb[gi][b] : Pgb[gi][b];
+        x.Q = g->Q[f][b]; x.L = g->L[f][b];
+        x.Qt16 = reinterpret_cast<bf16_t*>(g->Qt16[f][b]); x.P16 = reinterpret_cast<bf16_t*>(g->P16[f][b]);
+        if (V) { x.Vs = V[gi][b] + voff; x.Vk = V[gi][b] + voff + NLB_K * x.d; }
+        voff += 2 * NLB_K * x.d;
+        const int64_t dd = x.d * x.d;
+        x.T1b = w.take<bf16_t>(dd); x.QnTb = w.take<bf16_t>(dd); x.Rb = w.take<bf16_t>(dd); x.RQTb = w.take<bf16_t>(dd);
+        x.Qn = w.take<float>(dd); x.RQ = w.take<float>(dd);
+        x.coef = w.take<float>(4); x.rs = w.take<float>(4); x.pc = w.take<float>(8);
+        x.tpart = w.take<float>(2 * (size_t)gemm_bf16_tiles(x.d, x.d, 0, 1));
+        x.rtp = w.take<float>(rform_pairs(x.d));
+        items.push_back(x);
+      }
+    }
+  }
+  // batches: items sorted by (d descending, other), cut into runs of one d of at most MAXB
+  std::vector<B16Item*> order;
+  for (auto& x : items) order.push_back(&x);
+  std::stable_sort(order.begin(), order.end(), [](const B16Item* a, const B16Item* b) {
+    return a->d != b->d ? a->d > b->d : a->other < b->other;
+  });
+  std::vector<std::vector<B16Item*>> batches;
+  for (size_t i = 0; i < order.size();) {
+    std::vector<B16Item*> bt;
+    const int64_t d = order[i]->d;
+    while (i < order.size() && order[i]->d == d && (int)bt.size() < MAXB) bt.push_back(order[i++]);
+    batches.push_back(bt);
+  }
+  std::vector<NlbWs> nws(batches.size());
+  for (size_t k = 0; k < batches.size(); ++k) nlb_take(w, batches[k][0]->d, (int)batches[k].size(), nws[k]);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  for (int gi = 0; gi < ng; ++gi) {
+    PSGDK_TRY(check_ptrs(noise[gi], gs[gi]->nb, "noise"));
+    PSGDK_TRY(check_ptrs(V[gi], gs[gi]->nb, "V"));
+  }
+  // streams: the per-group phase of group gi and batch k run on side stream gi % S and k % S; every batch starts
+  // after every group's Pg exists. Under HIP graph capture everything stays on the caller's stream: a capture that
+  // forked onto these side streams ended in a host-side crash inside the end of the capture, so that combination
+  // is not used.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PSGDK_HIP(hipStreamIsCapturing(st, &cap), "capture status");
+  const int S = cap != hipStreamCaptureStatusNone ? 1 : std::min<int>(g_upd_streams, std::max<int>(ng, (int)batches.size()));
+  SideStreams* ss = nullptr;
+  if (S > 1) {
+    PSGDK_TRY(side_streams(S, &ss));
+    PSGDK_HIP(hipEventRecord(ss->ev[0], st), "fork");
+    for (int i = 0; i < S; ++i) PSGDK_HIP(hipStreamWaitEvent(ss->s[i], ss->ev[0], 0), "fork wait");
+  }
+  auto lane = [&](int i) { return S > 1 ? ss->s[i % S] : st; };
+  for (int gi = 0; gi < ng; ++gi) {
+    const psgdk_kron2d_t* g = gs[gi];
+    const int nb = g->nb;
+    const int64_t m = g->m, n = g->n;
+    hipStream_t st = lane(gi);
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
+      for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.out2[b] = Xb[gi][b]; }
+      PSGDK_HIP(noise_launch(a, st), "noise");
+    }
+    const void *A[MAXB], *B[MAXB];
+    {  // Y = X P2 -> Y^T
+      B16Out out;
+      out.ldct = m;
+      for (int b = 0; b < nb; ++b) { A[b] = Xb[gi][b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[gi][b]; }
+      EpiSpec e;
+      PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+    }
+    {  // Pg = P1 Y -> Pg, Pg^T
+      B16Out out;
+      out.ldcb = n; out.ldct = m;
+      for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[gi][b]; out.Cb[b] = Pgb[gi][b]; out.CTb[b] = PgTb[gi][b]; }
+      EpiSpec e;
+      PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, nullptr, st));
+    }
+  }
+  if (S > 1) {
+    for (int i = 0; i < S; ++i) PSGDK_HIP(hipEventRecord(ss->ev[1 + i], ss->s[i]), "phase join");
+    for (int i = 0; i < S; ++i)
+      for (int j = 0; j < S; ++j)
+        if (i != j) PSGDK_HIP(hipStreamWaitEvent(ss->s[i], ss->ev[1 + j], 0), "phase join wait");
+  }
+  for (size_t k = 0; k < batches.size(); ++k) PSGDK_TRY(b16_items(batches[k], os[0], nws[k], lane((int)k)));
+  if (S > 1) {
+    for (int i = 0; i < S; ++i) {
+      PSGDK_HIP(hipEventRecord(ss->ev[1 + S + i], ss->s[i]), "join");
+      PSGDK_HIP(hipStreamWaitEvent(st, ss->ev[1 + S + i], 0), "join wait");
+    }
+  }
+  return PSGDK_OK;
+}
+
+int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+               const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st) {
+  return b16_update_groups(1, &g, &o, &noise, &V, ws, ws_bytes, st);
 }
 
 // Precondition + clip + update of a bf16-path group: Y = G P2 (A = G bf16, B = P2 shadow) -> Y^T bf16;
@@ -896,8 +1020,8 @@ int factor_update_run(int prec, int nb, int64_t d, const float* const* T1, int t
   {
     NlbFinal fin;
     std::memset(&fin, 0, sizeof fin);
-    fin.mode = NLB_FINAL_FACTOR; fin.lr = lr; fin.beta = betaL; fin.term2 = term2;
-    for (int b = 0; b < nb; ++b) { fin.L[b] = Lv[b]; fin.coef[b] = w.coef[b]; }
+    fin.mode = NLB_FINAL_FACTOR; fin.lr = lr; fin.beta = betaL;
+    for (int b = 0; b < nb; ++b) { fin.L[b] = Lv[b]; fin.coef[b] = w.coef[b]; fin.term2[b] = term2; }
     if (t1_tri) PSGDK_TRY(run_nlb(d, 1, nb, T1, d, false, V, fin, w.nw, st));
     else PSGDK_TRY(run_nlb_full(d, 1, nb, reinterpret_cast<const void* const*>(T1), d, 0, V, fin, w.nw, st));
   }
@@ -1312,6 +1436,28 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
   return PSGDK_OK;
 }
 
+int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
+                               const psgdk_update_opts_t* const* opts, const float* const* const* noise,
+                               const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
+  if (ngroups < 1 || ngroups > PSGDK_MAX_GROUPS)
+    return fail(PSGDK_EINVAL, "ngroups = %d: must be in 1..%d", ngroups, PSGDK_MAX_GROUPS);
+  if (!groups || !opts) return fail(PSGDK_EINVAL, "null groups or options");
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  for (int i = 0; i < ngroups; ++i) {
+    PSGDK_TRY(check_group(groups[i]));
+    const psgdk_update_opts_t* o = opts[i];
+    if (!o) return fail(PSGDK_EINVAL, "null options of group %d", i);
+    if (o->r2 != 0 && o->r2 != 1) return fail(PSGDK_EINVAL, "r2 = %d (0: procrustes_step2, 1: procrustes_step_r2)", o->r2);
+    if (o->lr != opts[0]->lr || o->betaL != opts[0]->betaL || o->r2 != opts[0]->r2 || o->tri != opts[0]->tri)
+      return fail(PSGDK_EINVAL, "group %d: lr, betaL, r2 and tri must be the same for every group of one call", i);
+    if (!b16_group(groups[i], o->tri))
+      return fail(PSGDK_EINVAL, "group %d is not a bf16-path group (bf16 precision, two dense factors with bf16 "
+                  "shadows, sides multiples of 8, full storage)", i);
+  }
+  if (ws && (!noise || !V)) return fail(PSGDK_EINVAL, "null noise or V");
+  return b16_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, (hipStream_t)stream);
+}
+
 int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params,
                        float* const* pre_out, float* const* clipped_out, void* ws, size_t* ws_bytes,
                        psgdk_stream_t stream) {
@@ -1510,6 +1656,11 @@ int psgdk_set_option(int option, int value) {
   if (option == 5) {
     if (value != 0 && value != 1) return fail(PSGDK_EINVAL, "option 5 (term1 Q through Pg) must be 0 or 1");
     g_t1q_pg = value;
+    return PSGDK_OK;
+  }
+  if (option == 6) {
+    if (value < 0 || value > 8) return fail(PSGDK_EINVAL, "option 6 (grouped update side streams) must be 0 .. 8");
+    g_upd_streams = value;
     return PSGDK_OK;
   }
   return fail(PSGDK_EINVAL, "unknown option %d", option);

@@ -4,7 +4,8 @@
 
 namespace psgdk {
 
-constexpr int MAXB = 16;  // problems per grouped launch (kernel-argument space, captured by value)
+constexpr int MAXB = 64;  // problems per grouped launch (pointer arrays in the kernel arguments, by value; the
+                          // largest argument block, the norm bound's final stage, is about 8 KB)
 
 // Epilogues. acc is op(A) op(B) accumulated in fp32; s = the problem's device scalars.
 enum Epi : int {

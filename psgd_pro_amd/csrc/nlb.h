@@ -38,7 +38,8 @@ enum : int { NLB_FINAL_NONE = 0, NLB_FINAL_FACTOR = 1, NLB_FINAL_SCALE = 2 };
 
 struct NlbFinal {
   int mode;
-  float lr, beta, term2;
+  float lr, beta;
+  float term2[MAXB];  // factor: numel / d of each problem
   float* L[MAXB];     // factor: the smoothness EMA (1 float)
   float* coef[MAXB];  // factor: {lr / L, term2}; scale: {1 / (bound + smallest normal)}
 };

@@ -194,12 +194,12 @@ __global__ void __launch_bounds__(64) nlb_final_kernel(const NlbArgs p, NlbFinal
     p.scal[b][NLB_BOUND] = bound;
     if (f.mode == NLB_FINAL_FACTOR) {
       // psgd_pro.py:132-135: ell = bound + term2; L = max(beta L + (1 - beta) ell, ell); coef = lr / L, term2
-      const float ell = bound + f.term2;
+      const float ell = bound + f.term2[b];
       float* L = f.L[b];
       const float Ln = fmaxf(f.beta * L[0] + (1.f - f.beta) * ell, ell);
       L[0] = Ln;
       f.coef[b][0] = f.lr / Ln;
-      f.coef[b][1] = f.term2;
+      f.coef[b][1] = f.term2[b];
     } else if (f.mode == NLB_FINAL_SCALE) {
       // psgd_pro.py:88: R / (bound + smallest normal)
       f.coef[b][0] = 1.f / (bound + kSmallestNormal);

@@ -77,7 +77,8 @@ class KronWhiten:
                  seed=None,
                  tri=None,
                  streams=4,
-                 graphs=False):
+                 graphs=False,
+                 fuse_groups=True):
         self.lr_params = lr_params
         self.lr_preconditioner = lr_preconditioner
         self.betaL = betaL
@@ -118,6 +119,9 @@ class KronWhiten:
             raise ValueError("streams: a count >= 0")
         self._nstreams, self._lanes = int(streams), None
         self._use_graphs = bool(graphs)
+        # one psgdk_kron2d_update_groups call for every bf16-path group: the factor work of all groups is batched
+        # by factor side (results are bitwise those of one call per group)
+        self._fuse = bool(fuse_groups)
         self._graphs, self._seen = {}, set()
         self._draw_buf = None
         self._init_scale = preconditioner_init_scale
@@ -297,12 +301,39 @@ class KronWhiten:
             if ln.stream is not None:
                 cur.wait_stream(ln.stream)
 
+    @staticmethod
+    def _b16(grp):
+        """The group takes the library's bf16 path (its b16_group rule): bf16 shadows of both dense factors exist
+        (bf16 precision, two dense factors, sides multiples of 8, full storage) and every operand is under 2 GiB."""
+        big = max(grp.m, grp.n)
+        return (grp.Qt16[0] is not None and grp.Qt16[1] is not None and big * big * 2 < 2 ** 31
+                and grp.m * grp.n * 2 < 2 ** 31)
+
     def _update(self, srcs, noise, V):
         o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))
         dev = srcs[0].device
         cur, lanes = self._fork(dev)
-        for gi, grp in enumerate(self._groups):
-            ln = lanes[gi % len(lanes)]
+        fused = [g for g in self._groups if self._fuse and self._b16(g)][:L.MAX_GROUPS]
+        rest = [g for g in self._groups if not any(g is f for f in fused)]
+        if fused:
+            ln = lanes[0]
+            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                opts, nzs, vvs = [], [], []
+                for grp in fused:
+                    og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
+                    og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
+                    opts.append(og)
+                    nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
+                    vvs.append(L.ptrs([V[p.index] for p in grp.members]))
+                ng = len(fused)
+                garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
+                oarr = (ctypes.POINTER(L.UpdateOpts) * ng)(*[ctypes.pointer(x) for x in opts])
+                narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
+                varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
+                L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
+                          stream=L.stream_of(srcs[0]))
+        for gi, grp in enumerate(rest):
+            ln = lanes[(gi + (1 if fused else 0)) % len(lanes)]
             with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
                 s = grp.struct
                 gdt = self._bind_sources(grp, srcs)

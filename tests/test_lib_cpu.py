@@ -135,6 +135,37 @@ def test_group_validation():
     assert "r2" in _err()
 
 
+def test_update_groups_validation():
+    """psgdk_kron2d_update_groups refuses a bad group count, options that differ in a shared field, and a group that
+    is not on the bf16 path, with a message, before touching the device."""
+    lib = L.lib()
+    sz = C.c_size_t(0)
+
+    def group(prec=L.PREC_BF16, shadows=True):
+        g = L.Kron2d()
+        g.nb, g.prec, g.m, g.n = 1, prec, 64, 128
+        g.kind[0], g.kind[1] = L.FACTOR_DENSE, L.FACTOR_DENSE
+        g.G[0] = 0x1000
+        for f in range(2):
+            g.Q[f][0] = g.P[f][0] = g.L[f][0] = 0x1000
+            if shadows:
+                g.Qt16[f][0] = g.P16[f][0] = 0x1000
+        return g
+
+    def call(gs, os):
+        ga = (C.POINTER(L.Kron2d) * len(gs))(*[C.pointer(g) for g in gs])
+        oa = (C.POINTER(L.UpdateOpts) * len(os))(*[C.pointer(o) for o in os])
+        return lib.psgdk_kron2d_update_groups(len(gs), ga, oa, None, None, None, C.byref(sz), None)
+
+    o = L.UpdateOpts(0.1, 0.9, 1e-9, 7.8e-3, 0, 0)
+    assert call([group(), group()], [o, o]) == L.OK and sz.value > 0
+    assert lib.psgdk_kron2d_update_groups(0, None, None, None, None, None, C.byref(sz), None) == L.EINVAL
+    o2 = L.UpdateOpts(0.2, 0.9, 1e-9, 7.8e-3, 0, 0)
+    assert call([group(), group()], [o, o2]) == L.EINVAL and "same" in _err()
+    assert call([group(), group(shadows=False)], [o, o]) == L.EINVAL and "bf16" in _err()
+    assert call([group(prec=L.PREC_F32)], [o]) == L.EINVAL
+
+
 def test_python_surface_on_cpu():
     """The optimizer and the ops refuse CPU tensors with a clear error (no silent CPU path)."""
     from psgd_pro_amd import KronWhiten, make_ops
