@@ -300,11 +300,13 @@ def bench_llama(args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     opt._nstreams, opt._use_graphs = 0, False
+    L.check(L.lib().psgdk_set_option(6, 0))  # one stream: each launch's event time is its own
     L.profile_start()
     for _ in range(2):
         opt.step_math(grads)
     torch.cuda.synchronize()
     recs = L.profile_stop()
+    L.check(L.lib().psgdk_set_option(6, args.upd_streams))
     return {"metric": "Kron update+apply ms/step at Llama shapes (4096x4096 + 4096x14336), 1 GPU", "value": round(ms, 3),
             "unit": "ms/step", "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": args.precision,
             "data": "synthetic", "config": {"workload": "llama-4096x4096+4096x14336-kron-update-apply",
