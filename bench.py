@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
     ap.add_argument("--fuse", type=int, default=1,
                     help="0: one update call per weight group instead of one call batching all groups' factor work")
+    ap.add_argument("--tile-cfg", type=int, default=-1,
+                    help="bf16 GEMM tile configuration for every launch (library option 1; -1: chosen by size)")
     ap.add_argument("--upd-streams", type=int, default=3,
                     help="side streams of the grouped update inside the library (library option 6)")
     ap.add_argument("--t1q-pg", type=int, default=1,
@@ -139,6 +141,7 @@ def bench_vitb(args):
     dev = torch.device("cuda:0")
     L.check(L.lib().psgdk_set_option(5, args.t1q_pg))
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
+    L.check(L.lib().psgdk_set_option(1, args.tile_cfg))
     skew = math.inf if args.skew == "inf" else float(args.skew)
     shapes = VIT_B * args.blocks
     gen = torch.Generator().manual_seed(0)

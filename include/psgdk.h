@@ -104,6 +104,14 @@ int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* 
                                 const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
                                 psgdk_stream_t stream);
 
+/* norm_lower_bound_spd (psgd_pro.py:19-41) of P P^T (d x d) given P (d x k bf16, rows k-contiguous) and Pt = P^T
+ * (k x d bf16), without forming P P^T: the squared row norms come from P (P^T P), the diagonal from the rows of P,
+ * row j from P P_j^T, and each product V (P P^T) as (V P) P^T. The bound the bf16 update takes for term1 = Pg Pg^T
+ * or Pg^T Pg when the other side k is under half of d. d and k multiples of 8, 16-byte aligned operands. */
+int psgdk_norm_lower_bound_gram(int64_t d, int64_t k, int nb, const void* const* P, const void* const* Pt,
+                                const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
+                                psgdk_stream_t stream);
+
 /* Full symmetric n x n matrix from its row-major packed upper triangle.
  * Replaces psgd::unpack (kernels/ops.py:112-116, kernels/k2.py:88-103). */
 int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int64_t ldc, psgdk_stream_t stream);

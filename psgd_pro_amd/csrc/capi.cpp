@@ -437,6 +437,66 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
   return PSGDK_OK;
 }
 
+// The SPD bound of term1 = Pc Pc^T (d x d) from its factor Pc (d x k bf16 rows; Pr = Pc^T, k x d rows), without
+// forming term1: the same bound (psgd_pro.py:19-41) on the same matrix, the products associated the other way.
+//   H = Pr Pr^T = Pc^T Pc (k x k, SYRK) -> Hb; W = Pc H -> Wb (d x k); row statistics of term1 (squared row norms
+//   rowsum(W * Pc), diagonal rowsum(Pc * Pc)); argmax j; row j of term1 = Pc Pc_j^T; V0 from it;
+//   4 x { U = V Pc (32 x k), V <- U Pc^T / nf (normalized every second time) }; bound and the consumer's scalars.
+// Needs k, d multiples of 8 and 16-byte aligned operands (the bf16 update's Pg route: k < d / 2).
+int run_nlb_gram(int64_t d, int64_t k, int nb, const bf16_t* const* Pc, const bf16_t* const* Pr, bf16_t* const* Hb,
+                 bf16_t* const* Wb, const float* const* V, const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
+  const void *A[MAXB], *B[MAXB];
+  {  // H = Pr Pr^T (k x k, mirrored bf16)
+    B16Out out;
+    out.ldcb = k;
+    for (int b = 0; b < nb; ++b) { A[b] = Pr[b]; out.Cb[b] = Hb[b]; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, k, k, d, A, d, A, d, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
+  }
+  {  // W = Pc H (d x k bf16)
+    B16Out out;
+    out.ldcb = k;
+    for (int b = 0; b < nb; ++b) { A[b] = Pc[b]; B[b] = Hb[b]; out.Cb[b] = Wb[b]; }
+    EpiSpec e;
+    PSGDK_TRY(run_b16(nb, d, k, k, A, k, B, k, out, e, 0, 0, nullptr, st));
+  }
+  GramArgs ga;
+  std::memset(&ga, 0, sizeof ga);
+  ga.nb = nb; ga.d = (int)d; ga.k = (int)k;
+  for (int b = 0; b < nb; ++b) {
+    ga.P[b] = Pc[b]; ga.W[b] = Wb[b]; ga.rn2[b] = w.rn2[b]; ga.rmax[b] = w.rpart[b]; ga.diag[b] = w.cpart[b];
+    ga.scal[b] = w.scal[b]; ga.aj[b] = reinterpret_cast<bf16_t*>(w.vb1[b]);  // vb1 is free until the first product
+  }
+  for (int stage = 0; stage < 3; ++stage) PSGDK_HIP(gram_launch(ga, stage, st), "gram statistics");
+  const float* Af[MAXB];
+  for (int b = 0; b < nb; ++b) Af[b] = reinterpret_cast<const float*>(ga.aj[b]);
+  NlbArgs a = nlb_args(d, 1, nb, Af, 0, w);  // row stride 0: the init kernel's "row j" is aj itself
+  a.vmm_cols = 1; a.ssc = 64; a.vmm_u = g_vmm_u == 2 ? 2 : 4;
+  for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
+  PSGDK_HIP(nlb_full_launch(a, 1, 1, 0, st), "nlb init");
+  float* const* vb[2] = {w.vb0, w.vb1};
+  float* const* ss[2] = {w.ss0, w.ss1};
+  int cur = 0;
+  for (int it = 0; it < 4; ++it) {
+    const int normalize = it & 1;
+    NlbArgs h1 = a;  // U = V Pc: A = Pr (k rows of d), 32 x k, no scale
+    h1.n = (int)k; h1.kdim = (int)d; h1.lda = d; h1.plain = 1;
+    for (int b = 0; b < nb; ++b) { h1.A[b] = reinterpret_cast<const float*>(Pr[b]); h1.Vin[b] = vb[cur][b]; h1.Vout[b] = w.part[b]; }
+    PSGDK_HIP(nlb_full_launch(h1, 2, 1, 0, st), "V Pc");
+    NlbArgs h2 = a;  // V' = U Pc^T / nf: A = Pc (d rows of k)
+    h2.n = (int)d; h2.kdim = (int)k; h2.lda = k;
+    for (int b = 0; b < nb; ++b) {
+      h2.A[b] = reinterpret_cast<const float*>(Pc[b]); h2.Vin[b] = w.part[b]; h2.Vout[b] = vb[cur ^ 1][b];
+      h2.ssin[b] = ss[0][b]; h2.ssout[b] = ss[normalize][b];
+    }
+    PSGDK_HIP(nlb_full_launch(h2, 2, 1, normalize, st), "U Pc^T");
+    cur ^= 1;
+  }
+  for (int b = 0; b < nb; ++b) a.ssin[b] = ss[1][b];
+  PSGDK_HIP(nlb_final_launch(a, fin, st), "nlb_final");
+  return PSGDK_OK;
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // Kron 2-D group helpers
 
@@ -646,31 +706,51 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
   const int nb = (int)it.size();
   const int64_t d = it[0]->d;
   const void *A[MAXB], *B[MAXB];
-  // term1 = pcol pcol^T, full symmetric bf16 (its only consumers read bf16): one launch per distinct other side
+  // The SPD bound of term1 = pcol pcol^T. Items whose other side is under half of d (the Pg route: term1 Q goes
+  // through pcol) bound term1 from pcol without forming it (run_nlb_gram, one launch sequence per other side, H in
+  // the T1b buffer and pcol H in the Rb buffer, both free until later phases); the others form term1 by SYRK (one
+  // launch per other side) and share one full-storage bound.
+  std::vector<int> full;
   for (int i0 = 0; i0 < nb;) {
     int k = 0;
     int idx[MAXB];
     const int64_t other = it[i0]->other;
     for (int i = i0; i < nb; ++i)
       if (it[i]->other == other) idx[k++] = i;
-    B16Out out;
+    while (i0 < nb && it[i0]->other == other) ++i0;  // items arrive sorted by other side within a batch
+    if (g_t1q_pg && 2 * other < d) {
+      NlbFinal fin;
+      std::memset(&fin, 0, sizeof fin);
+      fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL;
+      const bf16_t *Pc[MAXB], *Pr[MAXB];
+      bf16_t *Hb[MAXB], *Wb[MAXB];
+      const float* Vs[MAXB];
+      for (int j = 0; j < k; ++j) {
+        const B16Item* x = it[idx[j]];
+        fin.L[j] = x->L; fin.coef[j] = x->coef; fin.term2[j] = x->term2;
+        Pc[j] = x->pcol; Pr[j] = x->prow; Hb[j] = x->T1b; Wb[j] = x->Rb; Vs[j] = x->Vs;
+      }
+      PSGDK_TRY(run_nlb_gram(d, other, k, Pc, Pr, Hb, Wb, Vs, fin, nw, st));
+      continue;
+    }
+    B16Out out;  // term1 = pcol pcol^T, full symmetric bf16 (its only consumers read bf16)
     out.ldcb = d;
-    for (int j = 0; j < k; ++j) { A[j] = it[idx[j]]->pcol; out.Cb[j] = it[idx[j]]->T1b; }
+    for (int j = 0; j < k; ++j) { A[j] = it[idx[j]]->pcol; out.Cb[j] = it[idx[j]]->T1b; full.push_back(idx[j]); }
     EpiSpec e;
     PSGDK_TRY(run_b16(k, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
-    while (i0 < nb && it[i0]->other == other) ++i0;  // items arrive sorted by other side within a batch
   }
-  {
+  if (!full.empty()) {
     NlbFinal fin;
     std::memset(&fin, 0, sizeof fin);
     fin.mode = NLB_FINAL_FACTOR; fin.lr = o->lr; fin.beta = o->betaL;
     const void* T1c[MAXB];
     const float* Vs[MAXB];
-    for (int b = 0; b < nb; ++b) {
-      fin.L[b] = it[b]->L; fin.coef[b] = it[b]->coef; fin.term2[b] = it[b]->term2;
-      T1c[b] = it[b]->T1b; Vs[b] = it[b]->Vs;
+    for (size_t j = 0; j < full.size(); ++j) {
+      const B16Item* x = it[full[j]];
+      fin.L[j] = x->L; fin.coef[j] = x->coef; fin.term2[j] = x->term2;
+      T1c[j] = x->T1b; Vs[j] = x->Vs;
     }
-    PSGDK_TRY(run_nlb_full(d, 1, nb, T1c, d, 1, Vs, fin, nw, st));
+    PSGDK_TRY(run_nlb_full(d, 1, (int)full.size(), T1c, d, 1, Vs, fin, nw, st));
   }
   // Qn = Q - lr/L (term1 Q - term2 Q) -> fp32 + Qn^T bf16; items whose other side is under half of d form
   // term1 Q = pcol (prow Q): 4 other d^2 flops instead of 2 d^3, the same product associated the other way
@@ -1324,6 +1404,41 @@ int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* 
   std::memset(&fin, 0, sizeof fin);
   fin.mode = NLB_FINAL_NONE;
   PSGDK_TRY(run_nlb_full(n, sign, nb, A, lda, a_dtype == PSGDK_BF16, V, fin, nw, st));
+  for (int b = 0; b < nb; ++b)
+    PSGDK_HIP(hipMemcpyAsync(out[b], nw.scal[b] + NLB_BOUND, sizeof(float), hipMemcpyDeviceToDevice, st), "copy bound");
+  return PSGDK_OK;
+}
+
+int psgdk_norm_lower_bound_gram(int64_t d, int64_t k, int nb, const void* const* P, const void* const* Pt,
+                                const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
+                                psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_dims(d, "d"));
+  PSGDK_TRY(check_dims(k, "k"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  if (d % 8 || k % 8) return fail(PSGDK_ESHAPE, "d = %lld and k = %lld must be multiples of 8", (long long)d, (long long)k);
+  if (d * k * 2 >= ((int64_t)1 << 31) || k * k * 2 >= ((int64_t)1 << 31)) return fail(PSGDK_ESHAPE, "operands over 2 GiB");
+  Ws w(ws);
+  bf16_t *Hb[MAXB], *Wb[MAXB];
+  for (int b = 0; b < nb; ++b) { Hb[b] = w.take<bf16_t>(k * k); Wb[b] = w.take<bf16_t>(d * k); }
+  NlbWs nw;
+  nlb_take(w, d, nb, nw);
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(P, nb, "P"));
+  PSGDK_TRY(check_ptrs(Pt, nb, "Pt"));
+  PSGDK_TRY(check_ptrs(V, nb, "V"));
+  PSGDK_TRY(check_ptrs(out, nb, "out"));
+  const bf16_t *Pc[MAXB], *Pr[MAXB];
+  for (int b = 0; b < nb; ++b) {
+    if (!aligned16(P[b]) || !aligned16(Pt[b])) return fail(PSGDK_EINVAL, "P[%d] / Pt[%d] not 16-byte aligned", b, b);
+    Pc[b] = reinterpret_cast<const bf16_t*>(P[b]); Pr[b] = reinterpret_cast<const bf16_t*>(Pt[b]);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  NlbFinal fin;
+  std::memset(&fin, 0, sizeof fin);
+  fin.mode = NLB_FINAL_NONE;
+  PSGDK_TRY(run_nlb_gram(d, k, nb, Pc, Pr, Hb, Wb, V, fin, nw, st));
   for (int b = 0; b < nb; ++b)
     PSGDK_HIP(hipMemcpyAsync(out[b], nw.scal[b] + NLB_BOUND, sizeof(float), hipMemcpyDeviceToDevice, st), "copy bound");
   return PSGDK_OK;

@@ -18,6 +18,8 @@ struct NlbArgs {
                             // ksplit x 32 x n partial products
   int vmm_cols;             // full path: 1 = one workgroup per 64 output columns over the whole k range (no
                             // partials, ssc = 64); 0 = split-K products plus a reduce kernel (ssc = 128)
+  int kdim;                 // column kernel: k extent of a rectangular product (0: n)
+  int plain;                // column kernel: no row scale and no sums of squares
   long long lda;
   const float* A[MAXB];     // n x n, upper triangle read
   const float* Vin[MAXB];   // init: the random start (32 x n)
@@ -43,6 +45,21 @@ struct NlbFinal {
   float* L[MAXB];     // factor: the smoothness EMA (1 float)
   float* coef[MAXB];  // factor: {lr / L, term2}; scale: {1 / (bound + smallest normal)}
 };
+
+// The norm bound of term1 = P P^T (d x d) from its factor P (d x k bf16 rows, k contiguous), without forming term1:
+// the statistics the init kernel reads and row j of P P^T.
+struct GramArgs {
+  int nb, d, k;
+  const bf16_t* P[MAXB];  // d x k, row stride k
+  const bf16_t* W[MAXB];  // d x k: P H with H = P^T P (row stride k)
+  float* rn2[MAXB];       // out: squared row norms of P P^T
+  float* rmax[MAXB];      // out: zero (the row maxima are read by skew bounds only)
+  float* diag[MAXB];      // out: the diagonal of P P^T
+  float* scal[MAXB];      // NLB scalars: the argmax kernel writes NLB_J
+  bf16_t* aj[MAXB];       // out: row j of P P^T (d values)
+};
+// stage 0: rn2 = rowsum(W * P), diag = rowsum(P * P); 1: argmax of rn2 (first maximum) into scal; 2: aj
+hipError_t gram_launch(const GramArgs& a, int stage, hipStream_t st);
 
 hipError_t nlb_rownorm_launch(const NlbArgs& a, hipStream_t st);
 hipError_t nlb_init_launch(const NlbArgs& a, hipStream_t st);

@@ -653,6 +653,8 @@ __global__ void __launch_bounds__(256) vmm_reduce_kernel(const NlbArgs p, int no
 // is required: n and the row stride multiples of 16 bytes, aligned bases, each matrix < 2 GiB; the host checks).
 // Epilogue: thread t owns row t / 8 and 8 consecutive columns: W in T (one 16- or 32-byte store) and
 // ssout[r][cb] = sum over the block's columns of W[r][c]^2, reduced over the row's 8 lanes in a fixed tree.
+// Rectangular products (kdim > 0): V is 32 x kdim, A is n x kdim, W is 32 x n; plain: no row scale and no sums of
+// squares (the first half of a product through a factor, V Pcol then (V Pcol) Pcol^T).
 // grid: nb * ceil(n / 64).
 constexpr int VMC = 64;     // output columns per workgroup
 constexpr int VMC_LD = 68;  // LDS row stride (floats) of the partial blocks
@@ -665,6 +667,7 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
   __shared__ float rs[NLB_K];
   __shared__ __attribute__((aligned(16))) float red[4][NLB_K][VMC_LD];
   const int n = p.n, nbk = (n + VMC - 1) / VMC;
+  const int K = p.kdim ? p.kdim : n;  // k extent (rectangular products: V is 32 x K, A is n x K)
   const int b = blockIdx.x / nbk, cb = blockIdx.x % nbk;
   // the wave index sets the k range, hence the loads' scalar offset: readfirstlane makes it provably uniform
   // (otherwise every load becomes a waterfall loop)
@@ -673,12 +676,12 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
   const int c0 = cb * VMC;
   const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
   const T* __restrict__ V = reinterpret_cast<const T*>(p.Vin[b]);
-  if (tid < NLB_K) rs[tid] = vmm_row_scale(p, b, tid, nbk, normalize);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * n * sizeof(T));
+  if (tid < NLB_K) rs[tid] = p.plain ? 1.f : vmm_row_scale(p, b, tid, nbk, normalize);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * K * sizeof(T));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * sizeof(T));
   int vo[2], ao[4];  // byte offsets of this lane's pieces at k = 0 (kOob: a column past n reads zero)
 #pragma unroll
-  for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * n + g * ACH) * (int)sizeof(T);
+  for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * K + g * ACH) * (int)sizeof(T);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = c0 + j * 16 + r16;
@@ -689,8 +692,8 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int kq = ((n + 3) / 4 + KS - 1) / KS * KS;
-  const int kbeg = wave * kq, kend = min(n, kbeg + kq);
+  const int kq = ((K + 3) / 4 + KS - 1) / KS * KS;
+  const int kbeg = wave * kq, kend = min(K, kbeg + kq);
   for (int k0 = kbeg; k0 < kend; k0 += U * KS) {
     uint4 vf[U][2], af[U][4];
 #pragma unroll
@@ -762,10 +765,100 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
     for (int e = 0; e < 8; ++e)
       if (col + e < n) W[e] = from_f32<T>(w[e]);
   }
+  if (p.plain) return;
   sq += __shfl_xor(sq, 1, 64);
   sq += __shfl_xor(sq, 2, 64);
   sq += __shfl_xor(sq, 4, 64);
   if ((tid & 7) == 0) p.ssout[b][row * nbk + cb] = sq;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Norm bound of term1 = P P^T from its factor P (d x k, k < d / 2 on the bf16 update's Pg route). With H = P^T P:
+// ||row i of P P^T||^2 = P_i H P_i^T = sum_c (P H)_ic P_ic, (P P^T)_ii = ||P_i||^2, row j of P P^T = P P_j^T.
+
+// One wave per row i: rn2[i] = sum_c W_ic P_ic, diag[i] = sum_c P_ic^2, rmax[i] = 0 (16-byte loads; k % 8 == 0 and
+// 16-byte aligned rows, which the host checks). grid: nb * ceil(d / 4).
+__global__ void __launch_bounds__(256) gram_stats_kernel(const GramArgs p) {
+  const int nrb = (p.d + 3) / 4;
+  const int b = blockIdx.x / nrb, i = (blockIdx.x % nrb) * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (i >= p.d) return;
+  const bf16_t* __restrict__ pr = p.P[b] + (long long)i * p.k;
+  const bf16_t* __restrict__ wr = p.W[b] + (long long)i * p.k;
+  float s = 0.f, q = 0.f;
+  for (int c = lane; c < p.k / 8; c += 64) {
+    float x[8], w[8];
+    load8(pr + 8 * c, x);
+    load8(wr + 8 * c, w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s += w[e] * x[e];
+      q += x[e] * x[e];
+    }
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  if (lane == 0) {
+    p.rn2[b][i] = s;
+    p.diag[b][i] = q;
+    p.rmax[b][i] = 0.f;
+  }
+}
+
+// One workgroup per matrix: j = the first maximum of rn2 (the init kernel's rule) into scal[NLB_J].
+__global__ void __launch_bounds__(256) gram_argmax_kernel(const GramArgs p) {
+  __shared__ float sval[4];
+  __shared__ int sidx[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float* __restrict__ rn2 = p.rn2[b];
+  float best = -1.f;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < p.d; i += 256) {
+    const float v = rn2[i];
+    if (v > best) { best = v; bi = i; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { sval[tid >> 6] = best; sidx[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    float bv = sval[0];
+    int bj = sidx[0];
+    for (int w = 1; w < 4; ++w)
+      if (sval[w] > bv || (sval[w] == bv && sidx[w] < bj)) { bv = sval[w]; bj = sidx[w]; }
+    p.scal[b][NLB_J] = (float)(bj < p.d ? bj : 0);
+  }
+}
+
+// One wave per row c: aj[c] = sum_k P_ck P_jk (row j of P P^T, rounded to bf16 like the matrices the bound reads).
+// grid: nb * ceil(d / 4).
+__global__ void __launch_bounds__(256) gram_row_kernel(const GramArgs p) {
+  const int nrb = (p.d + 3) / 4;
+  const int b = blockIdx.x / nrb, c = (blockIdx.x % nrb) * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (c >= p.d) return;
+  const int j = (int)p.scal[b][NLB_J];
+  const bf16_t* __restrict__ pc = p.P[b] + (long long)c * p.k;
+  const bf16_t* __restrict__ pj = p.P[b] + (long long)j * p.k;
+  float s = 0.f;
+  for (int q = lane; q < p.k / 8; q += 64) {
+    float x[8], y[8];
+    load8(pc + 8 * q, x);
+    load8(pj + 8 * q, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[e] * y[e];
+  }
+  s = wave_sum(s);
+  if (lane == 0) p.aj[b][c] = f32_to_bf16(s);
+}
+
+hipError_t gram_launch(const GramArgs& a, int stage, hipStream_t st) {
+  const int nrb = (a.d + 3) / 4;
+  if (stage == 0) hipLaunchKernelGGL(gram_stats_kernel, dim3(nrb * a.nb), dim3(256), 0, st, a);
+  else if (stage == 1) hipLaunchKernelGGL(gram_argmax_kernel, dim3(a.nb), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(gram_row_kernel, dim3(nrb * a.nb), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st) {

@@ -255,6 +255,32 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, ta
         assert g <= top * (1 + rel)
 
 
+@pytest.mark.parametrize("d,k", [(64, 16), (384, 128), (1000, 248), (3072, 768)])
+def test_norm_lower_bound_gram_matches_oracle(hip, d, k):
+    """psgdk_norm_lower_bound_gram: the SPD bound (psgd_pro.py:19-41) of P P^T from P (d x k bf16) without forming
+    P P^T, for three matrices of different scales, against the float64 oracle on the same (bf16) P: rel 2e-2 (the
+    products run on bf16 V and factors); at most ||P P^T||_2; bitwise repeatable."""
+    from oracle.psgd_oracle import norm_lower_bound
+    Ps = [((0.5 + b) * rnd(d, k, seed=d + k + b)).to(torch.bfloat16) for b in range(3)]
+    Vs = [rnd(32, d, seed=7 + b) for b in range(3)]
+    Pd = [P.to(DEV) for P in Ps]
+    Ptd = [P.T.contiguous() for P in Pd]
+    Vd = [v.to(DEV) for v in Vs]
+    outs = [torch.empty((), device=DEV) for _ in Ps]
+
+    def run():
+        L.call_ws(L.lib().psgdk_norm_lower_bound_gram, d, k, len(Ps), L.ptrs(Pd), L.ptrs(Ptd), L.ptrs(Vd), L.ptrs(outs),
+                  ws=K._WS, device=Pd[0].device, stream=L.stream_of(Pd[0]))
+        return [float(o) for o in outs]
+    got, again = run(), run()
+    assert got == again
+    for P, V, g in zip(Ps, Vs, got):
+        A = P.double() @ P.double().T
+        ref = float(norm_lower_bound(A, V.double(), skew=False))
+        assert g == pytest.approx(ref, rel=2e-2)
+        assert g <= float(torch.linalg.matrix_norm(A, 2)) * (1 + 2e-2)
+
+
 @pytest.mark.parametrize("cols", [1, 0], ids=["cols", "split"])
 def test_norm_lower_bound_full_sixteen_matrices(hip, cols):
     """A full group (16 matrices, the most one call takes) of 320 x 320 bf16 SPD matrices of different scales:
