@@ -205,6 +205,7 @@ int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of th
 int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape, 0 split-K + reduce, 1 column blocks
 int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
 int g_upd_streams = 3;    // psgdk_set_option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
+int g_rq16 = 1;           // psgdk_set_option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -847,13 +848,17 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
     }
   } else {
     int nt = 0;
-    {  // RQ = R Qn / (bound + sn) -> fp32 + RQ^T bf16, trace partials (tr(R RQ) reads the bf16 R of the product)
+    {  // RQ = R Qn / (bound + sn) -> bf16 (or fp32, option 7) + RQ^T bf16, trace partials (tr(R RQ) reads the
+       // bf16 R of the product). RQ enters the Q update as the correction a RQ; the product already comes from
+       // bf16 operands, so its bf16 rounding adds an error of the same size and halves that operand's bytes
       B16Out out;
-      out.ldc = d; out.ldct = d;
+      out.ldc = d; out.ldcb = d; out.ldct = d;
       EpiSpec e;
       e.epi = EPI_RQ; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
-        A[b] = it[b]->Rb; B[b] = it[b]->QnTb; out.C[b] = it[b]->RQ; out.CTb[b] = it[b]->RQTb;
+        A[b] = it[b]->Rb; B[b] = it[b]->QnTb; out.CTb[b] = it[b]->RQTb;
+        if (g_rq16) out.Cb[b] = reinterpret_cast<bf16_t*>(it[b]->RQ);
+        else out.C[b] = it[b]->RQ;
         e.X1[b] = reinterpret_cast<const float*>(it[b]->Rb); e.s[b] = it[b]->rs; e.part[b] = it[b]->tpart;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, &nt, st));
@@ -869,7 +874,7 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
       B16Out out;
       out.ldc = d; out.ldct = d;
       EpiSpec e;
-      e.epi = EPI_PROC; e.ldx = d;
+      e.epi = g_rq16 ? EPI_PROCB : EPI_PROC; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
         A[b] = it[b]->Rb; B[b] = it[b]->RQTb; out.C[b] = it[b]->Q; out.CTb[b] = it[b]->Qt16;
         e.X1[b] = it[b]->Qn; e.X2[b] = it[b]->RQ; e.s[b] = it[b]->pc;
@@ -1771,6 +1776,11 @@ int psgdk_set_option(int option, int value) {
   if (option == 5) {
     if (value != 0 && value != 1) return fail(PSGDK_EINVAL, "option 5 (term1 Q through Pg) must be 0 or 1");
     g_t1q_pg = value;
+    return PSGDK_OK;
+  }
+  if (option == 7) {
+    if (value != 0 && value != 1) return fail(PSGDK_EINVAL, "option 7 (R Q in bf16) must be 0 or 1");
+    g_rq16 = value;
     return PSGDK_OK;
   }
   if (option == 6) {

@@ -258,9 +258,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   const float* __restrict__ X1 = p.X1[b];
   const float* __restrict__ X2 = p.X2[b];
   float s0 = 0.f, s1 = 0.f;
-  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_SCALE || EPI == EPI_RQ || EPI == EPI_STRACE)
+  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_SCALE || EPI == EPI_RQ ||
+                EPI == EPI_STRACE)
     s0 = p.s[b][0];
-  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) s1 = p.s[b][1];
+  if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB) s1 = p.s[b][1];
   const bool mirror = p.tri && p.out_mode == 1;
   const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ || EPI == EPI_STRACE;
   auto al = [](const void* q, int bytes) { return (reinterpret_cast<uintptr_t>(q) & (bytes - 1)) == 0; };
@@ -301,7 +302,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         for (int e = 0; e < 4; ++e) ok[e] = FAST || (row < p.M && col + e < p.N && !(p.tri && row > col + e));
         const long long xo = (long long)row * p.ldx + col;
         float q1[4] = {0.f, 0.f, 0.f, 0.f}, q2[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC) {
+        if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB) {
           if constexpr (FAST) {
             const float4 t = *reinterpret_cast<const float4*>(X1 + xo);
             q1[0] = t.x; q1[1] = t.y; q1[2] = t.z; q1[3] = t.w;
@@ -319,11 +320,22 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
             for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? X2[xo + e] : 0.f;
           }
         }
+        if constexpr (EPI == EPI_PROCB) {  // X2 in bf16, row-major with the same leading dimension
+          const bf16_t* x2 = reinterpret_cast<const bf16_t*>(X2) + xo;
+          if constexpr (FAST) {
+            const uint2 t = *reinterpret_cast<const uint2*>(x2);
+            q2[0] = bf16_to_f32((bf16_t)(t.x & 0xffff)); q2[1] = bf16_to_f32((bf16_t)(t.x >> 16));
+            q2[2] = bf16_to_f32((bf16_t)(t.y & 0xffff)); q2[3] = bf16_to_f32((bf16_t)(t.y >> 16));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? bf16_to_f32(x2[e]) : 0.f;
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if constexpr (EPI == EPI_FACTOR) {
             v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
-          } else if constexpr (EPI == EPI_PROC) {
+          } else if constexpr (EPI == EPI_PROC || EPI == EPI_PROCB) {
             v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
           } else if constexpr (EPI == EPI_STRACE) {
             v[e] = (s0 * v[e]) * s0;
@@ -493,6 +505,7 @@ static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
   switch (a.epi) {
     case EPI_FACTOR: return launch_b16<BM, BN, WGM, WGN, EPI_FACTOR>(a, st);
     case EPI_PROC: return launch_b16<BM, BN, WGM, WGN, EPI_PROC>(a, st);
+    case EPI_PROCB: return launch_b16<BM, BN, WGM, WGN, EPI_PROCB>(a, st);
     case EPI_SCALE: return launch_b16<BM, BN, WGM, WGN, EPI_SCALE>(a, st);
     case EPI_RQ: return launch_b16<BM, BN, WGM, WGN, EPI_RQ>(a, st);
     case EPI_SUMSQ: return launch_b16<BM, BN, WGM, WGN, EPI_SUMSQ>(a, st);

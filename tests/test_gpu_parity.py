@@ -108,15 +108,21 @@ def test_fp32_parity_1024_weight(hip):
     assert_fp32(worst, base)
 
 
-def test_bf16_parity(hip, b16cfg):
+@pytest.mark.parametrize("rq16", [1, 0], ids=["rq_bf16", "rq_fp32"])
+def test_bf16_parity(hip, b16cfg, rq16):
     """bf16 gradients and bf16 MFMA inputs against the float32 oracle on the same gradients upcast: per-element
     2e-2 on Q (floor 1e-3 max); normwise 2e-2 on the preconditioned gradient and the parameters (a per-element
     floor of 1e-3 max sits below bfloat16's rounding noise (2^-9) of a sum with cancellation). Run in every tile
     configuration of the bf16 kernel: 384 = 256 + 128 gives the 256-tile ones interior and ragged tiles, so every
-    fused epilogue (factor update, RQ with traces, Q update, SYRK mirror) runs on both of its paths."""
+    fused epilogue (factor update, RQ with traces, Q update, SYRK mirror) runs on both of its paths; with R Q kept
+    in bf16 (the default) and in fp32 between the two Procrustes products."""
     eps16 = torch.finfo(torch.bfloat16).eps
-    worst, _ = run_pair([(256, 384), (384, 256)], steps=8, skew=math.inf, prec="bf16", gdt=torch.bfloat16,
-                        grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
+    assert hip.psgdk_set_option(7, rq16) == 0
+    try:
+        worst, _ = run_pair([(256, 384), (384, 256)], steps=8, skew=math.inf, prec="bf16", gdt=torch.bfloat16,
+                            grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
+    finally:
+        hip.psgdk_set_option(7, 1)
     assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
 
 
