@@ -609,20 +609,28 @@ int precondition(const psgdk_kron2d_t* g, const void* const* X, int xdt, float* 
   return PSGDK_OK;
 }
 
-// The bf16 path with k-contiguous bf16 operands applies to groups with two dense factors, bf16 shadows for both,
-// rows of whole 16-byte vectors and full (not triangle) storage.
+// The bf16 path with k-contiguous bf16 operands applies to groups with two dense factors, or one dense and one
+// diagonal factor, bf16 shadows for every dense factor, rows of whole 16-byte vectors and full (not triangle)
+// storage.
 bool b16_group(const psgdk_kron2d_t* g, int tri) {
   if (g->prec != PSGDK_PREC_BF16 || tri) return false;
-  if (g->kind[0] != PSGDK_FACTOR_DENSE || g->kind[1] != PSGDK_FACTOR_DENSE) return false;
+  const int k0 = g->kind[0], k1 = g->kind[1];
+  const bool dd = k0 == PSGDK_FACTOR_DENSE && k1 == PSGDK_FACTOR_DENSE;
+  const bool mixed = (k0 == PSGDK_FACTOR_DENSE && k1 == PSGDK_FACTOR_DIAG) ||
+                     (k0 == PSGDK_FACTOR_DIAG && k1 == PSGDK_FACTOR_DENSE);
+  if (!dd && !mixed) return false;
   if (g->m % 8 || g->n % 8) return false;
-  for (int f = 0; f < 2; ++f)
+  for (int f = 0; f < 2; ++f) {
+    if (g->kind[f] != PSGDK_FACTOR_DENSE) continue;
+    const int64_t d = f == 0 ? g->m : g->n;
+    if (d * d * 2 >= ((int64_t)1 << 31)) return false;
     for (int b = 0; b < g->nb; ++b)
       if (!g->Qt16[f][b] || !g->P16[f][b] || !aligned16(g->Qt16[f][b]) || !aligned16(g->P16[f][b])) return false;
+  }
   // G's alignment does not matter: the update reads G through the noise kernel and the apply copies a misaligned
   // bf16 G into aligned workspace, so a group's path depends on its own storage only (the bf16 path keeps fp32 P
   // current at refresh points only, and no other path may run on the group in between)
-  const int64_t big = std::max(g->m, g->n);
-  if (big * big * 2 >= ((int64_t)1 << 31) || g->m * g->n * 2 >= ((int64_t)1 << 31)) return false;
+  if (g->m * g->n * 2 >= ((int64_t)1 << 31)) return false;
   return true;
 }
 
@@ -900,6 +908,7 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
                       hipStream_t st) {
   Ws w(ws);
   std::vector<std::vector<bf16_t*>> Xb(ng), YTb(ng), Pgb(ng), PgTb(ng);
+  std::vector<std::vector<float*>> dterm(ng);  // a diagonal factor's term1
   std::vector<B16Item> items;
   for (int gi = 0; gi < ng; ++gi) {
     const psgdk_kron2d_t* g = gs[gi];
@@ -909,10 +918,12 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
       YTb[gi].push_back(w.take<bf16_t>(mn));
       Pgb[gi].push_back(w.take<bf16_t>(mn));
       PgTb[gi].push_back(w.take<bf16_t>(mn));
+      dterm[gi].push_back(w.take<float>(std::max(g->m, g->n)));
     }
     for (int b = 0; b < g->nb; ++b) {
       int64_t voff = 0;
       for (int f = 0; f < 2; ++f) {
+        if (g->kind[f] != PSGDK_FACTOR_DENSE) continue;  // a diagonal factor is updated in the per-group phase
         B16Item x;
         x.d = f == 0 ? g->m : g->n;
         x.other = f == 0 ? g->n : g->m;
@@ -973,27 +984,65 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
     const int nb = g->nb;
     const int64_t m = g->m, n = g->n;
     hipStream_t st = lane(gi);
-    {
+    const bool d0 = g->kind[0] == PSGDK_FACTOR_DENSE, d1 = g->kind[1] == PSGDK_FACTOR_DENSE;
+    const void *A[MAXB], *B[MAXB];
+    if (d0 && !d1) {  // P2 diagonal: Pg = P1 (X diag(p2)), the scaled X transposed to bf16 by the noise kernel
       EwArgs a;
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
-      for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.out2[b] = Xb[gi][b]; }
-      PSGDK_HIP(noise_launch(a, st), "noise");
-    }
-    const void *A[MAXB], *B[MAXB];
-    {  // Y = X P2 -> Y^T
-      B16Out out;
-      out.ldct = m;
-      for (int b = 0; b < nb; ++b) { A[b] = Xb[gi][b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[gi][b]; }
-      EpiSpec e;
-      PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
-    }
-    {  // Pg = P1 Y -> Pg, Pg^T
+      for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.in3[b] = g->P[1][b]; a.out2[b] = Xb[gi][b]; }
+      PSGDK_HIP(noise_t_launch(a, st), "noise (transposed, column-scaled)");
       B16Out out;
       out.ldcb = n; out.ldct = m;
-      for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[gi][b]; out.Cb[b] = Pgb[gi][b]; out.CTb[b] = PgTb[gi][b]; }
+      for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = Xb[gi][b]; out.Cb[b] = Pgb[gi][b]; out.CTb[b] = PgTb[gi][b]; }
       EpiSpec e;
       PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, nullptr, st));
+    } else {
+      {  // X (P1 diagonal: diag(p1) X) -> bf16
+        EwArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
+        for (int b = 0; b < nb; ++b) {
+          a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.out2[b] = Xb[gi][b]; a.in3[b] = d0 ? nullptr : g->P[0][b];
+        }
+        PSGDK_HIP(noise_launch(a, st), "noise");
+      }
+      if (d0) {
+        {  // Y = X P2 -> Y^T
+          B16Out out;
+          out.ldct = m;
+          for (int b = 0; b < nb; ++b) { A[b] = Xb[gi][b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[gi][b]; }
+          EpiSpec e;
+          PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+        }
+        {  // Pg = P1 Y -> Pg, Pg^T
+          B16Out out;
+          out.ldcb = n; out.ldct = m;
+          for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[gi][b]; out.Cb[b] = Pgb[gi][b]; out.CTb[b] = PgTb[gi][b]; }
+          EpiSpec e;
+          PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, nullptr, st));
+        }
+      } else {  // Pg = (diag(p1) X) P2 -> Pg, Pg^T
+        B16Out out;
+        out.ldcb = n; out.ldct = m;
+        for (int b = 0; b < nb; ++b) { A[b] = Xb[gi][b]; B[b] = g->P16[1][b]; out.Cb[b] = Pgb[gi][b]; out.CTb[b] = PgTb[gi][b]; }
+        EpiSpec e;
+        PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+      }
+    }
+    for (int f = 0; f < 2; ++f) {  // a diagonal factor (psgd_pro.py:126-130): term1 = row sums of squares of Pg
+      if (g->kind[f] != PSGDK_FACTOR_DIAG) continue;  // (f = 0) or of Pg^T (f = 1), read in bf16; L EMA, q, P = q^2
+      const int64_t d = f == 0 ? m : n, other = f == 0 ? n : m;
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = d; a.n = other;
+      for (int b = 0; b < nb; ++b) { a.in[b] = f == 0 ? Pgb[gi][b] : PgTb[gi][b]; a.out[b] = dterm[gi][b]; }
+      PSGDK_HIP(rowsq_launch(a, st), "diagonal factor term1");
+      EwArgs u;
+      std::memset(&u, 0, sizeof u);
+      u.nb = nb; u.m = d; u.f0 = os[gi]->lr; u.f1 = os[gi]->betaL; u.f2 = (float)(m * n) / (float)d;
+      for (int b = 0; b < nb; ++b) { u.in2[b] = dterm[gi][b]; u.out[b] = g->Q[f][b]; u.out2[b] = g->P[f][b]; u.sc[b] = g->L[f][b]; }
+      PSGDK_HIP(diag_update_launch(u, st), "diagonal factor update");
     }
   }
   if (S > 1) {
@@ -1041,28 +1090,49 @@ int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const*
   for (int b = 0; b < nb; ++b)
     if (pre_out && pre_out[b]) pre[b] = pre_out[b];
   const void *A[MAXB], *B[MAXB];
-  if (conv) {
-    EwArgs a;
-    std::memset(&a, 0, sizeof a);
-    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype;
-    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.out2[b] = Gb[b]; }
-    PSGDK_HIP(noise_launch(a, st), "G to bf16");
-  }
-  {
-    B16Out out;
-    out.ldct = m;
-    for (int b = 0; b < nb; ++b) { A[b] = conv ? (const void*)Gb[b] : g->G[b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[b]; }
-    EpiSpec e;
-    PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
-  }
+  const bool d0 = g->kind[0] == PSGDK_FACTOR_DENSE, d1 = g->kind[1] == PSGDK_FACTOR_DENSE;
   int np = 0;
-  {
+  if (d0 && d1) {
+    if (conv) {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype;
+      for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.out2[b] = Gb[b]; }
+      PSGDK_HIP(noise_launch(a, st), "G to bf16");
+    }
+    {
+      B16Out out;
+      out.ldct = m;
+      for (int b = 0; b < nb; ++b) { A[b] = conv ? (const void*)Gb[b] : g->G[b]; B[b] = g->P16[1][b]; out.CTb[b] = YTb[b]; }
+      EpiSpec e;
+      PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, nullptr, st));
+    }
     B16Out out;
     out.ldc = n;
     EpiSpec e;
     e.epi = EPI_SUMSQ;
     for (int b = 0; b < nb; ++b) { A[b] = g->P16[0][b]; B[b] = YTb[b]; out.C[b] = pre[b]; e.part[b] = part[b]; }
     PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, &np, st));
+  } else {
+    // one diagonal factor: its P scales G's rows (P1) or columns (P2) on the way to the bf16 operand, and one GEMM
+    // with the dense factor's P shadow gives pre; P2 diagonal needs the operand transposed (Gb holds m n bf16)
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype;
+    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.out2[b] = YTb[b]; a.in3[b] = d0 ? g->P[1][b] : g->P[0][b]; }
+    if (d0) PSGDK_HIP(noise_t_launch(a, st), "G diag(p2) transposed to bf16");
+    else PSGDK_HIP(noise_launch(a, st), "diag(p1) G to bf16");
+    B16Out out;
+    out.ldc = n;
+    EpiSpec e;
+    e.epi = EPI_SUMSQ;
+    for (int b = 0; b < nb; ++b) {
+      A[b] = d0 ? (const void*)g->P16[0][b] : (const void*)YTb[b];
+      B[b] = d0 ? (const void*)YTb[b] : (const void*)g->P16[1][b];
+      out.C[b] = pre[b]; e.part[b] = part[b];
+    }
+    if (d0) PSGDK_TRY(run_b16(nb, m, n, m, A, m, B, m, out, e, 0, 0, &np, st));  // P1 (G diag(p2))
+    else PSGDK_TRY(run_b16(nb, m, n, n, A, n, B, n, out, e, 0, 0, &np, st));     // (diag(p1) G) P2
   }
   EwArgs a;
   std::memset(&a, 0, sizeof a);

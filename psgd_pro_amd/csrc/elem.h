@@ -20,8 +20,13 @@ struct EwArgs {
   float* sc[MAXB];         // device scalars
 };
 
-// X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N null: X = G)  (psgd_pro.py:121-123)
+// X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N null: X = G)  (psgd_pro.py:121-123);
+// in3 (optional): a row scale applied to X (a diagonal P1 of P1 X P2)
 hipError_t noise_launch(const EwArgs& a, hipStream_t st);
+// out2 = bf16 (X diag(in3))^T with X as noise_launch (a diagonal P2 folded into the transposed operand of P1 X P2)
+hipError_t noise_t_launch(const EwArgs& a, hipStream_t st);
+// out[i] = sum_j X[i][j]^2 of a bf16 m x n matrix (a diagonal factor's term1 from the bf16 Pg or Pg^T)
+hipError_t rowsq_launch(const EwArgs& a, hipStream_t st);
 // R = Q^T - Q (sign = +1) or Q - Q^T (sign = -1), square d x d, plus an optional bf16 copy in out2
 // (psgd_pro.py:87; psgd_pro_fast.py:147)
 hipError_t rform_launch(const EwArgs& a, hipStream_t st);

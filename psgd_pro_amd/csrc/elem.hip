@@ -73,8 +73,9 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   const float* N = a.in2[b];
   float* X = a.out[b];
   bf16_t* Xb = reinterpret_cast<bf16_t*>(a.out2[b]);
+  const float* rsc = a.in3[b];  // optional row scale (a diagonal P1 folded into the input of P1 X P2)
   const long long total = a.m * a.n;
-  if ((total & 7) == 0 && al16(G) && (!N || al16(N)) && (!X || al16(X)) && (!Xb || al16(Xb))) {
+  if ((total & 7) == 0 && (a.n & 7) == 0 && al16(G) && (!N || al16(N)) && (!X || al16(X)) && (!Xb || al16(Xb))) {
     ew_range8(total, blocks_per, beg, end);
     for (long long v = beg + threadIdx.x; v < end; v += EW_THREADS) {
       float g[8], nz[8];
@@ -84,6 +85,11 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
 #pragma unroll
         for (int e = 0; e < 8; ++e) g[e] = g[e] + (a.f0 + a.f1 * fabsf(g[e])) * nz[e];
       }
+      if (rsc) {
+        const float r = rsc[(8 * v) / a.n];  // n % 8 == 0: the 8 elements share a row
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] *= r;
+      }
       if (X) ew_store8(X + 8 * v, g);
       if (Xb) ew_store8(Xb + 8 * v, g);
     }
@@ -92,7 +98,8 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   ew_range(total, blocks_per, beg, end);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     const float g = ldv(G, a.dt, i);
-    const float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[i] : g;
+    float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[i] : g;
+    if (rsc) x *= rsc[i / a.n];
     if (X) X[i] = x;
     if (Xb) Xb[i] = f32_to_bf16(x);
   }
@@ -100,6 +107,80 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
 hipError_t noise_launch(const EwArgs& a, hipStream_t st) {
   const int bp = ew_blocks(a.m * a.n);
   hipLaunchKernelGGL(noise_kernel, dim3(bp * a.nb), dim3(EW_THREADS), 0, st, a, bp);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out2 = bf16 of (X diag(c))^T (n x m) with X = G + (f0 + f1 |G|) N (N optional) and the column scale c = in3
+// (optional): the transposed bf16 operand of P1 (X P2) when P2 is diagonal. 64 x 64 tiles through LDS: row-wise
+// reads of G and N, row-wise (along m) writes of the transpose. grid: nb * ceil(m / 64) * ceil(n / 64).
+__global__ void __launch_bounds__(256) noise_t_kernel(const EwArgs a) {
+  __shared__ float t[64][65];
+  const long long m = a.m, n = a.n;
+  const int tm = (int)((m + 63) / 64), tn = (int)((n + 63) / 64);
+  const int b = blockIdx.x / (tm * tn), tile = blockIdx.x % (tm * tn);
+  const int I = tile / tn, J = tile % tn;
+  const void* G = a.in[b];
+  const float* N = a.in2[b];
+  const float* csc = a.in3[b];
+  bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
+  const int tid = threadIdx.x, c = tid & 63, r0 = tid >> 6;
+  const long long gj = (long long)J * 64 + c;
+#pragma unroll 4
+  for (int r = r0; r < 64; r += 4) {
+    const long long gi = (long long)I * 64 + r;
+    float x = 0.f;
+    if (gi < m && gj < n) {
+      const long long o = gi * n + gj;
+      const float g = ldv(G, a.dt, o);
+      x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[o] : g;
+      if (csc) x *= csc[gj];
+    }
+    t[r][c] = x;
+  }
+  __syncthreads();
+  const long long oi = (long long)I * 64 + c;  // output column (an input row)
+#pragma unroll 4
+  for (int r = r0; r < 64; r += 4) {
+    const long long oj = (long long)J * 64 + r;  // output row (an input column)
+    if (oj < n && oi < m) Y[oj * m + oi] = f32_to_bf16(t[c][r]);
+  }
+}
+hipError_t noise_t_launch(const EwArgs& a, hipStream_t st) {
+  const long long tm = (a.m + 63) / 64, tn = (a.n + 63) / 64;
+  hipLaunchKernelGGL(noise_t_kernel, dim3((unsigned)(tm * tn * a.nb)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// out[b][i] = sum_j X[i][j]^2 over the rows of a bf16 m x n matrix X = in[b] (one wave per row; 16-byte loads when
+// n % 8 == 0 and the base is 16-byte aligned): a diagonal factor's term1 from the bf16 Pg (rows) or Pg^T (columns).
+__global__ void __launch_bounds__(256) rowsq_kernel(const EwArgs a) {
+  const long long nrb = (a.m + 3) / 4;
+  const int b = (int)(blockIdx.x / nrb);
+  const long long i = (blockIdx.x % nrb) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= a.m) return;
+  const bf16_t* row = reinterpret_cast<const bf16_t*>(a.in[b]) + i * a.n;
+  float s = 0.f;
+  if ((a.n & 7) == 0 && al16(a.in[b])) {
+    for (long long c = lane; c < a.n / 8; c += 64) {
+      float x[8];
+      ew_load8(row + 8 * c, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += x[e] * x[e];
+    }
+  } else {
+    for (long long c = lane; c < a.n; c += 64) {
+      const float x = bf16_to_f32(row[c]);
+      s += x * x;
+    }
+  }
+  s = wave_sum(s);
+  if (lane == 0) a.out[b][i] = s;
+}
+hipError_t rowsq_launch(const EwArgs& a, hipStream_t st) {
+  const long long nrb = (a.m + 3) / 4;
+  hipLaunchKernelGGL(rowsq_kernel, dim3((unsigned)(nrb * a.nb)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -186,7 +186,7 @@ class KronWhiten:
                     if k == L.FACTOR_DENSE:
                         Q = torch.eye(d, device=dev, dtype=torch.float32).mul_(s).expand(nb, d, d).contiguous()
                         P = torch.empty(nb, d, d, device=dev, dtype=torch.float32)
-                        if (self._prec == L.PREC_BF16 and not self._tri and grp.kind == (L.FACTOR_DENSE, L.FACTOR_DENSE)
+                        if (self._prec == L.PREC_BF16 and not self._tri and L.FACTOR_NONE not in grp.kind
                                 and grp.m % 8 == 0 and grp.n % 8 == 0):
                             # bf16 shadows (Q^T and P) read by the bf16 contractions; the library keeps them current
                             grp.Qt16[f] = torch.empty(nb, d, d, device=dev, dtype=torch.bfloat16)
@@ -303,11 +303,15 @@ class KronWhiten:
 
     @staticmethod
     def _b16(grp):
-        """The group takes the library's bf16 path (its b16_group rule): bf16 shadows of both dense factors exist
-        (bf16 precision, two dense factors, sides multiples of 8, full storage) and every operand is under 2 GiB."""
-        big = max(grp.m, grp.n)
-        return (grp.Qt16[0] is not None and grp.Qt16[1] is not None and big * big * 2 < 2 ** 31
-                and grp.m * grp.n * 2 < 2 ** 31)
+        """The group takes the library's bf16 path (its b16_group rule): two factors, dense or diagonal with at least
+        one dense, every dense factor with its bf16 shadows (bf16 precision, sides multiples of 8, full storage) and
+        every operand under 2 GiB."""
+        if L.FACTOR_NONE in grp.kind or L.FACTOR_DENSE not in grp.kind:
+            return False
+        for f, d in enumerate((grp.m, grp.n)):
+            if grp.kind[f] == L.FACTOR_DENSE and (grp.Qt16[f] is None or d * d * 2 >= 2 ** 31):
+                return False
+        return grp.m * grp.n * 2 < 2 ** 31
 
     def _update(self, srcs, noise, V):
         o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))

@@ -126,6 +126,17 @@ def test_bf16_parity(hip, b16cfg, rq16):
     assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
 
 
+def test_bf16_parity_dense_diag(hip, b16cfg):
+    """Weights with one dense and one diagonal factor on the bf16 path (max_skew 1: 96 x 256 and 64 x 264 have a
+    diagonal column factor, 256 x 96 a diagonal row factor): the diagonal P scales X's rows or columns on the way to
+    the bf16 operand (transposed for columns), the diagonal factor's term1 comes from the bf16 Pg; against the
+    float32 oracle on the same gradients upcast at the bf16 bar, in every tile configuration (264: ragged)."""
+    eps16 = torch.finfo(torch.bfloat16).eps
+    worst, _ = run_pair([(96, 256), (256, 96), (64, 264)], steps=8, skew=1.0, prec="bf16", gdt=torch.bfloat16,
+                        grad_eps=eps16, ref_dtype=torch.float32, baseline=False)
+    assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16 and worst["L"] < TOL16, worst
+
+
 @pytest.mark.parametrize("via_pg", [1, 0], ids=["pg", "term1"])
 @pytest.mark.parametrize("r2", [False, True], ids=["step2", "r2"])
 def test_bf16_parity_thin_weights(hip, b16cfg, r2, via_pg):
@@ -246,20 +257,22 @@ def test_side_streams_bitwise_identical(hip, prec):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("skew", [math.inf, 2.0], ids=["dense", "mixed"])
 @pytest.mark.parametrize("r2", [False, True], ids=["step2", "r2"])
-def test_fused_groups_bitwise_identical(hip, r2):
+def test_fused_groups_bitwise_identical(hip, r2, skew):
     """fuse_groups=True (one psgdk_kron2d_update_groups call; factor work batched by side across groups and both
     dimensions) against one psgdk_kron2d_update per group: Q, L, the P shadows and the parameters bitwise equal
     after 4 steps, on a mixed set (bf16 groups sharing factor sides 128 and 384 across shapes, plus a vector and an
     fp32-gradient weight that stay on the per-group path)."""
-    shapes = [(128, 384), (128, 384), (128, 128), (384, 128), (384, 128), (128, 512), (96,), (64, 40)]
+    shapes = [(128, 384), (128, 384), (128, 128), (384, 128), (384, 128), (128, 512), (96,), (64, 40), (32, 512),
+              (512, 48)]  # the last two: a dense and a diagonal factor (512^2 > 2 x 32 x 512)
     gen = torch.Generator().manual_seed(5)
     grads = [[(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16 if len(s) == 2 and s != (64, 40)
                                                       else torch.float32).to(DEV) for s in shapes] for _ in range(4)]
     res = []
     for fuse in (True, False):
         W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
-        opt = KronWhiten(W, precision="bf16", draws="host", seed=3, preconditioner_max_skew=math.inf,
+        opt = KronWhiten(W, precision="bf16", draws="host", seed=3, preconditioner_max_skew=skew,
                          preconditioner_init_scale=1.0, fuse_groups=fuse, r2=r2)
         for gs in grads:
             opt.step_math(gs)
