@@ -270,8 +270,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
                     (!CTb || ((p.ldct & 3) == 0 && al(CTb, 8))) && (p.ldx & 3) == 0 &&
                     (!X1 || al(X1, EPI == EPI_RQ ? 8 : 16)) && (!X2 || al(X2, 16));
   float t1 = 0.f, t2 = 0.f;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  // one half of each wave's rows; h is a template constant so that the accumulator indices stay static (a loop
+  // over h is too large to be unrolled, and a dynamic index would move the accumulators to scratch)
+  auto half = [&](auto h_c) {
+    constexpr int h = decltype(h_c)::value;
     // (1) park accumulators: tile (i, j) of this half at local row (i - h FM/2) * 16 + 4g + e, column 16 j + r
 #pragma unroll
     for (int ii = 0; ii < FM / 2; ++ii)
@@ -283,11 +285,28 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     const int grow0 = m0 + wm * TM + h * HR;  // global row of local row 0
     const int gcol0 = n0 + wn * TN;
     // (2) row pass, (3) column pass. An interior tile (fast: inside M and N, strictly above the diagonal for a
-    // SYRK, every leading dimension and base 16-byte compatible) needs no per-element checks, so its loads and
-    // stores are whole vectors and its unrolled loop keeps several iterations' loads in flight; edge tiles check
-    // each element.
-    auto row_pass = [&](auto fast_c) {
-      constexpr bool FAST = decltype(fast_c)::value;
+    // SYRK, every leading dimension and base 16-byte compatible) needs no per-element checks: its loads and stores
+    // are whole vectors (row_pass_fast). Edge tiles check each element (row_pass).
+    // The element-wise epilogue of 4 consecutive columns of one row (acc values in v, X1 / X2 values in q1 / q2).
+    auto epi_math = [&](float* v, const float* q1, const float* q2, const bool* ok, int row, int col) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (EPI == EPI_FACTOR) {
+          v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
+        } else if constexpr (EPI == EPI_PROC || EPI == EPI_PROCB) {
+          v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
+        } else if constexpr (EPI == EPI_STRACE) {
+          v[e] = (s0 * v[e]) * s0;
+        } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
+          v[e] = s0 * v[e];
+          if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
+        } else {
+          v[e] = p.alpha * v[e];
+          if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
+        }
+      }
+    };
+    auto row_pass = [&]() {
       constexpr int IT = HR * (WC / 4) / 64;
       static_assert(IT * 64 == HR * (WC / 4), "row pass: whole iterations");
 #pragma unroll 4
@@ -299,82 +318,111 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         float v[4] = {a.x, a.y, a.z, a.w};
         bool ok[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ok[e] = FAST || (row < p.M && col + e < p.N && !(p.tri && row > col + e));
+        for (int e = 0; e < 4; ++e) ok[e] = row < p.M && col + e < p.N && !(p.tri && row > col + e);
         const long long xo = (long long)row * p.ldx + col;
         float q1[4] = {0.f, 0.f, 0.f, 0.f}, q2[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB) {
-          if constexpr (FAST) {
-            const float4 t = *reinterpret_cast<const float4*>(X1 + xo);
-            q1[0] = t.x; q1[1] = t.y; q1[2] = t.z; q1[3] = t.w;
-          } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q1[e] = ok[e] ? X1[xo + e] : 0.f;
-          }
+          for (int e = 0; e < 4; ++e) q1[e] = ok[e] ? X1[xo + e] : 0.f;
         }
         if constexpr (EPI == EPI_PROC) {
-          if constexpr (FAST) {
-            const float4 t = *reinterpret_cast<const float4*>(X2 + xo);
-            q2[0] = t.x; q2[1] = t.y; q2[2] = t.z; q2[3] = t.w;
-          } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? X2[xo + e] : 0.f;
-          }
+          for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? X2[xo + e] : 0.f;
         }
         if constexpr (EPI == EPI_PROCB) {  // X2 in bf16, row-major with the same leading dimension
           const bf16_t* x2 = reinterpret_cast<const bf16_t*>(X2) + xo;
-          if constexpr (FAST) {
-            const uint2 t = *reinterpret_cast<const uint2*>(x2);
-            q2[0] = bf16_to_f32((bf16_t)(t.x & 0xffff)); q2[1] = bf16_to_f32((bf16_t)(t.x >> 16));
-            q2[2] = bf16_to_f32((bf16_t)(t.y & 0xffff)); q2[3] = bf16_to_f32((bf16_t)(t.y >> 16));
-          } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? bf16_to_f32(x2[e]) : 0.f;
-          }
+          for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? bf16_to_f32(x2[e]) : 0.f;
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (EPI == EPI_FACTOR) {
-            v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
-          } else if constexpr (EPI == EPI_PROC || EPI == EPI_PROCB) {
-            v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
-          } else if constexpr (EPI == EPI_STRACE) {
-            v[e] = (s0 * v[e]) * s0;
-          } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
-            v[e] = s0 * v[e];
-            if (EPI == EPI_RQ && ok[e] && row == col + e) t1 += v[e];
-          } else {
-            v[e] = p.alpha * v[e];
-            if (EPI == EPI_SUMSQ && ok[e]) t1 += v[e] * v[e];
-          }
-        }
+        epi_math(v, q1, q2, ok, row, col);
         if constexpr (EPI == EPI_STRACE) {  // sum C_ij X1_ij over the stored (upper) elements, diagonal included
-          if constexpr (FAST) {
-            const float4 t = *reinterpret_cast<const float4*>(X1 + xo);
-            t2 += v[0] * t.x + v[1] * t.y + v[2] * t.z + v[3] * t.w;
-          } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (ok[e]) t2 += v[e] * X1[xo + e];
-          }
+          for (int e = 0; e < 4; ++e)
+            if (ok[e]) t2 += v[e] * X1[xo + e];
         }
         *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
         if (C) {
           float* dst = C + (long long)row * p.ldc + col;
-          if (FAST || (all && (p.ldc & 3) == 0)) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          if (all && (p.ldc & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
           else
 #pragma unroll
             for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = v[e];
         }
         if (Cb) {
           bf16_t* dst = Cb + (long long)row * p.ldcb + col;
-          if (FAST || (all && (p.ldcb & 3) == 0))
+          if (all && (p.ldcb & 3) == 0)
             *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
                                                          pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
           else
 #pragma unroll
             for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = f32_to_bf16(v[e]);
         }
+      }
+    };
+    // Interior tiles: the X1 / X2 loads of the next U iterations go out before the current U are processed (two
+    // register sets; the batch loop is unrolled so that the set index is static). Stores sit behind branches on
+    // C / Cb, which the scheduler does not move loads across, so without this each wave would have only one
+    // iteration's loads in flight and the epilogue would run at the latency of HBM.
+    auto row_pass_fast = [&]() {
+      constexpr int IT = HR * (WC / 4) / 64, U = 8, NBT = IT / U;
+      static_assert(IT % U == 0, "row pass: whole batches");
+      constexpr bool L1 = EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE;
+      float4 x1[2][U], x2[2][U];
+      uint2 xb[2][U];
+      auto issue = [&](int set, int it0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int idx = lane + 64 * (it0 + u);
+          const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
+          const long long xo = (long long)(grow0 + lr) * p.ldx + gcol0 + lc;
+          if constexpr (L1) x1[set][u] = *reinterpret_cast<const float4*>(X1 + xo);
+          if constexpr (EPI == EPI_PROC) x2[set][u] = *reinterpret_cast<const float4*>(X2 + xo);
+          if constexpr (EPI == EPI_PROCB)
+            xb[set][u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(X2) + xo);
+        }
+      };
+      // one iteration: 4 columns of one row, X1 / X2 values from register set `set`, slot u
+      auto step = [&](int it, int set, int u) {
+        const int idx = lane + 64 * it;
+        const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
+        const int row = grow0 + lr, col = gcol0 + lc;
+        const float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
+        float v[4] = {a.x, a.y, a.z, a.w};
+        const bool ok[4] = {true, true, true, true};
+        float q1[4] = {0.f, 0.f, 0.f, 0.f}, q2[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (L1) {
+          q1[0] = x1[set][u].x; q1[1] = x1[set][u].y; q1[2] = x1[set][u].z; q1[3] = x1[set][u].w;
+        }
+        if constexpr (EPI == EPI_PROC) {
+          q2[0] = x2[set][u].x; q2[1] = x2[set][u].y; q2[2] = x2[set][u].z; q2[3] = x2[set][u].w;
+        }
+        if constexpr (EPI == EPI_PROCB) {
+          const uint2 t = xb[set][u];
+          q2[0] = bf16_to_f32((bf16_t)(t.x & 0xffff)); q2[1] = bf16_to_f32((bf16_t)(t.x >> 16));
+          q2[2] = bf16_to_f32((bf16_t)(t.y & 0xffff)); q2[3] = bf16_to_f32((bf16_t)(t.y >> 16));
+        }
+        epi_math(v, q1, q2, ok, row, col);
+        if constexpr (EPI == EPI_STRACE) t2 += v[0] * q1[0] + v[1] * q1[1] + v[2] * q1[2] + v[3] * q1[3];
+        *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
+        if (C)
+          *reinterpret_cast<float4*>(C + (long long)row * p.ldc + col) = make_float4(v[0], v[1], v[2], v[3]);
+        if (Cb)
+          *reinterpret_cast<uint2*>(Cb + (long long)row * p.ldcb + col) =
+              make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])), pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+      };
+      if constexpr (L1) {
+        issue(0, 0);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          const int set = bt & 1;
+          if (bt + 1 < NBT) issue(set ^ 1, (bt + 1) * U);
+#pragma unroll
+          for (int u = 0; u < U; ++u) step(bt * U + u, set, u);
+        }
+      } else {  // nothing to load: a rolled loop (the fully unrolled form measured slower for store-only epilogues)
+#pragma unroll 4
+        for (int it = 0; it < IT; ++it) step(it, 0, 0);
       }
     };
     auto col_pass = [&](auto fast_c) {
@@ -455,15 +503,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         }
       }
     };
-    if (fast) row_pass(std::true_type{});
-    else row_pass(std::false_type{});
+    if (fast) row_pass_fast();
+    else row_pass();
     __syncthreads();
     if (colpass) {
       if (fast) col_pass(std::true_type{});
       else col_pass(std::false_type{});
       __syncthreads();
     }
-  }
+  };
+  half(std::integral_constant<int, 0>{});
+  half(std::integral_constant<int, 1>{});
   if constexpr (EPI == EPI_RQ || EPI == EPI_SUMSQ || EPI == EPI_STRACE) {
     __shared__ float red[16];
     t1 = block_sum(t1, red);
