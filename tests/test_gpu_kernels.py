@@ -218,12 +218,14 @@ def nlb_full(As, Vs, sign):
                                    (3072, 0)])
 @pytest.mark.parametrize("sign", [1, -1])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("cols,target", [(1, 1024), (0, 1), (0, 1024), (0, 1 << 20)],
-                         ids=["cols", "split1", "split1024", "splitmax"])
+@pytest.mark.parametrize("cols,target", [(-1, 1024), (1, 1024), (2, 1024), (0, 1), (0, 1024), (0, 1 << 20)],
+                         ids=["auto", "cols", "rows", "split1", "split1024", "splitmax"])
 def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, target):
     """Full-storage bound (psgd_pro.py:19-65) of two matrices in one call, against the float64 oracle on the same
     (storage-rounded) matrices. cols = 1: the column-block V A kernel where the layout allows it (n and lda
     multiples of 16 bytes: fp32 n = 100 with a ragged last block, 768, 1000, 3072), else the split-K kernel;
+    cols = 2: the same with A staged through LDS for bf16 (n = 1000: ragged last k chunk and column block), the
+    column-block kernel for fp32; cols = -1: the library's choice by shape;
     cols = 0: the split-K kernel, whose workgroup target 1 gives one k slice, 2^20 the most slices, 1024 the
     default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path). fp32:
     rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
@@ -239,7 +241,7 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, ta
         dev_mats.append(buf.to(DEV)[:, :n])
     lib = L.lib()
     assert lib.psgdk_set_option(2, target) == 0
-    assert lib.psgdk_set_option(4, -1 if cols else 0) == 0
+    assert lib.psgdk_set_option(4, cols) == 0
     try:
         got = nlb_full(dev_mats, [v.to(DEV) for v in Vs], sign)
         again = nlb_full(dev_mats, [v.to(DEV) for v in Vs], sign)
@@ -256,10 +258,12 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, ta
 
 
 @pytest.mark.parametrize("d,k", [(64, 16), (384, 128), (1000, 248), (3072, 768)])
-def test_norm_lower_bound_gram_matches_oracle(hip, d, k):
+@pytest.mark.parametrize("cols", [-1, 1, 2], ids=["auto", "cols", "rows"])
+def test_norm_lower_bound_gram_matches_oracle(hip, d, k, cols):
     """psgdk_norm_lower_bound_gram: the SPD bound (psgd_pro.py:19-41) of P P^T from P (d x k bf16) without forming
     P P^T, for three matrices of different scales, against the float64 oracle on the same (bf16) P: rel 2e-2 (the
-    products run on bf16 V and factors); at most ||P P^T||_2; bitwise repeatable."""
+    products run on bf16 V and factors); at most ||P P^T||_2; bitwise repeatable. Each V A kernel of the
+    rectangular products (cols as psgdk_set_option 4)."""
     from oracle.psgd_oracle import norm_lower_bound
     Ps = [((0.5 + b) * rnd(d, k, seed=d + k + b)).to(torch.bfloat16) for b in range(3)]
     Vs = [rnd(32, d, seed=7 + b) for b in range(3)]
@@ -272,7 +276,11 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k):
         L.call_ws(L.lib().psgdk_norm_lower_bound_gram, d, k, len(Ps), L.ptrs(Pd), L.ptrs(Ptd), L.ptrs(Vd), L.ptrs(outs),
                   ws=K._WS, device=Pd[0].device, stream=L.stream_of(Pd[0]))
         return [float(o) for o in outs]
-    got, again = run(), run()
+    assert L.lib().psgdk_set_option(4, cols) == 0
+    try:
+        got, again = run(), run()
+    finally:
+        L.lib().psgdk_set_option(4, -1)
     assert got == again
     for P, V, g in zip(Ps, Vs, got):
         A = P.double() @ P.double().T
@@ -281,7 +289,7 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k):
         assert g <= float(torch.linalg.matrix_norm(A, 2)) * (1 + 2e-2)
 
 
-@pytest.mark.parametrize("cols", [1, 0], ids=["cols", "split"])
+@pytest.mark.parametrize("cols", [-1, 1, 2, 0], ids=["auto", "cols", "rows", "split"])
 def test_norm_lower_bound_full_sixteen_matrices(hip, cols):
     """A full group (16 matrices, the most one call takes) of 320 x 320 bf16 SPD matrices of different scales:
     every matrix's bound against the float64 oracle (rel 2e-2), both V A kernels."""
@@ -293,7 +301,7 @@ def test_norm_lower_bound_full_sixteen_matrices(hip, cols):
         mats.append(((0.5 + b) * (X @ X.T)).to(torch.bfloat16))
         Vs.append(rnd(32, n, seed=200 + b))
     lib = L.lib()
-    assert lib.psgdk_set_option(4, -1 if cols else 0) == 0
+    assert lib.psgdk_set_option(4, cols) == 0
     try:
         got = nlb_full([M.to(DEV) for M in mats], [v.to(DEV) for v in Vs], 1)
     finally:
