@@ -160,16 +160,18 @@ typedef struct psgdk_apply_opts {
 /* One preconditioner update of every parameter in the group: update_2d (psgd_pro_fast.py:168-192), i.e.
  * update_precond_kron_whiten_q0p5eq1p5 (psgd_pro.py:114-137) with P = Q^T Q cached: Pg = P1 (G + (damping +
  * grad_eps |G|) noise) P2; per factor: term1 (SYRK or sums of squares), norm lower bound, L EMA, Q update,
- * Procrustes rotation (psgd_pro.py:71-94); then P refresh. Draws are passed in: noise[b] is m x n N(0,1); V[b]
- * holds, per dense factor in dimension order, two 32 x d blocks (the SPD bound's start, then the skew bound's).
+ * Procrustes rotation (psgd_pro.py:71-94); then P refresh. Draws are passed in: noise[b] is m x n N(0,1) stored in
+ * the gradient's dtype (g_dtype), as randn_like(G) draws it (psgd_pro_fast.py:202); V[b] (fp32) holds, per dense
+ * factor in dimension order, two 32 x d blocks (the SPD bound's start, then the skew bound's).
  * The balancing coin (psgd_pro.py:138-139) is the caller's (psgdk_kron2d_balance). */
-int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const void* const* noise,
                         const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
 
 /* The update of several groups in one call: the same operation as psgdk_kron2d_update on each group, with the
  * factor work of all groups batched by factor side (each launch covers up to 64 factors of one side, from any
- * group and either dimension). Every group must be on the bf16 path (prec bf16, two dense factors with Qt16 / P16
- * shadows, sides multiples of 8, tri = 0); lr, betaL, r2 and tri must agree across opts[]; damping and grad_eps
+ * group and either dimension). Every group must be on the bf16 path (prec bf16, two factors, dense or diagonal with
+ * at least one dense, every dense factor with its Qt16 / P16 shadows, sides multiples of 8, tri = 0); lr, betaL,
+ * r2 and tri must agree across opts[]; damping and grad_eps
  * are per group. noise[g] and V[g] are the group's arrays as in psgdk_kron2d_update. Results are bitwise those of
  * one psgdk_kron2d_update per group. The work runs on side streams the library creates once per device (default
  * priority; psgdk_set_option 6), forked from and joined back to `stream` with events; while `stream` is being
@@ -177,7 +179,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
  * loop of update_2d calls
  * (psgd_pro_fast.py:351-368; the reference's batch=True stacks same-shape parameters, psgd_pro_fast.py:327-349). */
 int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
-                               const psgdk_update_opts_t* const* opts, const float* const* const* noise,
+                               const psgdk_update_opts_t* const* opts, const void* const* const* noise,
                                const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
 
 /* Precondition, clip and update: pre = P1 G P2 (apply_2d, psgd_pro_fast.py:156-161 = precond_grad_kron,

@@ -170,16 +170,18 @@ def gram(Pg, i, dense):
 
 
 def update_preconditioner(Q, L, G, draws, lr=0.1, betaL=0.9, damping=1e-9, grad_eps=None, r2=False, trace=None,
-                          draw_dtype=torch.float32):
+                          draw_dtype=torch.float32, noise_dtype=None):
     """psgd_pro.py:114-139 (update_precond_kron_whiten_q0p5eq1p5), in place on Q and L, with the draws taken from
     `draws` in psgd_pro.py's order. The normals are drawn in draw_dtype (psgd_pro.py draws them in the gradient's
-    dtype: float32 for the float32 models every comparison here uses) and cast to the working dtype. grad_eps
-    overrides finfo(G.dtype).eps in the damping scale (the reference uses the gradient's own dtype; a bfloat16
-    gradient upcast for this oracle passes bfloat16's eps)."""
+    dtype: float32 for the float32 models every comparison here uses) and cast to the working dtype; noise_dtype
+    (default draw_dtype) overrides the dtype of the gradient-shaped noise alone, as psgd_pro_fast.draw_normals draws
+    it like the gradient and the 32 x d starts like the factors (psgd_pro_fast.py:200-206): a bfloat16 gradient
+    upcast for this oracle passes bfloat16. grad_eps overrides finfo(G.dtype).eps in the damping scale (the
+    reference uses the gradient's own dtype; a bfloat16 gradient upcast for this oracle passes bfloat16's eps)."""
     eps = torch.finfo(G.dtype).eps if grad_eps is None else grad_eps
     numel = G.numel()
     damp = damping + eps * G.abs()
-    noise = draws.normal(G.shape, draw_dtype).to(G.dtype)
+    noise = draws.normal(G.shape, noise_dtype or draw_dtype).to(G.dtype)
     Pg = precondition(Q, G + damp * noise)
     for i, q in enumerate(Q):
         if q.dim() < 2:
@@ -225,7 +227,8 @@ class OracleKron:
     def __init__(self, params, preconditioner_max_size=math.inf, preconditioner_max_skew=1.0,
                  preconditioner_init_scale=None, lr_params=0.001, lr_preconditioner=0.1, betaL=0.9, damping=1e-9,
                  momentum=0.0, grad_clip_max_amps=(2.0, 10.0), preconditioner_update_probability=1.0,
-                 update_preconditioner_first=True, whiten_grad=True, seed=0, dtype=None, grad_eps=None, r2=False):
+                 update_preconditioner_first=True, whiten_grad=True, seed=0, dtype=None, grad_eps=None, r2=False,
+                 noise_dtype=None):
         self.params = list(params)  # updated in place
         self.max_size, self.max_skew = preconditioner_max_size, preconditioner_max_skew
         self.lr_params, self.lr_preconditioner = lr_params, lr_preconditioner
@@ -237,6 +240,7 @@ class OracleKron:
         self.whiten_grad = whiten_grad
         self.dtype = dtype
         self.grad_eps, self.r2 = grad_eps, r2
+        self.noise_dtype = noise_dtype
         self.draws = Draws(seed)
         self.Q = self.L = None
         self.ms, self.counter_m = None, 0
@@ -254,7 +258,8 @@ class OracleKron:
     def _update(self, srcs):
         for Q, L, g in zip(self.Q, self.L, srcs):
             update_preconditioner(Q, L, g, self.draws, lr=self.lr_preconditioner, betaL=self.betaL,
-                                  damping=self.damping, grad_eps=self.grad_eps, r2=self.r2, trace=self.trace)
+                                  damping=self.damping, grad_eps=self.grad_eps, r2=self.r2, trace=self.trace,
+                                  noise_dtype=self.noise_dtype)
 
     @torch.no_grad()
     def step(self, grads):

@@ -906,7 +906,7 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
 // The update of ng bf16-path groups: per-group noise, Y and Pg, then the items of every dense factor in batches of
 // one side d (largest first), the items of a batch ordered by their other side.
 int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_update_opts_t* const* os,
-                      const float* const* const* noise, const float* const* const* V, void* ws, size_t* ws_bytes,
+                      const void* const* const* noise, const float* const* const* V, void* ws, size_t* ws_bytes,
                       hipStream_t st) {
   Ws w(ws);
   std::vector<std::vector<bf16_t*>> Xb(ng), YTb(ng), Pgb(ng), PgTb(ng);
@@ -992,7 +992,10 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
       EwArgs a;
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
-      for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.in3[b] = g->P[1][b]; a.out2[b] = Xb[gi][b]; }
+      for (int b = 0; b < nb; ++b) {
+        a.in[b] = g->G[b]; a.in2[b] = reinterpret_cast<const float*>(noise[gi][b]); a.in3[b] = g->P[1][b];
+        a.out2[b] = Xb[gi][b];
+      }
       PSGDK_HIP(noise_t_launch(a, st), "noise (transposed, column-scaled)");
       B16Out out;
       out.ldcb = n; out.ldct = m;
@@ -1005,7 +1008,8 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
         std::memset(&a, 0, sizeof a);
         a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
         for (int b = 0; b < nb; ++b) {
-          a.in[b] = g->G[b]; a.in2[b] = noise[gi][b]; a.out2[b] = Xb[gi][b]; a.in3[b] = d0 ? nullptr : g->P[0][b];
+          a.in[b] = g->G[b]; a.in2[b] = reinterpret_cast<const float*>(noise[gi][b]); a.out2[b] = Xb[gi][b];
+          a.in3[b] = d0 ? nullptr : g->P[0][b];
         }
         PSGDK_HIP(noise_launch(a, st), "noise");
       }
@@ -1063,7 +1067,7 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   return PSGDK_OK;
 }
 
-int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+int b16_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const void* const* noise,
                const float* const* V, void* ws, size_t* ws_bytes, hipStream_t st) {
   return b16_update_groups(1, &g, &o, &noise, &V, ws, ws_bytes, st);
 }
@@ -1535,7 +1539,7 @@ int psgdk_unpack(int64_t n, int nb, const float* const* Pk, float* const* C, int
 }
 
 // ------------------------------------------------------------------------------------------------------------
-int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const float* const* noise,
+int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, const void* const* noise,
                         const float* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
   PSGDK_TRY(check_group(g));
   if (!o) return fail(PSGDK_EINVAL, "null options");
@@ -1568,7 +1572,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
     EwArgs a;
     std::memset(&a, 0, sizeof a);
     a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = o->damping; a.f1 = o->grad_eps;
-    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = noise[b]; a.out[b] = X[b]; }
+    for (int b = 0; b < nb; ++b) { a.in[b] = g->G[b]; a.in2[b] = reinterpret_cast<const float*>(noise[b]); a.out[b] = X[b]; }
     PSGDK_HIP(noise_launch(a, st), "noise");
   }
   // Pg = P1 X P2
@@ -1629,7 +1633,7 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
 }
 
 int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
-                               const psgdk_update_opts_t* const* opts, const float* const* const* noise,
+                               const psgdk_update_opts_t* const* opts, const void* const* const* noise,
                                const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream) {
   if (ngroups < 1 || ngroups > PSGDK_MAX_GROUPS)
     return fail(PSGDK_EINVAL, "ngroups = %d: must be in 1..%d", ngroups, PSGDK_MAX_GROUPS);

@@ -20,7 +20,8 @@ struct EwArgs {
   float* sc[MAXB];         // device scalars
 };
 
-// X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N null: X = G)  (psgd_pro.py:121-123);
+// X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N in G's dtype dt; N null: X = G)
+// (psgd_pro.py:121-123);
 // in3 (optional): a row scale applied to X (a diagonal P1 of P1 X P2)
 hipError_t noise_launch(const EwArgs& a, hipStream_t st);
 // out2 = bf16 (X diag(in3))^T with X as noise_launch (a diagonal P2 folded into the transposed operand of P1 X P2)

@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   const int b = blockIdx.x / blocks_per;
   long long beg, end;
   const void* G = a.in[b];
-  const float* N = a.in2[b];
+  const void* N = a.in2[b];  // the noise, in G's dtype
   float* X = a.out[b];
   bf16_t* Xb = reinterpret_cast<bf16_t*>(a.out2[b]);
   const float* rsc = a.in3[b];  // optional row scale (a diagonal P1 folded into the input of P1 X P2)
@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
       float g[8], nz[8];
       ew_load8_dt(G, a.dt, 8 * v, g);
       if (N) {
-        ew_load8(N + 8 * v, nz);
+        ew_load8_dt(N, a.dt, 8 * v, nz);
 #pragma unroll
         for (int e = 0; e < 8; ++e) g[e] = g[e] + (a.f0 + a.f1 * fabsf(g[e])) * nz[e];
       }
@@ -98,7 +98,7 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   ew_range(total, blocks_per, beg, end);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     const float g = ldv(G, a.dt, i);
-    float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[i] : g;
+    float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, i) : g;
     if (rsc) x *= rsc[i / a.n];
     if (X) X[i] = x;
     if (Xb) Xb[i] = f32_to_bf16(x);
@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(256) noise_t_kernel(const EwArgs a) {
   const int b = blockIdx.x / (tm * tn), tile = blockIdx.x % (tm * tn);
   const int I = tile / tn, J = tile % tn;
   const void* G = a.in[b];
-  const float* N = a.in2[b];
+  const void* N = a.in2[b];  // the noise, in G's dtype
   const float* csc = a.in3[b];
   bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
   const int tid = threadIdx.x, c = tid & 63, r0 = tid >> 6;
@@ -133,7 +133,7 @@ __global__ void __launch_bounds__(256) noise_t_kernel(const EwArgs a) {
     if (gi < m && gj < n) {
       const long long o = gi * n + gj;
       const float g = ldv(G, a.dt, o);
-      x = N ? g + (a.f0 + a.f1 * fabsf(g)) * N[o] : g;
+      x = N ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, o) : g;
       if (csc) x *= csc[gj];
     }
     t[r][c] = x;

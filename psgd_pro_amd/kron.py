@@ -123,7 +123,7 @@ class KronWhiten:
         # by factor side (results are bitwise those of one call per group)
         self._fuse = bool(fuse_groups)
         self._graphs, self._seen = {}, set()
-        self._draw_buf = None
+        self._draw_buf = self._draw_buf16 = None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
             self._init([p.squeeze() for p in self._params_with_grad], preconditioner_init_scale)
@@ -240,38 +240,54 @@ class KronWhiten:
         s.g_dtype = L.dtype_code(dt)
         return dt
 
-    def _draw_update(self, srcs):
-        """Normals of one update (noise, then per dense factor the SPD and skew starts) in one device buffer,
-        in psgd_pro.py's order; returns (per-parameter noise views, per-parameter V views, balance coins)."""
-        sizes = []
-        for p in self._params:
-            sizes.append((p.m * p.n, sum(2 * _K * d for d in self._dense_dims(p))))
-        total = sum(a + b for a, b in sizes)
-        dev = srcs[0].device
+    def _draw_update(self, grads):
+        """Normals of one update (noise, then per dense factor the SPD and skew starts) in psgd_pro.py's order;
+        returns (per-parameter noise views, per-parameter V views, balance coins). The noise is drawn in the dtype
+        of the tensor the update reads (the gradient, or the float32 momentum buffer when whiten_grad is off), as
+        randn_like(G) does (psgd_pro_fast.py:200-206), the starts in float32 (the factors' dtype). Two persistent
+        device buffers (fixed addresses: captured graphs read them), one per dtype, each view at a multiple of 8
+        elements."""
+        ndt = [g.dtype if self._whiten_grad else torch.float32 for g in grads]
+        r8 = lambda x: (x + 7) // 8 * 8
+        lay, tot = [], {torch.float32: 0, torch.bfloat16: 0}  # per parameter: (noise offset, V offset, sizes)
+        for p, dt in zip(self._params, ndt):
+            a, b = p.m * p.n, sum(2 * _K * d for d in self._dense_dims(p))
+            no = tot[dt]
+            tot[dt] += r8(a)
+            vo = tot[torch.float32]
+            tot[torch.float32] += r8(b)
+            lay.append((no, vo, a, b))
+        dev = grads[0].device
+        bufs = {}
+        for dt, attr in ((torch.float32, "_draw_buf"), (torch.bfloat16, "_draw_buf16")):
+            cur = getattr(self, attr, None)
+            if cur is None or cur.numel() < max(1, tot[dt]):
+                cur = torch.empty(max(1, tot[dt]), device=dev, dtype=dt)
+                setattr(self, attr, cur)
+            bufs[dt] = cur
         coins = []
-        # one persistent device buffer (fixed address: captured graphs read it), refilled before the step's work
-        if self._draw_buf is None or self._draw_buf.numel() < max(1, total):
-            self._draw_buf = torch.empty(max(1, total), device=dev, dtype=torch.float32)
-        flat = self._draw_buf[:total]
         if self._draws == "host":
-            parts = []
-            for p, (a, b) in zip(self._params, sizes):
-                parts.append(torch.randn(a, generator=self._gen))
+            host = {dt: torch.zeros(max(1, tot[dt]), dtype=dt) for dt in bufs}
+            for p, dt, (no, vo, a, b) in zip(self._params, ndt, lay):
+                host[dt][no:no + a] = torch.randn(a, generator=self._gen, dtype=dt)
+                o = vo
                 for d in self._dense_dims(p):
-                    parts.append(torch.randn(_K * d, generator=self._gen))
-                    parts.append(torch.randn(_K * d, generator=self._gen))
+                    for _ in range(2):
+                        host[torch.float32][o:o + _K * d] = torch.randn(_K * d, generator=self._gen)
+                        o += _K * d
                 coins.append(self._rand() < 0.01)
-            if total:
-                flat.copy_(torch.cat(parts).pin_memory(), non_blocking=True)
+            for dt in bufs:
+                if tot[dt]:
+                    bufs[dt][:tot[dt]].copy_(host[dt][:tot[dt]].pin_memory(), non_blocking=True)
         else:
             coins = (torch.rand(len(self._params), generator=self._gen) < 0.01).tolist()
-            if total:
-                torch.randn(total, device=dev, dtype=torch.float32, out=flat)
-        noise, V, off = [], [], 0
-        for a, b in sizes:
-            noise.append(flat[off:off + a])
-            V.append(flat[off + a:off + a + b] if b else None)
-            off += a + b
+            for dt in bufs:
+                if tot[dt]:
+                    torch.randn(tot[dt], device=dev, dtype=dt, out=bufs[dt][:tot[dt]])
+        noise, V = [], []
+        for dt, (no, vo, a, b) in zip(ndt, lay):
+            noise.append(bufs[dt][no:no + a])
+            V.append(bufs[torch.float32][vo:vo + b] if b else None)
         return noise, V, coins
 
     # Groups share no state (each owns its factors, shadows and parameters), so their update and apply chains

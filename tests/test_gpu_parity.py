@@ -52,10 +52,12 @@ def run_pair(shapes, steps, seed=0, skew=1.0, max_size=math.inf, prec="fp32", gd
               momentum=momentum, update_preconditioner_first=update_first, whiten_grad=whiten_grad)
     opt = KronWhiten(Wg, precision=prec, draws="host", seed=seed, tri=tri, r2=r2, **kw)
     opt.capture = True
+    # the noise is drawn like the tensor the update reads (the gradient, or the float32 momentum buffer)
+    ndt = gdt if whiten_grad else torch.float32
     ref = O.OracleKron([torch.zeros(s, dtype=ref_dtype) for s in shapes], seed=seed, dtype=ref_dtype,
-                       grad_eps=grad_eps, r2=r2, **kw)
+                       grad_eps=grad_eps, r2=r2, noise_dtype=ndt, **kw)
     o32 = O.OracleKron([torch.zeros(s, dtype=torch.float32) for s in shapes], seed=seed, dtype=torch.float32,
-                       grad_eps=grad_eps, r2=r2, **kw) if baseline else None
+                       grad_eps=grad_eps, r2=r2, noise_dtype=ndt, **kw) if baseline else None
     worst = {}
     base = {}
     for t in range(steps):
