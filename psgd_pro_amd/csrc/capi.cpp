@@ -343,6 +343,9 @@ void nlb_take(Ws& w, int64_t n, int nb, NlbWs& o) {
   }
 }
 
+// Whether rform_kernel's row statistics of an n x n matrix (2 n ceil(n / 64) floats) fit in a bound's part buffer.
+bool rform_stats_fit(int64_t n, const NlbWs& w) { return 2 * n * ((n + 63) / 64) <= w.part_cols * NLB_K; }
+
 NlbArgs nlb_args(int64_t n, int sign, int nb, const float* const* A, int64_t lda, const NlbWs& w) {
   NlbArgs a;
   std::memset(&a, 0, sizeof a);
@@ -408,8 +411,10 @@ bool vmm_cols_ok(int64_t n, int nb, const void* const* A, int64_t lda, int esz, 
   return true;
 }
 
+// stats_in_part: the producer of the (skew) matrices left per-(row, column block) row statistics in w.part
+// (rform_kernel's aux output; rform_stats_fit says where they fit), reduced here instead of a pass over A.
 int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_bf16, const float* const* V,
-                 const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
+                 const NlbFinal& fin, const NlbWs& w, hipStream_t st, bool stats_in_part = false) {
   const float* Af[MAXB];
   for (int b = 0; b < nb; ++b) Af[b] = reinterpret_cast<const float*>(A[b]);
   NlbArgs a = nlb_args(n, sign, nb, Af, lda, w);
@@ -418,7 +423,8 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
   a.vmm_cols = g_vmm_cols != 0 && vmm_cols_ok(n, nb, A, lda, a_bf16 ? 2 : 4, w) ? (a_bf16 && g_vmm_cols != 1 ? 2 : 1) : 0;
   a.ssc = a.vmm_cols ? 64 : 128;
   if (a.vmm_cols && a.vmm_u == 8) a.vmm_u = 4;
-  PSGDK_HIP(nlb_full_launch(a, 0, a_bf16, 0, st), "row norms");
+  if (stats_in_part) PSGDK_HIP(nlb_full_launch(a, 3, a_bf16, 0, st), "row norms from partials");
+  else PSGDK_HIP(nlb_full_launch(a, 0, a_bf16, 0, st), "row norms");
   for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
   PSGDK_HIP(nlb_full_launch(a, 1, a_bf16, 0, st), "nlb init");
   float* const* vb[2] = {w.vb0, w.vb1};
@@ -797,11 +803,17 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
       PSGDK_TRY(run_b16(k, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }
   }
-  {  // R = Qn^T - Qn -> bf16 (r2: and the partials of sum R * Qn)
+  // R = Qn^T - Qn -> bf16 (r2: and the partials of sum R * Qn), with the skew bound's row statistics of the bf16 R
+  // as a by-product (no separate pass over R)
+  const bool rstats = rform_stats_fit(d, nw);
+  {
     EwArgs a;
     std::memset(&a, 0, sizeof a);
     a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
-    for (int b = 0; b < nb; ++b) { a.in[b] = it[b]->Qn; a.out2[b] = it[b]->Rb; a.sc[b] = o->r2 ? it[b]->rtp : nullptr; }
+    for (int b = 0; b < nb; ++b) {
+      a.in[b] = it[b]->Qn; a.out2[b] = it[b]->Rb; a.sc[b] = o->r2 ? it[b]->rtp : nullptr;
+      a.aux[b] = rstats ? nw.part[b] : nullptr;
+    }
     PSGDK_HIP(rform_launch(a, st), "R = Q^T - Q");
   }
   {
@@ -811,7 +823,7 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
     const void* Rc[MAXB];
     const float* Vk[MAXB];
     for (int b = 0; b < nb; ++b) { fin.coef[b] = it[b]->rs; Rc[b] = it[b]->Rb; Vk[b] = it[b]->Vk; }
-    PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st));
+    PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 1, Vk, fin, nw, st, rstats));
   }
   if (o->r2) {  // procrustes_step_r2 (psgd_pro_fast.py:141-153)
     // S = rs^2 R R^T in the RQ^T buffer (bf16); M = a rs R - a^2/2 S in the (unused) fp32 RQ buffer, as bf16

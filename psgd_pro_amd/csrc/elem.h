@@ -18,6 +18,7 @@ struct EwArgs {
   float* out[MAXB];
   void* out2[MAXB];
   float* sc[MAXB];         // device scalars
+  float* aux[MAXB];        // kernel-specific extra output
 };
 
 // X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N in G's dtype dt; N null: X = G)
@@ -29,7 +30,8 @@ hipError_t noise_t_launch(const EwArgs& a, hipStream_t st);
 // out[i] = sum_j X[i][j]^2 of a bf16 m x n matrix (a diagonal factor's term1 from the bf16 Pg or Pg^T)
 hipError_t rowsq_launch(const EwArgs& a, hipStream_t st);
 // R = Q^T - Q (sign = +1) or Q - Q^T (sign = -1), square d x d, plus an optional bf16 copy in out2
-// (psgd_pro.py:87; psgd_pro_fast.py:147)
+// (psgd_pro.py:87; psgd_pro_fast.py:147); aux (optional, with out2): per (row, 64-column block) sums of squares and
+// maxima of |.| of the bf16 R, block-major: aux[cb d + i], then aux[T d + cb d + i] (T = ceil(d / 64))
 hipError_t rform_launch(const EwArgs& a, hipStream_t st);
 // Procrustes step size from the trace partials     (psgd_pro.py:91-93)
 hipError_t proc_scalar_launch(const EwArgs& a, hipStream_t st);

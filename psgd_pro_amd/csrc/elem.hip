@@ -53,6 +53,20 @@ static int ew_blocks(long long total) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// x of the lane that DPP control C names (a move inside a row of 16 lanes; no LDS traffic, unlike a shuffle)
+template <int C>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), C, 0xf, 0xf, false));
+}
+// Sum and max over each row of 16 lanes, every lane getting the row's result: quad_perm(1,0,3,2) and (2,3,0,1) make
+// quad results, row_half_mirror combines the two quads of each half, row_mirror the two halves.
+__device__ __forceinline__ void row16_sum_max(float& s, float& m) {
+  s += dpp<0xB1>(s); m = fmaxf(m, dpp<0xB1>(m));
+  s += dpp<0x4E>(s); m = fmaxf(m, dpp<0x4E>(m));
+  s += dpp<0x141>(s); m = fmaxf(m, dpp<0x141>(m));
+  s += dpp<0x140>(s); m = fmaxf(m, dpp<0x140>(m));
+}
+
 // 8 consecutive elements of a bf16 (dt = 1) or fp32 buffer at element offset i (16-byte aligned), as floats
 __device__ __forceinline__ void ew_load8_dt(const void* p, int dt, long long i, float (&x)[8]) {
   if (dt) ew_load8(reinterpret_cast<const bf16_t*>(p) + i, x);
@@ -231,6 +245,8 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   __syncthreads();
   // out(rb, cb)[r][c] = sg (src_t[c][r] - src[r][c]): (I, J) from (qb, qa), (J, I) from (qa, qb)
   float tr = 0.f;  // sum of R_ij Q_ij (out-of-range elements are zero in both staged tiles)
+  float* __restrict__ st = a.aux[b];
+  __shared__ float rsq[2][64], rmx[2][64];  // row statistics of the two tiles, written out as 256-byte runs
   auto emit = [&](const float* src, const float* srct, int rb, int cb) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -240,6 +256,21 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
       for (int e = 0; e < 4; ++e) {
         v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
         tr += v[e] * src[r * TP + c4 + e];
+      }
+      if (st) {  // row statistics of the bf16 R over this tile's 64 columns (the 16 lanes of row r), fixed tree
+        float s2 = 0.f, mx = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float q = bf16_to_f32(f32_to_bf16(v[e]));
+          s2 += q * q;
+          mx = fmaxf(mx, fabsf(q));
+        }
+        row16_sum_max(s2, mx);
+        if ((tid & 15) == 0) {
+          const int t = rb == I ? 0 : 1;  // tile (I, J) or (J, I)
+          rsq[t][r] = s2;
+          rmx[t][r] = mx;
+        }
       }
       const long long o = (long long)gi * ld + gj;
       if (vec) {
@@ -259,6 +290,15 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   };
   emit(qa, qb, I, J);
   if (I != J) emit(qb, qa, J, I);
+  if (st) {
+    __syncthreads();
+    const int t = tid >> 6, r = tid & 63;  // threads 0-63: tile (I, J), 64-127: tile (J, I)
+    const int rb = t ? J : I, cb = t ? I : J, gi = rb * 64 + r;
+    if (t < 2 && (t == 0 || I != J) && gi < d) {
+      st[(long long)cb * d + gi] = rsq[t][r];
+      st[(long long)(T + cb) * d + gi] = rmx[t][r];
+    }
+  }
   if (a.sc[b]) {
     __shared__ float red[16];
     tr = block_sum(tr, red);

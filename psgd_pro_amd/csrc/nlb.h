@@ -66,7 +66,8 @@ hipError_t nlb_rownorm_launch(const NlbArgs& a, hipStream_t st);
 hipError_t nlb_init_launch(const NlbArgs& a, hipStream_t st);
 hipError_t nlb_reduce_launch(const NlbArgs& a, int normalize_in, hipStream_t st);
 hipError_t nlb_final_launch(const NlbArgs& a, const NlbFinal& f, hipStream_t st);
-// fully stored matrices: stage 0 row norms (rn2, rpart = row max |A|, cpart = diagonal), 1 init, 2 one V A product
+// fully stored matrices: stage 0 row norms (rn2, rpart = row max |A|, cpart = diagonal), 1 init, 2 one V A product,
+// 3 the stage-0 outputs of a skew matrix from the per-(row, 64-column block) partials its producer left in part
 hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st);
 hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);

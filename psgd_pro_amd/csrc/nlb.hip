@@ -281,6 +281,35 @@ __global__ void __launch_bounds__(256) rownorm_full_kernel(const NlbArgs p) {
   }
 }
 
+// The same row statistics from per-(row, 64-column block) partials in part[b] that the producer of a skew matrix
+// left (rform: sums of squares at part[cb n + i], then maxima of |.| at part[(T + cb) n + i]). 64 rows per
+// workgroup, four threads per row over quarters of the blocks, combined through LDS in quarter order. The diagonal
+// of R = +-(Q^T - Q) is zero. grid: nb * ceil(n / 64).
+__global__ void __launch_bounds__(256) rowstats_reduce_kernel(const NlbArgs p) {
+  __shared__ float ps[4][64], pm[4][64];
+  const int n = p.n, T = (n + 63) / 64, nrb = (n + 63) / 64;
+  const int b = blockIdx.x / nrb, r = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int i = (blockIdx.x % nrb) * 64 + r;
+  const float* __restrict__ S = p.part[b];
+  const int c0 = q * T / 4, c1 = (q + 1) * T / 4;
+  float s = 0.f, m = 0.f;
+  if (i < n) {
+#pragma unroll 4
+    for (int c = c0; c < c1; ++c) {
+      s += S[(long long)c * n + i];
+      m = fmaxf(m, S[(long long)(T + c) * n + i]);
+    }
+  }
+  ps[q][r] = s;
+  pm[q][r] = m;
+  __syncthreads();
+  if (q == 0 && i < n) {
+    p.rn2[b][i] = ((ps[0][r] + ps[1][r]) + ps[2][r]) + ps[3][r];
+    p.rpart[b][i] = fmaxf(fmaxf(pm[0][r], pm[1][r]), fmaxf(pm[2][r], pm[3][r]));
+    p.cpart[b][i] = 0.f;
+  }
+}
+
 // Eight consecutive elements of T at a 16-byte aligned address, as floats.
 __device__ __forceinline__ void load8(const bf16_t* src, float (&x)[8]) {
   const uint4 u = *reinterpret_cast<const uint4*>(src);
@@ -988,7 +1017,9 @@ hipError_t gram_launch(const GramArgs& a, int stage, hipStream_t st) {
 }
 
 hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normalize, hipStream_t st) {
-  if (stage == 0) {
+  if (stage == 3) {
+    hipLaunchKernelGGL(rowstats_reduce_kernel, dim3(((a.n + 63) / 64) * a.nb), dim3(256), 0, st, a);
+  } else if (stage == 0) {
     const int nrb = (a.n + 3) / 4;
     if (a_bf16) hipLaunchKernelGGL(rownorm_full_kernel<bf16_t>, dim3(nrb * a.nb), dim3(256), 0, st, a);
     else hipLaunchKernelGGL(rownorm_full_kernel<float>, dim3(nrb * a.nb), dim3(256), 0, st, a);
