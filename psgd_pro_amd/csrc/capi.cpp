@@ -870,17 +870,17 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
     }
   } else {
     int nt = 0;
-    {  // RQ = R Qn / (bound + sn) -> bf16 (or fp32, option 7) + RQ^T bf16, trace partials (tr(R RQ) reads the
-       // bf16 R of the product). RQ enters the Q update as the correction a RQ; the product already comes from
-       // bf16 operands, so its bf16 rounding adds an error of the same size and halves that operand's bytes
+    {  // RQ = R Qn / (bound + sn) -> RQ^T bf16 (and, option 7 = 0, RQ fp32), trace partials (tr(R RQ) reads the
+       // bf16 R of the product). RQ enters the Q update as the correction a RQ, read from the bf16 RQ^T that the
+       // second product takes as its B operand; the product already comes from bf16 operands, so its bf16 rounding
+       // adds an error of the same size, and no second copy of RQ is written
       B16Out out;
-      out.ldc = d; out.ldcb = d; out.ldct = d;
+      out.ldc = d; out.ldct = d;
       EpiSpec e;
       e.epi = EPI_RQ; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
         A[b] = it[b]->Rb; B[b] = it[b]->QnTb; out.CTb[b] = it[b]->RQTb;
-        if (g_rq16) out.Cb[b] = reinterpret_cast<bf16_t*>(it[b]->RQ);
-        else out.C[b] = it[b]->RQ;
+        if (!g_rq16) out.C[b] = it[b]->RQ;
         e.X1[b] = reinterpret_cast<const float*>(it[b]->Rb); e.s[b] = it[b]->rs; e.part[b] = it[b]->tpart;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, &nt, st));
@@ -899,7 +899,8 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
       e.epi = g_rq16 ? EPI_PROCB : EPI_PROC; e.ldx = d;
       for (int b = 0; b < nb; ++b) {
         A[b] = it[b]->Rb; B[b] = it[b]->RQTb; out.C[b] = it[b]->Q; out.CTb[b] = it[b]->Qt16;
-        e.X1[b] = it[b]->Qn; e.X2[b] = it[b]->RQ; e.s[b] = it[b]->pc;
+        e.X1[b] = it[b]->Qn; e.s[b] = it[b]->pc;
+        e.X2[b] = g_rq16 ? reinterpret_cast<const float*>(it[b]->RQTb) : it[b]->RQ;
       }
       PSGDK_TRY(run_b16(nb, d, d, d, A, d, B, d, out, e, 0, 0, nullptr, st));
     }

@@ -15,7 +15,8 @@ enum Epi : int {
   EPI_SCALE = 3,   // C = s[0] * acc
   EPI_RQ = 4,      // C = s[0] * acc and trace partials of tr(C), tr(s[0] X1 C) into part[]  (Procrustes RQ)
   EPI_SUMSQ = 5,   // C = alpha * acc and partial sums of C^2 into part[]                    (apply + clip stats)
-  EPI_PROCB = 7,   // bf16 kernel only: EPI_PROC with X2 read as bf16 (RQ kept in bf16 by its producer)
+  EPI_PROCB = 7,   // bf16 kernel only: EPI_PROC with X2 = (R Q)^T in bf16, row stride ldx (the transposed copy
+                   // that is also the product's B operand), read at (col, row)
   EPI_STRACE = 6,  // SYRK only: C = (s[0] acc) s[0] (the scale applied twice, so that acc = 0 gives 0 for any
                    // finite s[0]), and partials of sum_ij C_ij X1_ij over the whole symmetric C into part[2 t + 1]
                    // (part[2 t] = 0)                                    (Procrustes r2: S = Rn^T Rn, sum(S * Q))

@@ -293,8 +293,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       for (int e = 0; e < 4; ++e) {
         if constexpr (EPI == EPI_FACTOR) {
           v[e] = q1[e] - s0 * (v[e] - s1 * q1[e]);
-        } else if constexpr (EPI == EPI_PROC || EPI == EPI_PROCB) {
+        } else if constexpr (EPI == EPI_PROC) {
           v[e] = ok[e] ? q1[e] + s0 * q2[e] + 0.5f * s0 * s0 * s1 * v[e] : 0.f;
+        } else if constexpr (EPI == EPI_PROCB) {  // v holds a RQ + a^2/2 s1 acc (tcol_pass)
+          v[e] = ok[e] ? q1[e] + v[e] : 0.f;
         } else if constexpr (EPI == EPI_STRACE) {
           v[e] = (s0 * v[e]) * s0;
         } else if constexpr (EPI == EPI_SCALE || EPI == EPI_RQ) {
@@ -328,11 +330,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         if constexpr (EPI == EPI_PROC) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? X2[xo + e] : 0.f;
-        }
-        if constexpr (EPI == EPI_PROCB) {  // X2 in bf16, row-major with the same leading dimension
-          const bf16_t* x2 = reinterpret_cast<const bf16_t*>(X2) + xo;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) q2[e] = ok[e] ? bf16_to_f32(x2[e]) : 0.f;
         }
         epi_math(v, q1, q2, ok, row, col);
         if constexpr (EPI == EPI_STRACE) {  // sum C_ij X1_ij over the stored (upper) elements, diagonal included
@@ -369,7 +366,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       static_assert(IT % U == 0, "row pass: whole batches");
       constexpr bool L1 = EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE;
       float4 x1[2][U], x2[2][U];
-      uint2 xb[2][U];
       auto issue = [&](int set, int it0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -378,8 +374,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
           const long long xo = (long long)(grow0 + lr) * p.ldx + gcol0 + lc;
           if constexpr (L1) x1[set][u] = *reinterpret_cast<const float4*>(X1 + xo);
           if constexpr (EPI == EPI_PROC) x2[set][u] = *reinterpret_cast<const float4*>(X2 + xo);
-          if constexpr (EPI == EPI_PROCB)
-            xb[set][u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(X2) + xo);
         }
       };
       // one iteration: 4 columns of one row, X1 / X2 values from register set `set`, slot u
@@ -396,11 +390,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         }
         if constexpr (EPI == EPI_PROC) {
           q2[0] = x2[set][u].x; q2[1] = x2[set][u].y; q2[2] = x2[set][u].z; q2[3] = x2[set][u].w;
-        }
-        if constexpr (EPI == EPI_PROCB) {
-          const uint2 t = xb[set][u];
-          q2[0] = bf16_to_f32((bf16_t)(t.x & 0xffff)); q2[1] = bf16_to_f32((bf16_t)(t.x >> 16));
-          q2[2] = bf16_to_f32((bf16_t)(t.y & 0xffff)); q2[3] = bf16_to_f32((bf16_t)(t.y >> 16));
         }
         epi_math(v, q1, q2, ok, row, col);
         if constexpr (EPI == EPI_STRACE) t2 += v[0] * q1[0] + v[1] * q1[1] + v[2] * q1[2] + v[3] * q1[3];
@@ -423,6 +412,61 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       } else {  // nothing to load: a rolled loop (the fully unrolled form measured slower for store-only epilogues)
 #pragma unroll 4
         for (int it = 0; it < IT; ++it) step(it, 0, 0);
+      }
+    };
+    // EPI_PROCB: X2 = (R Q)^T in bf16 (the product's own B operand, row stride ldx), so R Q at (row, col) is read at
+    // (col, row): a column pass (4 consecutive rows of one column, 8 contiguous bytes) folds a RQ + a^2/2 s1 acc
+    // into the parked values before the row pass adds Qn. Interior tiles issue the loads 8 iterations ahead.
+    auto tcol_pass = [&](auto fast_c) {
+      constexpr bool FAST = decltype(fast_c)::value;
+      constexpr int IT = WC * (HR / 4) / 64, U = 8, NBT = IT / U;
+      static_assert(IT % U == 0, "transposed column pass: whole batches");
+      const float c2 = 0.5f * s0 * s0 * s1;
+      const bf16_t* __restrict__ X2b = reinterpret_cast<const bf16_t*>(X2);
+      auto fold = [&](int it, const float* q2) {
+        const int idx = lane + 64 * it;
+        const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float& x = ep[(lr + e) * EP + lc];
+          x = s0 * q2[e] + c2 * x;
+        }
+      };
+      if constexpr (FAST) {
+        uint2 xb[2][U];
+        auto issue = [&](int set, int it0) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int idx = lane + 64 * (it0 + u);
+            const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
+            xb[set][u] = *reinterpret_cast<const uint2*>(X2b + (long long)(gcol0 + lc) * p.ldx + grow0 + lr);
+          }
+        };
+        issue(0, 0);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          const int set = bt & 1;
+          if (bt + 1 < NBT) issue(set ^ 1, (bt + 1) * U);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const uint2 t = xb[set][u];
+            const float q2[4] = {bf16_to_f32((bf16_t)(t.x & 0xffff)), bf16_to_f32((bf16_t)(t.x >> 16)),
+                                 bf16_to_f32((bf16_t)(t.y & 0xffff)), bf16_to_f32((bf16_t)(t.y >> 16))};
+            fold(bt * U + u, q2);
+          }
+        }
+      } else {
+#pragma unroll 4
+        for (int it = 0; it < IT; ++it) {
+          const int idx = lane + 64 * it;
+          const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
+          const int col = gcol0 + lc, row = grow0 + lr;
+          float q2[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            q2[e] = row + e < p.M && col < p.N ? bf16_to_f32(X2b[(long long)col * p.ldx + row + e]) : 0.f;
+          fold(it, q2);
+        }
       }
     };
     auto col_pass = [&](auto fast_c) {
@@ -503,6 +547,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         }
       }
     };
+    if constexpr (EPI == EPI_PROCB) {
+      if (fast) tcol_pass(std::true_type{});
+      else tcol_pass(std::false_type{});
+      __syncthreads();
+    }
     if (fast) row_pass_fast();
     else row_pass();
     __syncthreads();
