@@ -21,6 +21,10 @@ namespace {
 
 constexpr int BK = 64, KP = 64;  // LDS rows of 128 bytes, 16-byte chunks XOR-swizzled by row (swz)
 
+// Row pitch (floats) of a wave's parked epilogue block of hr x wc: unpadded and swizzled for 64 x 64 blocks (see ei
+// in the kernel), padded by 4 otherwise.
+constexpr int epi_pitch(int hr, int wc) { return hr == 64 && wc == 64 ? wc : wc + 4; }
+
 __device__ __forceinline__ int remap_xcd(int w, int G) {
   const int cnt = G / 8, rem = G % 8, xcd = w % 8, slot = w / 8;
   return xcd < rem ? xcd * (cnt + 1) + slot : rem * (cnt + 1) + (xcd - rem) * cnt + slot;
@@ -250,8 +254,21 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   // consecutive rows of a column for the transposed bf16 copy, the SYRK mirror and the Procrustes trace.
   constexpr int HR = TM / 2;       // rows per wave per half
   constexpr int WC = TN;           // columns per wave
-  constexpr int EP = WC + 4;       // LDS row pitch (floats)
+  constexpr int EP = epi_pitch(HR, WC);  // LDS row pitch (floats)
   float* const ep = reinterpret_cast<float*>(smem) + wave * HR * EP;
+  // LDS slot of element (row, col) of the wave's parked block. For 64 x 64 blocks: rows of 64 floats, the float4
+  // group of the column XORed with the row's 4-row group k (its two 2-bit halves swapped), so that parking (16
+  // consecutive columns of rows 4 apart), the row pass (whole rows as float4) and the column passes (one column of
+  // 16 rows 4 apart) each touch 64 distinct banks; with a padded pitch of 68 the column passes met 4-way conflicts.
+  // Other shapes keep the padded pitch.
+  auto ei = [](int row, int col) {
+    if constexpr (EP == 64) {
+      const int k = (row >> 2) & 15, sw = ((k & 3) << 2) | (k >> 2);
+      return row * EP + (col ^ (sw << 2));
+    } else {
+      return row * EP + col;
+    }
+  };
   float* __restrict__ C = p.C[b];
   bf16_t* __restrict__ Cb = p.Cb[b];
   bf16_t* __restrict__ CTb = p.CTb[b];
@@ -280,7 +297,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ep[(ii * 16 + g * 4 + e) * EP + j * 16 + r] = acc[h * (FM / 2) + ii][j][e];
+        for (int e = 0; e < 4; ++e) ep[ei(ii * 16 + g * 4 + e, j * 16 + r)] = acc[h * (FM / 2) + ii][j][e];
     __syncthreads();
     const int grow0 = m0 + wm * TM + h * HR;  // global row of local row 0
     const int gcol0 = n0 + wn * TN;
@@ -316,7 +333,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         const int idx = lane + 64 * it;
         const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
         const int row = grow0 + lr, col = gcol0 + lc;
-        const float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
+        const float4 a = *reinterpret_cast<const float4*>(ep + ei(lr, lc));
         float v[4] = {a.x, a.y, a.z, a.w};
         bool ok[4];
 #pragma unroll
@@ -337,7 +354,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
           for (int e = 0; e < 4; ++e)
             if (ok[e]) t2 += v[e] * X1[xo + e];
         }
-        *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(ep + ei(lr, lc)) = make_float4(v[0], v[1], v[2], v[3]);
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
         if (C) {
           float* dst = C + (long long)row * p.ldc + col;
@@ -362,7 +379,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     // C / Cb, which the scheduler does not move loads across, so without this each wave would have only one
     // iteration's loads in flight and the epilogue would run at the latency of HBM.
     auto row_pass_fast = [&]() {
-      constexpr int IT = HR * (WC / 4) / 64, U = 8, NBT = IT / U;
+      // (two fp32 operands in flight take 4 iterations ahead, within the register budget)
+      constexpr int IT = HR * (WC / 4) / 64, U = EPI == EPI_PROC ? 4 : 8, NBT = IT / U;
       static_assert(IT % U == 0, "row pass: whole batches");
       constexpr bool L1 = EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE;
       float4 x1[2][U], x2[2][U];
@@ -381,7 +399,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         const int idx = lane + 64 * it;
         const int lr = idx / (WC / 4), lc = (idx % (WC / 4)) * 4;
         const int row = grow0 + lr, col = gcol0 + lc;
-        const float4 a = *reinterpret_cast<const float4*>(ep + lr * EP + lc);
+        const float4 a = *reinterpret_cast<const float4*>(ep + ei(lr, lc));
         float v[4] = {a.x, a.y, a.z, a.w};
         const bool ok[4] = {true, true, true, true};
         float q1[4] = {0.f, 0.f, 0.f, 0.f}, q2[4] = {0.f, 0.f, 0.f, 0.f};
@@ -393,7 +411,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         }
         epi_math(v, q1, q2, ok, row, col);
         if constexpr (EPI == EPI_STRACE) t2 += v[0] * q1[0] + v[1] * q1[1] + v[2] * q1[2] + v[3] * q1[3];
-        *reinterpret_cast<float4*>(ep + lr * EP + lc) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(ep + ei(lr, lc)) = make_float4(v[0], v[1], v[2], v[3]);
         if (C)
           *reinterpret_cast<float4*>(C + (long long)row * p.ldc + col) = make_float4(v[0], v[1], v[2], v[3]);
         if (Cb)
@@ -428,7 +446,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         const int lc = idx / (HR / 4), lr = (idx % (HR / 4)) * 4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float& x = ep[(lr + e) * EP + lc];
+          float& x = ep[ei(lr + e, lc)];
           x = s0 * q2[e] + c2 * x;
         }
       };
@@ -482,7 +500,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
         bool ok[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = ep[(lr + e) * EP + lc];
+          v[e] = ep[ei(lr + e, lc)];
           ok[e] = FAST || (row + e < p.M && col < p.N && !(p.tri && row + e > col));
         }
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
@@ -583,7 +601,8 @@ int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
 template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   constexpr int NW = WGM * WGN;
-  constexpr int smem_main = 2 * (BM + BN) * KP * 2, smem_epi = NW * (BM / WGM / 2) * (BN / WGN + 4) * 4;
+  constexpr int smem_main = 2 * (BM + BN) * KP * 2,
+                smem_epi = NW * (BM / WGM / 2) * epi_pitch(BM / WGM / 2, BN / WGN) * 4;
   constexpr int smem = smem_main > smem_epi ? smem_main : smem_epi;
   auto fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
   static bool attr = false;
