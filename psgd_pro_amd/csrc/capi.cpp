@@ -1776,7 +1776,7 @@ int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri,
                          psgdk_stream_t stream) {
   PSGDK_TRY(check_group(g, false));
   if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
-  constexpr int PB = 64;  // partial maxima per factor
+  constexpr int PB = 1024;  // partial maxima per factor (workgroups of its max |q| pass)
   Ws w(ws);
   float *part[MAXB], *sc[MAXB];
   for (int b = 0; b < g->nb; ++b) { part[b] = w.take<float>(2 * PB); sc[b] = w.take<float>(4); }

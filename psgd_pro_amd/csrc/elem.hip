@@ -576,8 +576,19 @@ __global__ void __launch_bounds__(EW_THREADS) absmax_kernel(const EwArgs a, int 
   long long beg, end;
   ew_range(a.m * a.n, blocks_per, beg, end);
   const float* x = reinterpret_cast<const float*>(a.in[b]);
+  const long long total = a.m * a.n;
   float m = 0.f;
-  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) m = fmaxf(m, fabsf(x[i]));
+  if ((total & 3) == 0 && al16(x)) {  // 16-byte loads: each workgroup owns a contiguous range of float4s
+    ew_range(total >> 2, blocks_per, beg, end);
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+#pragma unroll 4
+    for (long long v = beg + threadIdx.x; v < end; v += EW_THREADS) {
+      const float4 q = x4[v];
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+    }
+  } else {
+    for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) m = fmaxf(m, fabsf(x[i]));
+  }
   m = block_max(m, red);
   if (threadIdx.x == 0) a.out[b][blockIdx.x % blocks_per] = m;
 }
