@@ -48,6 +48,8 @@ def parse_args():
     ap.add_argument("--fuse", type=int, default=1,
                     help="0: one update call per weight group instead of one call batching all groups' factor work")
     ap.add_argument("--rq16", type=int, default=1, help="0: keep R Q in fp32 between the Procrustes products (option 7)")
+    ap.add_argument("--f32kc", type=int, default=1,
+                    help="0: fp32 products on the general engine instead of the k-contiguous kernel's fp32 twin (option 8)")
     ap.add_argument("--vmm", type=int, default=-1,
                     help="V A kernel of the norm bounds (option 4): -1 by shape, 0 split-K, 1 column blocks, 2 LDS rows")
     ap.add_argument("--tile-cfg", type=int, default=-1,
@@ -147,6 +149,7 @@ def bench_vitb(args):
     L.check(L.lib().psgdk_set_option(1, args.tile_cfg))
     L.check(L.lib().psgdk_set_option(7, args.rq16))
     L.check(L.lib().psgdk_set_option(4, args.vmm))
+    L.check(L.lib().psgdk_set_option(8, args.f32kc))
     skew = math.inf if args.skew == "inf" else float(args.skew)
     shapes = VIT_B * args.blocks
     gen = torch.Generator().manual_seed(0)

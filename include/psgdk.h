@@ -261,7 +261,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * 4 m d^2 flops; 0: term1 Q, 2 d^3 flops); option 6 = side streams of psgdk_kron2d_update_groups (default 3; 0 or
  * 1: everything on the caller's stream); option 7 = whether the bf16 update keeps R Q (the Procrustes correction)
  * in bf16 (1, default: only the bf16 (R Q)^T, which the Q update also reads) or fp32 (0) between its two
- * products. */
+ * products; option 8 = whether fp32 products with k- or m/n-contiguous operands (M > 32, one k range, no packed
+ * output) take the k-contiguous kernel's fp32 twin (1, default) or the general engine (0). */
 int psgdk_set_option(int option, int value);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,

@@ -151,9 +151,10 @@ int gemm_tiles(int64_t M, int64_t N, int tri) {
   return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
 }
 
-int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, const Opnd& B, float* const* C,
-             int64_t ldc, const EpiSpec& e, int tri, int out_mode, int kbeg_tri, int splitk, int64_t kchunk,
-             hipStream_t st) {
+// The general engine (gemm.hip): every operand mode, precision, split-K and triangular option.
+int run_gemm_general(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, const Opnd& B,
+                     float* const* C, int64_t ldc, const EpiSpec& e, int tri, int out_mode, int kbeg_tri, int splitk,
+                     int64_t kchunk, hipStream_t st) {
   GemmArgs a;
   gemm_init(a);
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
@@ -188,6 +189,10 @@ int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, c
   g_prof.recs.push_back(r);
   return PSGDK_OK;
 }
+// run_gemm_general, or the k-contiguous kernel's fp32 twin where it applies (defined after run_b16)
+int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, const Opnd& B, float* const* C,
+             int64_t ldc, const EpiSpec& e, int tri, int out_mode, int kbeg_tri, int splitk, int64_t kchunk,
+             hipStream_t st);
 
 // ------------------------------------------------------------------------------------------------------------
 // bf16 k-contiguous GEMM (gemm_bf16.hip). A: M x K rows, B: N x K rows (bf16, k contiguous); C = acc A B^T.
@@ -208,6 +213,7 @@ int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape (2 for 
 int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
 int g_upd_streams = 3;    // psgdk_set_option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
 int g_rq16 = 1;           // psgdk_set_option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
+int g_f32kc = 1;          // psgdk_set_option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -241,38 +247,51 @@ int b16_cfg(int64_t M, int64_t N, int tri, int nb) {
   return gemm_bf16_tiles(M, N, tri, 0) * nb >= 160 ? 0 : 1;
 }
 
-// Operand contract of gemm_bf16: K and both leading dimensions multiples of 8, 16-byte aligned bases, each operand
-// under 2 GiB (buffer extent).
+// Operand contract of the k-contiguous kernel (gemm_bf16, esz 2; its fp32 twin, esz 4): 16-byte aligned bases,
+// leading dimensions multiples of one 16-byte chunk, each operand under 2 GiB (buffer extent); a k-contiguous
+// operand (rows of the buffer: m or n) needs K a multiple of a chunk, an m/n-contiguous one (fp32 only, amc / bmc:
+// rows of the buffer: k) M or N a multiple of 4.
 template <typename P>
-bool b16_operands_ok(int nb, int64_t M, int64_t N, int64_t K, P const* A, int64_t lda, P const* B, int64_t ldb) {
-  if (K % 8 || lda % 8 || ldb % 8 || lda < K || ldb < K) return false;
-  if (M * lda * 2 >= ((int64_t)1 << 31) || N * ldb * 2 >= ((int64_t)1 << 31)) return false;
+bool b16_operands_ok(int nb, int64_t M, int64_t N, int64_t K, P const* A, int64_t lda, P const* B, int64_t ldb,
+                     int esz = 2, bool amc = false, bool bmc = false) {
+  const int64_t ce = 16 / esz, big = (int64_t)1 << 31;
+  auto one = [&](int64_t mn, int64_t ld, bool mc) {
+    if (ld % ce) return false;
+    if (mc) return mn % ce == 0 && ld >= mn && K * ld * esz < big;
+    return K % ce == 0 && ld >= K && mn * ld * esz < big;
+  };
+  if (!one(M, lda, amc) || !one(N, ldb, bmc)) return false;
   for (int b = 0; b < nb; ++b)
     if (!aligned16(A[b]) || !aligned16(B[b])) return false;
   return true;
 }
 
+// The k-contiguous kernel on bf16 (esz 2) or fp32 (esz 4) operands.
 int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64_t lda, const void* const* B,
-            int64_t ldb, const B16Out& o, const EpiSpec& e, int tri, int out_mode, int* ntiles, hipStream_t st) {
-  if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb))
-    return fail(PSGDK_EINVAL, "bf16 kernel operand contract violated (K, leading dimensions, alignment or size)");
+            int64_t ldb, const B16Out& o, const EpiSpec& e, int tri, int out_mode, int* ntiles, hipStream_t st,
+            int esz = 2, bool amc = false, bool bmc = false) {
+  if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb, esz, amc, tri ? amc : bmc))
+    return fail(PSGDK_EINVAL, "k-contiguous kernel operand contract violated (K, leading dimensions, alignment or size)");
   GB16Args a;
   std::memset(&a, 0, sizeof a);
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
   a.lda = lda; a.ldb = ldb; a.ldc = o.ldc; a.ldcb = o.ldcb; a.ldct = o.ldct; a.ldx = e.ldx;
   a.alpha = e.alpha; a.epi = e.epi; a.tri = tri; a.out_mode = out_mode; a.nb = nb;
   a.vec = g_tile_order;
+  a.amc = amc; a.bmc = tri ? amc : bmc;
   for (int b = 0; b < nb; ++b) {
     a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
     a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
     a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b];
     a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
   }
-  const int cfg = b16_cfg(M, N, tri, nb);
+  int cfg = b16_cfg(M, N, tri, nb);
+  if (esz == 4) cfg = 1;  // the fp32 kernel: the 128-tile configuration
   if (ntiles) *ntiles = gemm_bf16_tiles(M, N, tri, cfg);
-  if (!g_prof.on) return hip_check(gemm_bf16_launch(a, cfg, st), "bf16 gemm launch");
+  auto launch = [&]() { return esz == 4 ? gemm_f32kc_launch(a, cfg, st) : gemm_bf16_launch(a, cfg, st); };
+  if (!g_prof.on) return hip_check(launch(), "k-contiguous gemm launch");
   ProfRec r;
-  r.kernel_id = 5000 + cfg * 10 + a.epi;
+  r.kernel_id = (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
   r.flops = tri ? (double)M * (M + 1) * K * nb : 2.0 * M * N * K * nb;
@@ -280,10 +299,32 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
   PSGDK_HIP(hipEventRecord(r.a, st), "profiling event");
-  PSGDK_TRY(hip_check(gemm_bf16_launch(a, cfg, st), "bf16 gemm launch"));
+  PSGDK_TRY(hip_check(launch(), "k-contiguous gemm launch"));
   PSGDK_HIP(hipEventRecord(r.b, st), "profiling event");
   g_prof.recs.push_back(r);
   return PSGDK_OK;
+}
+
+int run_gemm(int prec, int nb, int64_t M, int64_t N, int64_t K, const Opnd& A, const Opnd& B, float* const* C,
+             int64_t ldc, const EpiSpec& e, int tri, int out_mode, int kbeg_tri, int splitk, int64_t kchunk,
+             hipStream_t st) {
+  // fp32 products on the k-contiguous kernel's fp32 twin: fp32 operands stored k- or m/n-contiguous (not a triangle),
+  // M > 32 (the general engine's 128 x 128 tiles, so that per-tile partials count the same), one k range, no packed
+  // output, a plain store only without beta, and a SYRK's single operand.
+  const bool kc_epi = e.epi == EPI_FACTOR || e.epi == EPI_PROC || e.epi == EPI_SCALE || e.epi == EPI_RQ ||
+                      e.epi == EPI_SUMSQ || e.epi == EPI_STRACE || (e.epi == EPI_STORE && e.beta == 0.f);
+  if (g_f32kc && prec == PSGDK_PREC_F32 && A.dt == PSGDK_F32 && B.dt == PSGDK_F32 && M > 32 && splitk == 1 &&
+      !kbeg_tri && out_mode != PSGDK_OUT_PACKED && kc_epi && A.mode != SYM && B.mode != SYM &&
+      (!tri || A.mode == B.mode) &&
+      b16_operands_ok(nb, M, tri ? M : N, K, A.p, A.ld, tri ? A.p : B.p, tri ? A.ld : B.ld, 4, A.mode == MC,
+                      (tri ? A.mode : B.mode) == MC)) {
+    B16Out o;
+    o.ldc = ldc;
+    for (int b = 0; b < nb; ++b) o.C[b] = C[b];
+    return run_b16(nb, M, N, K, A.p, A.ld, tri ? A.p : B.p, tri ? A.ld : B.ld, o, e, tri, out_mode, nullptr, st, 4,
+                   A.mode == MC, (tri ? A.mode : B.mode) == MC);
+  }
+  return run_gemm_general(prec, nb, M, N, K, A, B, C, ldc, e, tri, out_mode, kbeg_tri, splitk, kchunk, st);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -1855,6 +1896,11 @@ int psgdk_set_option(int option, int value) {
   if (option == 3) {
     if (value != 2 && value != 4 && value != 8) return fail(PSGDK_EINVAL, "option 3 (V A load batch) must be 2, 4 or 8");
     g_vmm_u = value;
+    return PSGDK_OK;
+  }
+  if (option == 8) {
+    if (value < 0 || value > 1) return fail(PSGDK_EINVAL, "option 8 (fp32 k-contiguous kernel) must be 0 or 1");
+    g_f32kc = value;
     return PSGDK_OK;
   }
   if (option == 4) {

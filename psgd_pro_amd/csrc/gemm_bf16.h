@@ -17,6 +17,7 @@ struct GB16Args {
   int tiles_m, tiles_n, ntiles, nb;
   int vec;            // 0: problem-major order (WG id = tile); 1: tiles dealt to XCDs in contiguous runs; 2: as 1,
                       // with tile rows grouped by 4 inside each problem
+  int amc, bmc;       // fp32 kernel: A / B stored m- / n-contiguous (rows of the buffer are k; M / N a multiple of 4)
   const bf16_t* A[MAXB];
   const bf16_t* B[MAXB];
   float* C[MAXB];
@@ -30,6 +31,10 @@ struct GB16Args {
 
 // cfg 0: 256 x 256 tiles (8 waves), cfg 1: 128 x 128 tiles (4 waves), cfg 2: 256 x 256 tiles (4 waves)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
+// The same kernel for k-contiguous fp32 operands (A, B reinterpreted as float; K, leading dimensions multiples of 4;
+// always the 128-tile configuration, with k summed in blocks of 128; operands k-contiguous or, with amc / bmc,
+// m- / n-contiguous; EPI_RQ reads R as fp32; every epilogue but EPI_PROCB, which reads a bf16 X operand)
+hipError_t gemm_f32kc_launch(GB16Args& a, int cfg, hipStream_t st);
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg);
 
 }  // namespace psgdk

@@ -19,7 +19,13 @@ namespace psgdk {
 
 namespace {
 
-constexpr int BK = 64, KP = 64;  // LDS rows of 128 bytes, 16-byte chunks XOR-swizzled by row (swz)
+// Element traits of the k-contiguous operands. A k tile is 8 chunks of 16 bytes (one 128-byte LDS row per m or n,
+// chunks XOR-swizzled by row, swz): 64 bf16 or 32 fp32. CE: elements per chunk; MPF: MFMAs per pair of 16-byte
+// fragments (one v_mfma_f32_16x16x32_bf16, or four v_mfma_f32_16x16x4f32 over the fragment's 4 k values, lane group
+// g holding k = 4 g + s for both operands).
+template <typename T> struct Kc;
+template <> struct Kc<bf16_t> { static constexpr int CE = 8, MPF = 1; using F = bf16x8_t; };
+template <> struct Kc<float> { static constexpr int CE = 4, MPF = 4; using F = f32x4_t; };
 
 // Row pitch (floats) of a wave's parked epilogue block of hr x wc: unpadded and swizzled for 64 x 64 blocks (see ei
 // in the kernel), padded by 4 otherwise.
@@ -37,51 +43,87 @@ __device__ __forceinline__ int remap_xcd(int w, int G) {
 // bytes); the 8 lanes that write one row still cover its 8 slots.
 __device__ __forceinline__ int swz(int row, int c) { return c ^ (row & 7); }
 
-// Global -> register -> LDS staging of one ROWS x 64 bf16 tile with buffer loads. Lane `tid` owns the 16-byte
+// Global -> register -> LDS staging of one ROWS x (8 chunks) tile with buffer loads. Lane `tid` owns the 16-byte
 // k chunk tid % 8 of rows tid / 8 + 32 i (i < NV): the lane part of the byte offset is the VGPR offset, the row
 // group and the tile's k origin are the scalar offset. A lane whose row is past the operand or whose k chunk is
-// past K (K is a multiple of 8) gets an offset beyond the buffer extent: it reads zero (or, where the scalar part
-// wraps the 32-bit sum, some element of the same buffer), and either way only feeds outputs that are not stored.
-template <int ROWS, int NT>
+// past K (K is a multiple of a chunk) gets an offset beyond the buffer extent: it reads zero (or, where the scalar
+// part wraps the 32-bit sum, some element of the same buffer), and either way only feeds outputs that are not
+// stored.
+template <typename T, int ROWS, int NT>
 struct Ld {
-  static constexpr int NV = ROWS * (BK / 8) / NT;  // 16-byte vectors per thread
+  static constexpr int CE = Kc<T>::CE, KP = 8 * CE;
+  static constexpr int NV = ROWS * 8 / NT;  // 16-byte vectors per thread
   uint4 r[NV];
 
   // t: the thread's index among the NT threads that load this tile
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int voff, long long ld, int mn0, int rows, int k0,
                                        int K, int t) {
     const int lrow = t >> 3;
-    const bool kok = k0 + (t & 7) * 8 < K;
+    const bool kok = k0 + (t & 7) * CE < K;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int base = mn0 + i * (NT / 8);
       const bool ok = kok && base + lrow < rows;
-      const int soff = (int)(((long long)base * ld + k0) * 2);
+      const int soff = (int)(((long long)base * ld + k0) * (long long)sizeof(T));
       r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff : 0x7fffffff, soff, 0));
     }
   }
 
-  __device__ __forceinline__ void store(bf16_t* lds, int t) const {
+  __device__ __forceinline__ void store(T* lds, int t) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int v = t + NT * i, row = v >> 3, kv = v & 7;
-      *reinterpret_cast<uint4*>(lds + row * KP + swz(row, kv) * 8) = r[i];
+      *reinterpret_cast<uint4*>(lds + row * KP + swz(row, kv) * CE) = r[i];
+    }
+  }
+
+  // An fp32 operand stored m- or n-contiguous, X[k][mn] with row stride ld (the rows of the buffer are k): thread t
+  // owns the 4 x 4 block of k chunk t % 8 and tile rows 4 (t / 8) .. + 3. Four 16-byte loads (k rows; the 8 lanes
+  // of one k chunk read 128 contiguous bytes of a k row) are transposed in registers into the block's four
+  // k-contiguous chunks, stored in the same swizzled layout (at most 2-way bank conflicts). One block per thread
+  // (ROWS = NT / 2); rows past the operand and k past K read zero.
+  __device__ __forceinline__ void load_mc(__amdgpu_buffer_rsrc_t rs, long long ld, int mn0, int rows, int k0, int K,
+                                          int t) {
+    static_assert(std::is_same_v<T, float> && NV == 4 && ROWS * 2 == NT, "m/n-contiguous loader: fp32, one block");
+    const int kc = t & 7, nb = t >> 3;
+    const bool nok = mn0 + nb * 4 < rows;
+    const int soff = (int)(((long long)k0 * ld + mn0) * 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = kc * 4 + i;
+      const int voff = (int)(((long long)k * ld + nb * 4) * 4);
+      r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, nok && k0 + k < K ? voff : 0x7fffffff,
+                                                                                soff, 0));
+    }
+  }
+  __device__ __forceinline__ void store_mc(T* lds, int t) const {
+    const int kc = t & 7, nb = t >> 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = nb * 4 + j;
+      const uint4 x = make_uint4((&r[0].x)[j], (&r[1].x)[j], (&r[2].x)[j], (&r[3].x)[j]);
+      *reinterpret_cast<uint4*>(lds + row * KP + swz(row, kc) * CE) = x;
     }
   }
 };
 
 }  // namespace
 
-// WGM x WGN waves, each owning a TM x TN block (TM = BM / WGM, TN = BN / WGN) of 16 x 16 MFMA tiles.
-template <int BM, int BN, int WGM, int WGN, int EPI>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Args p) {
+// WGM x WGN waves, each owning a TM x TN block (TM = BM / WGM, TN = BN / WGN) of 16 x 16 MFMA tiles; T = bf16_t
+// (the bf16 kernel) or float (its fp32 twin for k-contiguous fp32 operands: the same tiles, LDS layout, schedule
+// and epilogues, four fp32 MFMAs per fragment pair).
+// LAY (fp32 only): bit 0 set = A stored m-contiguous, bit 1 = B stored n-contiguous (the buffer's rows are k).
+template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0>
+__device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
+  constexpr int CE = Kc<T>::CE, BK = 8 * CE, KP = BK, MPF = Kc<T>::MPF;
+  using F = typename Kc<T>::F;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr bool PP = WGM == 2 && WGN == 4;  // ping-pong main loop (8 waves, two groups of 4)
   constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 tiles per wave along m, n
   extern __shared__ __align__(16) unsigned char smem[];
-  bf16_t* const As0 = reinterpret_cast<bf16_t*>(smem);
-  bf16_t* const Bs0 = As0 + 2 * BM * KP;
+  T* const As0 = reinterpret_cast<T*>(smem);
+  T* const Bs0 = As0 + 2 * BM * KP;
 
   const int G = p.ntiles * p.nb;
   const int logical = p.vec ? remap_xcd(blockIdx.x, G) : (int)blockIdx.x;
@@ -105,40 +147,62 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     tj = tile % p.tiles_n;
   }
   const int m0 = ti * BM, n0 = tj * BN;
-  const bf16_t* __restrict__ Ap = p.A[b];
-  const bf16_t* __restrict__ Bp = p.tri ? p.A[b] : p.B[b];
+  const T* __restrict__ Ap = reinterpret_cast<const T*>(p.A[b]);
+  const T* __restrict__ Bp = reinterpret_cast<const T*>(p.tri ? p.A[b] : p.B[b]);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   const int r = lane & 15, g = lane >> 4;
 
   f32x4_t acc[FM][FN];
+  // fp32 operands sum k in blocks of 128 (four k tiles) into `part`, folded into `acc` after each block, as the
+  // general fp32 engine does: one fp32 chain over all of K carries several times the rounding error against an
+  // fp64 product (measured 7.6x at K = 3072). The 128-tile configuration has the registers for the second set.
+  constexpr bool BLK = std::is_same_v<T, float>;
+  static_assert(!BLK || !PP, "blocked fp32 summation needs the 128-tile configuration");
+  constexpr int KC_TILES = 128 / BK;
+  f32x4_t part[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto& dst = BLK ? part : acc;  // the MFMA accumulators of the main loop
 
   const int nk = (p.K + BK - 1) / BK;
-  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(Ap, (long long)p.M * p.lda * 2);
-  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bp, (long long)(p.tri ? p.M : p.N) * p.ldb * 2);
+  // fp32 operands may be stored m- / n-contiguous (amc, bmc: the buffer's rows are k)
+  constexpr bool amc = (LAY & 1) != 0, bmc = (LAY & 2) != 0;  // a SYRK (B = A) has both bits or neither
+  static_assert(LAY == 0 || std::is_same_v<T, float>, "m/n-contiguous operands: fp32 only");
+  const __amdgpu_buffer_rsrc_t rsA =
+      make_rsrc(Ap, (long long)(amc ? p.K : p.M) * p.lda * (long long)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rsB =
+      make_rsrc(Bp, (long long)(bmc ? p.K : (p.tri ? p.M : p.N)) * p.ldb * (long long)sizeof(T));
+  // acc += a b over one pair of 16-byte fragments (32 k of bf16, or 16 k of fp32 in four steps)
+  auto mma = [](f32x4_t& c, const F& a, const F& bb) {
+    if constexpr (MPF == 1) {
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb, c, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < MPF; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bb[s], c, 0, 0, 0);
+    }
+  };
   const int rowsB = p.tri ? p.M : p.N;
-  // 2 x 32-deep MFMA steps of one k tile from LDS (B fragments held, A fragments streamed one row ahead)
-  auto mma_tile = [&](const bf16_t* As, const bf16_t* Bs) {
+  // 2 steps of 4 chunks per k tile from LDS (B fragments held, A fragments streamed one row ahead)
+  auto mma_tile = [&](const T* As, const T* Bs) {
 #pragma unroll 1
-    for (int ks = 0; ks < BK / 32; ++ks) {
+    for (int ks = 0; ks < 2; ++ks) {
       // fragment rows are 16-aligned plus r, so their swizzle is that of r
-      const int ko = swz(r, ks * 4 + g) * 8;
-      bf16x8_t bfr[FN];
+      const int ko = swz(r, ks * 4 + g) * CE;
+      F bfr[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
-      bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + r) * KP + ko);
+        bfr[j] = *reinterpret_cast<const F*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
+      F a_cur = *reinterpret_cast<const F*>(As + (wm * TM + r) * KP + ko);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        bf16x8_t a_nxt = a_cur;
+        F a_nxt = a_cur;
         if (i + 1 < FM)
-          a_nxt = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + (i + 1) * 16 + r) * KP + ko);
+          a_nxt = *reinterpret_cast<const F*>(As + (wm * TM + (i + 1) * 16 + r) * KP + ko);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FN; ++j) mma(dst[i][j], a_cur, bfr[j]);
         a_cur = a_nxt;
       }
     }
@@ -147,18 +211,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   // pipe fed. All 2 x FM A rows of the tile are streamed 3 rows ahead of their MFMAs; the second step's B
   // fragments are read during the first step. sched_group_barrier pins the order: reads go out ahead of the
   // MFMAs that hide their latency.
-  auto mma_tile_pp = [&](const bf16_t* As, const bf16_t* Bs) {
+  auto mma_tile_pp = [&](const T* As, const T* Bs) {
     constexpr int NQ = 2 * FM, LA = 3;
-    bf16x8_t bq[2][FN], aq[NQ];
+    F bq[2][FN], aq[NQ];
     auto rd_b = [&](int ks) {
-      const int ko = swz(r, ks * 4 + g) * 8;
+      const int ko = swz(r, ks * 4 + g) * CE;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bq[ks][j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
+        bq[ks][j] = *reinterpret_cast<const F*>(Bs + (wn * TN + j * 16 + r) * KP + ko);
     };
     auto rd_a = [&](int q) {
       const int ks = q / FM, i = q % FM;
-      aq[q] = *reinterpret_cast<const bf16x8_t*>(As + (wm * TM + i * 16 + r) * KP + swz(r, ks * 4 + g) * 8);
+      aq[q] = *reinterpret_cast<const F*>(As + (wm * TM + i * 16 + r) * KP + swz(r, ks * 4 + g) * CE);
     };
     rd_b(0);
 #pragma unroll
@@ -170,7 +234,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       const int ks = q / FM, i = q % FM;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q], bq[ks][j], acc[i][j], 0, 0, 0);
+        mma(acc[i][j], aq[q], bq[ks][j]);
     }
     __builtin_amdgcn_sched_group_barrier(0x100, FN + LA, 0);
 #pragma unroll
@@ -178,31 +242,46 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
       if (q + LA < NQ && q == FM / 2) __builtin_amdgcn_sched_group_barrier(0x100, FN + 1, 0);
       else if (q + LA < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       else if (q == FM / 2) __builtin_amdgcn_sched_group_barrier(0x100, FN, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FN * MPF, 0);
     }
   };
   if constexpr (!PP) {
-    const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * 8) * 2);
-    const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * 8) * 2);
-    Ld<BM, NT> la;
-    Ld<BN, NT> lb;
-    la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K, tid);
-    lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K, tid);
-    la.store(As0, tid);
-    lb.store(Bs0, tid);
+    const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * CE) * (long long)sizeof(T));
+    const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * CE) * (long long)sizeof(T));
+    Ld<T, BM, NT> la;
+    Ld<T, BN, NT> lb;
+    auto load = [&](int k0) {
+      if constexpr (amc) la.load_mc(rsA, p.lda, m0, p.M, k0, p.K, tid);
+      else la.load(rsA, voffA, p.lda, m0, p.M, k0, p.K, tid);
+      if constexpr (bmc) lb.load_mc(rsB, p.ldb, n0, rowsB, k0, p.K, tid);
+      else lb.load(rsB, voffB, p.ldb, n0, rowsB, k0, p.K, tid);
+    };
+    auto store = [&](T* as, T* bs) {
+      if constexpr (amc) la.store_mc(as, tid);
+      else la.store(as, tid);
+      if constexpr (bmc) lb.store_mc(bs, tid);
+      else lb.store(bs, tid);
+    };
+    load(0);
+    store(As0, Bs0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
       const bool more = kt + 1 < nk;
-      if (more) {
-        la.load(rsA, voffA, p.lda, m0, p.M, (kt + 1) * BK, p.K, tid);
-        lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 1) * BK, p.K, tid);
-      }
+      if (more) load((kt + 1) * BK);
       mma_tile(As0 + cur * BM * KP, Bs0 + cur * BN * KP);
-      if (more) {
-        la.store(As0 + (cur ^ 1) * BM * KP, tid);
-        lb.store(Bs0 + (cur ^ 1) * BN * KP, tid);
+      if constexpr (BLK) {
+        if ((kt + 1) % KC_TILES == 0 || !more) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+              acc[i][j] += part[i][j];
+              part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
       }
+      if (more) store(As0 + (cur ^ 1) * BM * KP, Bs0 + (cur ^ 1) * BN * KP);
       __syncthreads();
     }
   } else {
@@ -218,10 +297,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
     // h is uniform per wave but not provably so, and a scalar offset derived from it would be waterfalled.
     const int h = wave >> 2, t = (tid & 255) + h * (NT / 2) * 4;  // rows h * 128 + (tid & 255) / 8 (+ 32 i)
     static_assert(BM == BN && (NT / 2) * 4 == (BM / 2) * 8, "ping-pong loader: one group loads half the rows");
-    const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * 8) * 2);
-    const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * 8) * 2);
-    Ld<BM / 2, NT / 2> la;
-    Ld<BN / 2, NT / 2> lb;
+    const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * CE) * (long long)sizeof(T));
+    const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * CE) * (long long)sizeof(T));
+    Ld<T, BM / 2, NT / 2> la;
+    Ld<T, BN / 2, NT / 2> lb;
     la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K, t);
     lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K, t);
     la.store(As0, t);
@@ -285,7 +364,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   const bool fast = m0 + BM <= p.M && n0 + BN <= p.N && (!p.tri || ti < tj) &&
                     (!C || ((p.ldc & 3) == 0 && al(C, 16))) && (!Cb || ((p.ldcb & 3) == 0 && al(Cb, 8))) &&
                     (!CTb || ((p.ldct & 3) == 0 && al(CTb, 8))) && (p.ldx & 3) == 0 &&
-                    (!X1 || al(X1, EPI == EPI_RQ ? 8 : 16)) && (!X2 || al(X2, 16));
+                    (!X1 || al(X1, EPI == EPI_RQ && !std::is_same_v<T, float> ? 8 : 16)) && (!X2 || al(X2, 16));
   float t1 = 0.f, t2 = 0.f;
   // one half of each wave's rows; h is a template constant so that the accumulator indices stay static (a loop
   // over h is too large to be unrolled, and a dynamic index would move the accumulators to scratch)
@@ -504,7 +583,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
           ok[e] = FAST || (row + e < p.M && col < p.N && !(p.tri && row + e > col));
         }
         const bool all = ok[0] && ok[1] && ok[2] && ok[3];
-        if constexpr (EPI == EPI_RQ) {  // X1: R in bf16, read at (col, row..row+3)
+        if constexpr (EPI == EPI_RQ && std::is_same_v<T, float>) {  // X1: R in fp32, read at (col, row..row+3)
+          const float* x = X1 + (long long)col * p.ldx + row;
+          if constexpr (FAST) {
+            const float4 t = *reinterpret_cast<const float4*>(x);
+            t2 += s0 * (t.x * v[0] + t.y * v[1] + t.z * v[2] + t.w * v[3]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (ok[e]) t2 += s0 * x[e] * v[e];
+          }
+        } else if constexpr (EPI == EPI_RQ) {  // X1: R in bf16, read at (col, row..row+3)
           const bf16_t* x = reinterpret_cast<const bf16_t*>(X1) + (long long)col * p.ldx + row;
           if constexpr (FAST) {
             const uint2 t = *reinterpret_cast<const uint2*>(x);
@@ -592,19 +681,32 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Arg
   }
 }
 
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Args p) {
+  gemm_kc_body<bf16_t, BM, BN, WGM, WGN, EPI>(p);
+}
+
+// two workgroups per CU (two waves per SIMD): the register budget of every layout
+template <int BM, int BN, int WGM, int WGN, int EPI, int LAY>
+__global__ void __launch_bounds__(64 * WGM * WGN, 2) gemm_f32kc_kernel(const GB16Args p) {
+  gemm_kc_body<float, BM, BN, WGM, WGN, EPI, LAY>(p);
+}
+
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
   const int T = cfg == 1 ? 128 : 256;
   const long long tm = (M + T - 1) / T, tn = (N + T - 1) / T;
   return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
 }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
+template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0>
 static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   constexpr int NW = WGM * WGN;
-  constexpr int smem_main = 2 * (BM + BN) * KP * 2,
+  constexpr int smem_main = 2 * (BM + BN) * 128,
                 smem_epi = NW * (BM / WGM / 2) * epi_pitch(BM / WGM / 2, BN / WGN) * 4;
   constexpr int smem = smem_main > smem_epi ? smem_main : smem_epi;
-  auto fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
+  void (*fn)(GB16Args) = nullptr;
+  if constexpr (std::is_same_v<T, bf16_t>) fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
+  else fn = gemm_f32kc_kernel<BM, BN, WGM, WGN, EPI, LAY>;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
@@ -618,26 +720,43 @@ static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WGM, int WGN>
+template <typename T, int BM, int BN, int WGM, int WGN, int LAY = 0>
 static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
+  constexpr bool B16 = std::is_same_v<T, bf16_t>;
   switch (a.epi) {
-    case EPI_FACTOR: return launch_b16<BM, BN, WGM, WGN, EPI_FACTOR>(a, st);
-    case EPI_PROC: return launch_b16<BM, BN, WGM, WGN, EPI_PROC>(a, st);
-    case EPI_PROCB: return launch_b16<BM, BN, WGM, WGN, EPI_PROCB>(a, st);
-    case EPI_SCALE: return launch_b16<BM, BN, WGM, WGN, EPI_SCALE>(a, st);
-    case EPI_RQ: return launch_b16<BM, BN, WGM, WGN, EPI_RQ>(a, st);
-    case EPI_SUMSQ: return launch_b16<BM, BN, WGM, WGN, EPI_SUMSQ>(a, st);
-    case EPI_STRACE: return launch_b16<BM, BN, WGM, WGN, EPI_STRACE>(a, st);
-    default: return launch_b16<BM, BN, WGM, WGN, EPI_STORE>(a, st);
+    case EPI_FACTOR: return launch_b16<T, BM, BN, WGM, WGN, EPI_FACTOR, LAY>(a, st);
+    case EPI_PROC: return launch_b16<T, BM, BN, WGM, WGN, EPI_PROC, LAY>(a, st);
+    case EPI_SCALE: return launch_b16<T, BM, BN, WGM, WGN, EPI_SCALE, LAY>(a, st);
+    case EPI_SUMSQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_SUMSQ, LAY>(a, st);
+    case EPI_STRACE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STRACE, LAY>(a, st);
+    case EPI_STORE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STORE, LAY>(a, st);
+    case EPI_RQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_RQ, LAY>(a, st);  // R read as T
+    default: break;
   }
+  if constexpr (B16) {  // reads a bf16 X operand
+    if (a.epi == EPI_PROCB) return launch_b16<T, BM, BN, WGM, WGN, EPI_PROCB, LAY>(a, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 // cfg 0: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64; cfg 1: 128 x 128 tiles, 4 waves of 64 x 64;
 // cfg 2: 256 x 256 tiles, 4 waves of 128 x 128 (one wave per SIMD)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st) {
-  if (cfg == 1) return launch_epi<128, 128, 2, 2>(a, st);
-  if (cfg == 2) return launch_epi<256, 256, 2, 2>(a, st);
-  return launch_epi<256, 256, 2, 4>(a, st);
+  if (cfg == 1) return launch_epi<bf16_t, 128, 128, 2, 2>(a, st);
+  if (cfg == 2) return launch_epi<bf16_t, 256, 256, 2, 2>(a, st);
+  return launch_epi<bf16_t, 256, 256, 2, 4>(a, st);
+}
+
+// fp32: the 128-tile configuration only (its waves hold the blocked-summation accumulators)
+hipError_t gemm_f32kc_launch(GB16Args& a, int cfg, hipStream_t st) {
+  (void)cfg;
+  if (a.tri && a.amc != a.bmc) return hipErrorInvalidValue;  // a SYRK reads one operand
+  switch ((a.amc ? 1 : 0) | (a.bmc ? 2 : 0)) {
+    case 1: return launch_epi<float, 128, 128, 2, 2, 1>(a, st);
+    case 2: return launch_epi<float, 128, 128, 2, 2, 2>(a, st);
+    case 3: return launch_epi<float, 128, 128, 2, 2, 3>(a, st);
+    default: return launch_epi<float, 128, 128, 2, 2, 0>(a, st);
+  }
 }
 
 }  // namespace psgdk

@@ -418,6 +418,36 @@ def test_gemm_bf16_k_contiguous(hip, b16cfg, m, n, k):
     check_gemm_bound(C, A.double(), B.double().T)
 
 
+@pytest.mark.parametrize("nb,m,n,k", [(1, 256, 256, 256), (1, 100, 70, 36), (1, 1, 50, 76), (1, 264, 520, 72),
+                                      (1, 3072, 768, 768), (1, 1024, 1024, 3072), (12, 768, 768, 768)])
+def test_gemm_f32_k_contiguous(hip, nb, m, n, k):
+    """A (m x k) B^T with both fp32 operands k-contiguous (k a multiple of 4): the fp32 twin of the bf16 kernel (128
+    tiles, k summed in blocks of 128). Against float64: the elementwise bound of the other GEMM tests, and a worst
+    error no more than twice the general fp32 engine's on the same product (psgdk_set_option 8 = 0)."""
+    As = [rnd(m, k, seed=m + i) for i in range(nb)]
+    Bs = [rnd(n, k, seed=n + 7 * i + 1) for i in range(nb)]
+    Ad = [a.to(DEV) for a in As]
+    Bd = [b_.to(DEV) for b_ in Bs]
+    Cs = [torch.empty(m, n, device=DEV) for _ in range(nb)]
+    Cg = [torch.empty(m, n, device=DEV) for _ in range(nb)]
+
+    def run(out):
+        L.check(hip.psgdk_gemm(0, 0, 1, m, n, k, 1.0, 0, 0, nb, L.ptrs(Ad), k, L.ptrs(Bd), k, 0.0, L.ptrs(out), n,
+                               L.stream_of(Ad[0])))
+    try:
+        run(Cs)
+        assert hip.psgdk_set_option(8, 0) == 0
+        run(Cg)
+    finally:
+        hip.psgdk_set_option(8, 1)
+    for A, B, C, G in zip(As, Bs, Cs, Cg):
+        check_gemm_bound(C, A.double(), B.double().T)
+        ref = A.double() @ B.double().T
+        e_kc = float((C.double().cpu() - ref).abs().max())
+        e_gen = float((G.double().cpu() - ref).abs().max())
+        assert e_kc <= 2.0 * e_gen + 1e-6 * float(ref.abs().max()), (e_kc, e_gen)
+
+
 @pytest.mark.parametrize("order", [0, 1, 2])
 @pytest.mark.parametrize("nb,m,n,k", [(12, 768, 768, 768), (12, 1024, 1024, 512), (5, 1300, 520, 264)])
 def test_gemm_bf16_grouped(hip, b16cfg, order, nb, m, n, k):
