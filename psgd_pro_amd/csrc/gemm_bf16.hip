@@ -78,14 +78,14 @@ struct Ld {
   }
 
   // An fp32 operand stored m- or n-contiguous, X[k][mn] with row stride ld (the rows of the buffer are k): thread t
-  // owns the 4 x 4 block of k chunk t % 8 and tile rows 4 (t / 8) .. + 3. Four 16-byte loads (k rows; the 8 lanes
-  // of one k chunk read 128 contiguous bytes of a k row) are transposed in registers into the block's four
-  // k-contiguous chunks, stored in the same swizzled layout (at most 2-way bank conflicts). One block per thread
-  // (ROWS = NT / 2); rows past the operand and k past K read zero.
+  // owns the 4 x 4 block of k chunk (t / 4) % 8 and tile rows 4 nb .. + 3, nb = 4 (t / 32) + t % 4. Four 16-byte
+  // loads (k rows: each group of 4 lanes reads 64 contiguous bytes, the 8 lanes of one k chunk in a wave 128) are
+  // transposed in registers into the block's four k-contiguous chunks, stored in the same swizzled layout (at most
+  // 2-way bank conflicts). One block per thread (ROWS = NT / 2); rows past the operand and k past K read zero.
   __device__ __forceinline__ void load_mc(__amdgpu_buffer_rsrc_t rs, long long ld, int mn0, int rows, int k0, int K,
                                           int t) {
     static_assert(std::is_same_v<T, float> && NV == 4 && ROWS * 2 == NT, "m/n-contiguous loader: fp32, one block");
-    const int kc = t & 7, nb = t >> 3;
+    const int kc = (t >> 2) & 7, nb = (t >> 5) * 4 + (t & 3);
     const bool nok = mn0 + nb * 4 < rows;
     const int soff = (int)(((long long)k0 * ld + mn0) * 4);
 #pragma unroll
@@ -97,7 +97,7 @@ struct Ld {
     }
   }
   __device__ __forceinline__ void store_mc(T* lds, int t) const {
-    const int kc = t & 7, nb = t >> 3;
+    const int kc = (t >> 2) & 7, nb = (t >> 5) * 4 + (t & 3);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = nb * 4 + j;
