@@ -594,6 +594,19 @@ int precondition(const psgdk_kron2d_t* g, const void* const* X, int xdt, float* 
   for (int b = 0; b < nb; ++b) cur[b] = X[b];
   bool sumsq_done = false;
   float* const* dst1 = k1 != PSGDK_FACTOR_NONE ? tmp : out;
+  if (g->prec == PSGDK_PREC_F32 && curdt == PSGDK_BF16 && g_f32kc && k0 == PSGDK_FACTOR_DENSE &&
+      k1 == PSGDK_FACTOR_DENSE && m > 32) {
+    // bf16 X on the fp32 path: widened into `out` (free until the second product) so that P1 X takes the fp32
+    // twin of the k-contiguous kernel (the general engine, reading the bf16 X, ran 12 products of 768 x 3072 x 768
+    // at 27.5 TFLOP/s)
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = m; a.n = n; a.dt = curdt;
+    for (int b = 0; b < nb; ++b) { a.in[b] = cur[b]; a.out[b] = out[b]; }
+    PSGDK_HIP(noise_launch(a, st), "X to fp32");
+    curdt = PSGDK_F32;
+    for (int b = 0; b < nb; ++b) cur[b] = out[b];
+  }
   // rows: P1 X
   if (k0 == PSGDK_FACTOR_DENSE) {
     Opnd A, B;

@@ -128,6 +128,16 @@ def test_bf16_parity(hip, b16cfg, rq16):
     assert worst["Q"] < TOL16 and worst["pre_norm"] < TOL16 and worst["W"] < TOL16, worst
 
 
+@pytest.mark.parametrize("shapes,skew", [([(96, 256), (256, 96)], math.inf), ([(96, 256)], 1.0)])
+def test_fp32_precision_bf16_grads(hip, shapes, skew):
+    """fp32 arithmetic on bf16 gradients (the apply widens a bf16 gradient to fp32 before its first fp32 product;
+    the noise is drawn in bf16 like the gradient) against the float64 oracle on the same gradients upcast, at the
+    fp32 bar."""
+    eps16 = torch.finfo(torch.bfloat16).eps
+    worst, base = run_pair(shapes, steps=4, skew=skew, prec="fp32", gdt=torch.bfloat16, grad_eps=eps16)
+    assert_fp32(worst, base)
+
+
 def test_bf16_parity_dense_diag(hip, b16cfg):
     """Weights with one dense and one diagonal factor on the bf16 path (max_skew 1: 96 x 256 and 64 x 264 have a
     diagonal column factor, 256 x 96 a diagonal row factor): the diagonal P scales X's rows or columns on the way to
