@@ -200,6 +200,7 @@ struct B16Out {
   float* C[MAXB] = {};
   bf16_t* Cb[MAXB] = {};
   bf16_t* CTb[MAXB] = {};
+  float* CT[MAXB] = {};  // fp32 kernel only
   int64_t ldc = 0, ldcb = 0, ldct = 0;
 };
 
@@ -282,7 +283,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   for (int b = 0; b < nb; ++b) {
     a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
     a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
-    a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b];
+    a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b]; a.CT[b] = o.CT[b];
     a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
   }
   int cfg = b16_cfg(M, N, tri, nb);
@@ -1223,6 +1224,7 @@ int b16_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const*
 
 struct FacWs {
   float *R[MAXB], *RQ[MAXB], *coef[MAXB], *rs[MAXB], *pc[MAXB], *tpart[MAXB], *rtp[MAXB];
+  float *Ta[MAXB], *Tb[MAXB];  // fp32 transposed operands of the k-contiguous kernel (Q^T / (R Q)^T, Qn^T)
   NlbWs nw;
 };
 
@@ -1236,15 +1238,39 @@ void fac_take(Ws& w, int64_t d, int nb, FacWs& o) {
     o.pc[b] = w.take<float>(8);
     o.tpart[b] = w.take<float>(2 * (size_t)tp);
     o.rtp[b] = w.take<float>(rform_pairs(d));
+    o.Ta[b] = w.take<float>(d * d);
+    o.Tb[b] = w.take<float>(d * d);
   }
   nlb_take(w, d, nb, o.nw);
 }
 
+// Whether the fp32 factor products of a d x d group take the k-contiguous kernel's fp32 twin with transposed
+// fp32 copies of their n-contiguous operands (Q, Qn, R Q): fp32 arithmetic, d > 32 (the general engine's
+// 128 x 128 tiles, so that per-tile partials count the same), d a multiple of 4, 16-byte aligned matrices.
+bool fac_kc(int prec, int64_t d, int nb, std::initializer_list<const void* const*> ptrs) {
+  if (prec != PSGDK_PREC_F32 || !g_f32kc || d <= 32 || d % 4 || d * d * 4 >= ((int64_t)1 << 31)) return false;
+  for (auto p : ptrs)
+    for (int b = 0; b < nb; ++b)
+      if (!aligned16(p[b])) return false;
+  return true;
+}
+
+// fp32 transposed copies dst[b] = src[b]^T of d x d matrices
+int transpose_f32(int nb, int64_t d, const float* const* src, float* const* dst, hipStream_t st) {
+  EwArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.m = d; a.n = d; a.ld = d; a.i0 = 1;
+  for (int b = 0; b < nb; ++b) { a.in[b] = src[b]; a.out[b] = dst[b]; }
+  return hip_check(to_bf16_launch(a, st), "fp32 transpose");
+}
+
 // ell = nlb_spd(term1, V) + term2; L = max(betaL L + (1 - betaL) ell, ell); Qout = Q - lr/L (term1 Q - term2 Q)
 // (psgd_pro.py:132-135). term1: full symmetric, or its upper triangle when t1_tri. Qout must not alias Q.
+// qn_t (optional): set when Qout^T was also written, into w.Tb (the fp32 k-contiguous route; procrustes_run reads
+// it from there)
 int factor_update_run(int prec, int nb, int64_t d, const float* const* T1, int t1_tri, const float* const* Q,
                       float* const* Qout, float* const* Lv, const float* const* V, float lr, float betaL, float term2,
-                      const FacWs& w, hipStream_t st) {
+                      const FacWs& w, hipStream_t st, bool* qn_t = nullptr) {
   {
     NlbFinal fin;
     std::memset(&fin, 0, sizeof fin);
@@ -1260,6 +1286,18 @@ int factor_update_run(int prec, int nb, int64_t d, const float* const* T1, int t
   EpiSpec e;
   e.epi = EPI_FACTOR; e.ldx = d;
   for (int b = 0; b < nb; ++b) { a.p[b] = T1[b]; bq.p[b] = Q[b]; e.X1[b] = Q[b]; e.s[b] = w.coef[b]; }
+  if (qn_t && !t1_tri && fac_kc(prec, d, nb, {reinterpret_cast<const void* const*>(T1), reinterpret_cast<const void* const*>(Q),
+                                              reinterpret_cast<const void* const*>(Qout), reinterpret_cast<const void* const*>(w.Ta),
+                                              reinterpret_cast<const void* const*>(w.Tb)})) {
+    // Q^T into Ta; Qn = Q - c (term1 Q - term2 Q) with term1 and Q^T k-contiguous, Qn^T into Tb on the way out
+    PSGDK_TRY(transpose_f32(nb, d, Q, w.Ta, st));
+    B16Out o;
+    o.ldc = d; o.ldct = d;
+    const void *Ac[MAXB], *Bc[MAXB];
+    for (int b = 0; b < nb; ++b) { Ac[b] = T1[b]; Bc[b] = w.Ta[b]; o.C[b] = Qout[b]; o.CT[b] = w.Tb[b]; }
+    *qn_t = true;
+    return run_b16(nb, d, d, d, Ac, d, Bc, d, o, e, 0, 0, nullptr, st, 4);
+  }
   return run_gemm(prec, nb, d, d, d, a, bq, Qout, d, e, 0, 0, 0, 1, 0, st);
 }
 
@@ -1301,8 +1339,9 @@ int procrustes_r2_tail(int prec, int nb, int64_t d, const float* const* Q, float
   return run_gemm(prec, nb, d, d, d, a, bq, Qout, d, e, 0, 0, 0, 1, 0, st);
 }
 
+// q_t: w.Tb already holds Q^T (written by factor_update_run)
 int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* const* Qout, const float* const* V,
-                   const FacWs& w, hipStream_t st, bool r2 = false) {
+                   const FacWs& w, hipStream_t st, bool r2 = false, bool q_t = false) {
   {
     EwArgs a;
     std::memset(&a, 0, sizeof a);
@@ -1320,6 +1359,40 @@ int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* co
     PSGDK_TRY(run_nlb_full(d, -1, nb, Rc, d, 0, V, fin, w.nw, st));
   }
   if (r2) return procrustes_r2_tail(prec, nb, d, Q, Qout, w, st);
+  if (fac_kc(prec, d, nb, {reinterpret_cast<const void* const*>(Q), reinterpret_cast<const void* const*>(Qout),
+                           reinterpret_cast<const void* const*>(w.R), reinterpret_cast<const void* const*>(w.RQ),
+                           reinterpret_cast<const void* const*>(w.Ta), reinterpret_cast<const void* const*>(w.Tb)})) {
+    // k-contiguous operands: Q^T (Tb), then R Q -> RQ and (R Q)^T (Ta), then R RQ with (R Q)^T
+    if (!q_t) PSGDK_TRY(transpose_f32(nb, d, Q, w.Tb, st));
+    const void *Ac[MAXB], *Bc[MAXB];
+    {
+      B16Out o;
+      o.ldc = d; o.ldct = d;
+      EpiSpec e;
+      e.epi = EPI_RQ; e.ldx = d;
+      for (int b = 0; b < nb; ++b) {
+        Ac[b] = w.R[b]; Bc[b] = w.Tb[b]; o.C[b] = w.RQ[b]; o.CT[b] = w.Ta[b];
+        e.X1[b] = w.R[b]; e.s[b] = w.rs[b]; e.part[b] = w.tpart[b];
+      }
+      PSGDK_TRY(run_b16(nb, d, d, d, Ac, d, Bc, d, o, e, 0, 0, nullptr, st, 4));
+    }
+    {
+      EwArgs a;
+      std::memset(&a, 0, sizeof a);
+      a.nb = nb; a.i0 = gemm_tiles(d, d, 0); a.f0 = 0.125f;
+      for (int b = 0; b < nb; ++b) { a.in2[b] = w.tpart[b]; a.sc[b] = w.rs[b]; a.out[b] = w.pc[b]; }
+      PSGDK_HIP(proc_scalar_launch(a, st), "procrustes step size");
+    }
+    B16Out o;
+    o.ldc = d;
+    EpiSpec e;
+    e.epi = EPI_PROC; e.ldx = d;
+    for (int b = 0; b < nb; ++b) {
+      Ac[b] = w.R[b]; Bc[b] = w.Ta[b]; o.C[b] = Qout[b];
+      e.X1[b] = Q[b]; e.X2[b] = w.RQ[b]; e.s[b] = w.pc[b];
+    }
+    return run_b16(nb, d, d, d, Ac, d, Bc, d, o, e, 0, 0, nullptr, st, 4);
+  }
   {
     Opnd a, bq;
     a.mode = KC; a.ld = d;
@@ -1688,8 +1761,10 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
     const float* Qc[MAXB];
     const float* Qnc[MAXB];
     for (int b = 0; b < nb; ++b) { T1c[b] = T1[b]; Qc[b] = g->Q[f][b]; Qnc[b] = Qn[b]; }
-    PSGDK_TRY(factor_update_run(g->prec, nb, d, T1c, term_tri, Qc, Qn, g->L[f], Vs, o->lr, o->betaL, term2, fw, st));
-    PSGDK_TRY(procrustes_run(g->prec, nb, d, Qnc, g->Q[f], Vk, fw, st, o->r2 != 0));
+    bool qn_t = false;
+    PSGDK_TRY(factor_update_run(g->prec, nb, d, T1c, term_tri, Qc, Qn, g->L[f], Vs, o->lr, o->betaL, term2, fw, st,
+                                &qn_t));
+    PSGDK_TRY(procrustes_run(g->prec, nb, d, Qnc, g->Q[f], Vk, fw, st, o->r2 != 0, qn_t));
   }
   // P refresh (psgd_pro_fast.py:191-192)
   int sel[MAXB];

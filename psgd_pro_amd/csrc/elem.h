@@ -59,7 +59,8 @@ hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
 hipError_t sumsq_launch(const EwArgs& a, hipStream_t st);
 // full symmetric matrix from the packed upper triangle
 hipError_t unpack_launch(const EwArgs& a, hipStream_t st);
-// bf16 copy (i0 = 0) or bf16 transposed copy (i0 = 1) of an fp32 matrix into out2 (m x n, leading dimension n)
+// bf16 copy (i0 = 0) or bf16 transposed copy (i0 = 1) of an fp32 matrix into out2 (m x n, leading dimension n); with
+// out set, the fp32 copy into out
 hipError_t to_bf16_launch(const EwArgs& a, hipStream_t st);
 
 }  // namespace psgdk

@@ -714,7 +714,8 @@ hipError_t unpack_launch(const EwArgs& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // out2[b] (bf16, m x n row-major, leading dimension n) = bf16(in[b]) (i0 = 0) or bf16(in[b]^T) (i0 = 1, in is
-// n x m with leading dimension a.ld); 64 x 64 tiles through LDS. grid: tiles * nb.
+// n x m with leading dimension a.ld); with out[b] set, the same copy in fp32 into out[b] instead. 64 x 64 tiles
+// through LDS. grid: tiles * nb.
 __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
   __shared__ float t[64][65];
   const int TM = (int)((a.m + 63) / 64), TN = (int)((a.n + 63) / 64);
@@ -722,11 +723,15 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
   const int I = tile / TN, J = tile % TN;  // output tile (rows I, cols J)
   const float* __restrict__ X = reinterpret_cast<const float*>(a.in[b]);
   bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
+  float* __restrict__ Yf = a.out[b];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   if (a.i0 == 0) {
     for (int r = ty; r < 64; r += 4) {
       const long long gi = (long long)I * 64 + r, gj = (long long)J * 64 + tx;
-      if (gi < a.m && gj < a.n) Y[gi * a.n + gj] = f32_to_bf16(X[gi * a.ld + gj]);
+      if (gi < a.m && gj < a.n) {
+        if (Yf) Yf[gi * a.n + gj] = X[gi * a.ld + gj];
+        else Y[gi * a.n + gj] = f32_to_bf16(X[gi * a.ld + gj]);
+      }
     }
     return;
   }
@@ -738,7 +743,10 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
   __syncthreads();
   for (int r = ty; r < 64; r += 4) {
     const long long gi = (long long)I * 64 + r, gj = (long long)J * 64 + tx;
-    if (gi < a.m && gj < a.n) Y[gi * a.n + gj] = f32_to_bf16(t[tx][r]);
+    if (gi < a.m && gj < a.n) {
+      if (Yf) Yf[gi * a.n + gj] = t[tx][r];
+      else Y[gi * a.n + gj] = f32_to_bf16(t[tx][r]);
+    }
   }
 }
 hipError_t to_bf16_launch(const EwArgs& a, hipStream_t st) {

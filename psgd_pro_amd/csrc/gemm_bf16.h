@@ -6,7 +6,7 @@ namespace psgdk {
 
 // C = op over acc = A B^T where A is M x K and B is N x K, both row-major bf16 with k contiguous (X[mn][k]).
 // Outputs (each optional per launch): C (fp32, row-major, ldc), Cb (bf16, row-major, ldcb), CTb (bf16 of C^T,
-// row-major N x M, ldct). Epilogues as in gemm.h (EPI_STORE uses alpha only), except that EPI_RQ reads X1 (R) as
+// row-major N x M, ldct), CT (fp32 of C^T, ldct; the fp32 kernel). Epilogues as in gemm.h (EPI_STORE uses alpha only), except that EPI_RQ reads X1 (R) as
 // bf16.
 struct GB16Args {
   int M, N, K;
@@ -23,6 +23,7 @@ struct GB16Args {
   float* C[MAXB];
   bf16_t* Cb[MAXB];
   bf16_t* CTb[MAXB];
+  float* CT[MAXB];      // fp32 kernel: fp32 copy of C^T (row stride ldct)
   const float* X1[MAXB];
   const float* X2[MAXB];
   const float* s[MAXB];

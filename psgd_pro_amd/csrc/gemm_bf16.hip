@@ -351,6 +351,7 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   float* __restrict__ C = p.C[b];
   bf16_t* __restrict__ Cb = p.Cb[b];
   bf16_t* __restrict__ CTb = p.CTb[b];
+  float* __restrict__ CTf = p.CT[b];
   const float* __restrict__ X1 = p.X1[b];
   const float* __restrict__ X2 = p.X2[b];
   float s0 = 0.f, s1 = 0.f;
@@ -359,11 +360,12 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     s0 = p.s[b][0];
   if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB) s1 = p.s[b][1];
   const bool mirror = p.tri && p.out_mode == 1;
-  const bool colpass = CTb != nullptr || mirror || EPI == EPI_RQ || EPI == EPI_STRACE;
+  const bool colpass = CTb != nullptr || CTf != nullptr || mirror || EPI == EPI_RQ || EPI == EPI_STRACE;
   auto al = [](const void* q, int bytes) { return (reinterpret_cast<uintptr_t>(q) & (bytes - 1)) == 0; };
   const bool fast = m0 + BM <= p.M && n0 + BN <= p.N && (!p.tri || ti < tj) &&
                     (!C || ((p.ldc & 3) == 0 && al(C, 16))) && (!Cb || ((p.ldcb & 3) == 0 && al(Cb, 8))) &&
-                    (!CTb || ((p.ldct & 3) == 0 && al(CTb, 8))) && (p.ldx & 3) == 0 &&
+                    (!CTb || ((p.ldct & 3) == 0 && al(CTb, 8))) && (!CTf || ((p.ldct & 3) == 0 && al(CTf, 16))) &&
+                    (p.ldx & 3) == 0 &&
                     (!X1 || al(X1, EPI == EPI_RQ && !std::is_same_v<T, float> ? 8 : 16)) && (!X2 || al(X2, 16));
   float t1 = 0.f, t2 = 0.f;
   // one half of each wave's rows; h is a template constant so that the accumulator indices stay static (a loop
@@ -615,6 +617,13 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
             for (int e = 0; e < 4; ++e)
               if (ok[e] && row + e < col) t2 += v[e] * x[e];
           }
+        }
+        if (CTf) {
+          float* dst = CTf + (long long)col * p.ldct + row;
+          if (FAST || (all && (p.ldct & 3) == 0)) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          else
+#pragma unroll
+            for (int e = 0; e < 4; ++e) if (ok[e]) dst[e] = v[e];
         }
         if (CTb) {
           bf16_t* dst = CTb + (long long)col * p.ldct + row;
