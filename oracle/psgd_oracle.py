@@ -1,7 +1,8 @@
 """CPU oracle for the PSGD-Kron "Pro" preconditioner (dQ = Q^0.5 E Q^1.5).
 
-TEST INFRASTRUCTURE ONLY. This module is the checker: it is imported by tests/, by __graft_entry__.smoke() and by
-bench.py's cpu_baseline leg, and by nothing under psgd_pro_amd/. The product path never calls it.
+TEST INFRASTRUCTURE ONLY. This module is the reference against which results are compared: it is imported by
+tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, and by nothing under psgd_pro_amd/. The
+product path never calls it.
 
 A clean-room restatement, in plain PyTorch on the CPU (float64 or float32), of the arithmetic in the reference's
 psgd_pro.py (line numbers below are that file's unless another file is named). Every random draw comes from one
