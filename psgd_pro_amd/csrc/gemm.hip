@@ -38,15 +38,22 @@ template <> __device__ __forceinline__ uint4 pack_vec<1>(const float* v) {
                     pack2(f32_to_bf16(v[4]), f32_to_bf16(v[5])), pack2(f32_to_bf16(v[6]), f32_to_bf16(v[7])));
 }
 
+// Element (mn, k) of an operand (KC: p[mn][k]; MC: p[k][mn]; SYM: the upper triangle, the lower one mirrored with
+// `sign`, zero for sign 0, a zero diagonal for sign < 0), zero past rows or K. Branch-free: the offset and a scale
+// (0, 1 or sign) are selected first and the load is unconditional (element 0 for an element that is not read, the
+// scale then selecting zero rather than multiplying, so that a non-finite element 0 cannot leak in).
 template <typename T>
 __device__ __forceinline__ float fetch(const T* __restrict__ p, int mode, int sign, long long ld, int mn, int k,
                                        int rows, int K) {
-  if (mn >= rows || k >= K) return 0.f;
-  if (mode == KC) return to_f32<T>(p[(long long)mn * ld + k]);
-  if (mode == MC) return to_f32<T>(p[(long long)k * ld + mn]);
-  if (mn < k) return to_f32<T>(p[(long long)mn * ld + k]);
-  if (mn > k) return sign == 0 ? 0.f : (float)sign * to_f32<T>(p[(long long)k * ld + mn]);
-  return sign < 0 ? 0.f : to_f32<T>(p[(long long)k * ld + k]);
+  const bool in = mn < rows && k < K;
+  const bool up = mode == KC || (mode == SYM && mn < k);
+  const long long off = !in ? 0 : up ? (long long)mn * ld + k : (long long)k * ld + mn;
+  const float sc = !in ? 0.f
+                 : mode != SYM || mn < k ? 1.f
+                 : mn > k ? (float)sign
+                          : (sign < 0 ? 0.f : 1.f);
+  const float v = to_f32<T>(p[off]);
+  return sc != 0.f ? sc * v : 0.f;
 }
 
 // Loads CE consecutive k of row mn (KC addressing) and converts them to the compute type.
