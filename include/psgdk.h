@@ -254,8 +254,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * waves; other values are refused); option 2 = workgroups
  * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of the V A
  * kernels (2, 4 or 8; default 4; the column-block kernel takes 2 or 4); option 4 = the V A kernel of full-storage
- * norm bounds (-1 by shape: 2 for bf16, 1 for fp32; 0 split-K products plus a reduce kernel, 1 one workgroup per
- * 64 output columns over the whole k range, 2 the same with A staged through LDS in row-contiguous runs, bf16 only;
+ * norm bounds (-1 by shape: 2; 0 split-K products plus a reduce kernel, 1 one workgroup per
+ * 64 output columns over the whole k range, 2 the same with A staged through LDS in row-contiguous runs;
  * shapes the column kernels cannot read take the split-K kernel); option 5 = how the bf16 update
  * forms term1 Q for a factor whose other side m is under half of its side d (1, default: Pg^T (Pg Q) or Pg (Pg^T Q),
  * 4 m d^2 flops; 0: term1 Q, 2 d^3 flops); option 6 = side streams of psgdk_kron2d_update_groups (default 3; 0 or

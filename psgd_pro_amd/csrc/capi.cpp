@@ -208,9 +208,8 @@ int g_tile_order = 2;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous 
 int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's tile config
 int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
 int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
-int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape (2 for bf16, 1 for fp32 where the layout
-                          // holds, else 0), 0 split-K + reduce, 1 column blocks, 2 column blocks with A staged
-                          // through LDS (bf16; fp32 takes 1)
+int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape (2 where the layout holds, else 0),
+                          // 0 split-K + reduce, 1 column blocks, 2 column blocks with A staged through LDS
 int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
 int g_upd_streams = 3;    // psgdk_set_option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
 int g_rq16 = 1;           // psgdk_set_option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
@@ -462,7 +461,7 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
   NlbArgs a = nlb_args(n, sign, nb, Af, lda, w);
   nlb_full_plan(n, nb, w.part_cols, a.ksplit, a.kslice);
   a.vmm_u = g_vmm_u;
-  a.vmm_cols = g_vmm_cols != 0 && vmm_cols_ok(n, nb, A, lda, a_bf16 ? 2 : 4, w) ? (a_bf16 && g_vmm_cols != 1 ? 2 : 1) : 0;
+  a.vmm_cols = g_vmm_cols != 0 && vmm_cols_ok(n, nb, A, lda, a_bf16 ? 2 : 4, w) ? (g_vmm_cols != 1 ? 2 : 1) : 0;
   a.ssc = a.vmm_cols ? 64 : 128;
   if (a.vmm_cols && a.vmm_u == 8) a.vmm_u = 4;
   if (stats_in_part) PSGDK_HIP(nlb_full_launch(a, 3, a_bf16, 0, st), "row norms from partials");

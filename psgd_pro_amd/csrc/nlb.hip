@@ -801,55 +801,63 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
   if ((tid & 7) == 0) p.ssout[b][row * nbk + cb] = sq;
 }
 
-// The product of vmm_cols_kernel (bf16 operands) with A staged through LDS: the workgroup's 64 rows of A are read in
-// chunks of 64 rows x 256 k, each row's 512 bytes by 32 consecutive lanes (row-contiguous runs, as a row-norm pass
-// reads them; the MFMA fragment layout would read 64-byte pieces of 16 rows per load), stored with a 528-byte row
-// pitch (16 fragment rows land on 16 distinct 16-byte bank groups) and read back as MFMA fragments. Wave w
-// multiplies k = w 64 .. w 64 + 63 of every chunk (2 MFMA steps, V fragments straight from global memory); the next
-// chunk's A and V loads are in flight while a chunk is multiplied. The four waves' partial blocks are summed
-// through LDS in the fixed order w = 0..3 and the epilogue is vmm_cols_kernel's.
+// The product of vmm_cols_kernel with A staged through LDS: the workgroup's 64 rows of A are read in chunks of
+// 64 rows x 512 bytes (256 bf16 or 128 fp32 of k), each row's 512 bytes by 32 consecutive lanes (row-contiguous
+// runs, as a row-norm pass reads them; the MFMA fragment layout would read 64-byte pieces of 16 rows per load),
+// stored with a 528-byte row pitch (16 fragment rows land on 16 distinct 16-byte bank groups) and read back as MFMA
+// fragments. Wave w multiplies the k quarter w of every chunk (2 MFMA steps, V fragments straight from global
+// memory; fp32: four 16x16x4 MFMAs per fragment pair, element s of every lane's piece at k = kk + 4 g + s for both
+// operands); the next chunk's A and V loads are in flight while a chunk is multiplied. The four waves' partial
+// blocks are summed through LDS in the fixed order w = 0..3 and the epilogue is vmm_cols_kernel's.
 // grid: nb * ceil(n / 64).
-constexpr int VRK = 256;          // k per chunk
-constexpr int VR_LD = VRK + 8;    // LDS row pitch (bf16 elements): 528 bytes
-constexpr int VR_SMEM = VMC * VR_LD * 2 > 4 * NLB_K * VMC_LD * 4 ? VMC * VR_LD * 2 : 4 * NLB_K * VMC_LD * 4;
+constexpr int VR_ROWB = 512;                   // bytes of one row per chunk
+constexpr int VR_PITCH = VR_ROWB + 16;         // LDS row pitch in bytes
+constexpr int VR_SMEM = VMC * VR_PITCH > 4 * NLB_K * VMC_LD * 4 ? VMC * VR_PITCH : 4 * NLB_K * VMC_LD * 4;
 
+template <typename T>
 __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int normalize) {
+  constexpr int CE = 16 / sizeof(T);          // elements per 16-byte piece
+  constexpr int VRK = VR_ROWB / sizeof(T);    // k per chunk
+  constexpr int VR_LD = VR_PITCH / sizeof(T);  // LDS row pitch (elements)
+  constexpr int KS = 4 * CE;                  // k per MFMA step
   __shared__ float rs[NLB_K];
   __shared__ __attribute__((aligned(16))) unsigned char sm[VR_SMEM];
-  bf16_t* const As = reinterpret_cast<bf16_t*>(sm);
+  T* const As = reinterpret_cast<T*>(sm);
   const int n = p.n, nbk = (n + VMC - 1) / VMC;
   const int K = p.kdim ? p.kdim : n;
   const int b = blockIdx.x / nbk, cb = blockIdx.x % nbk;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   const int c0 = cb * VMC;
-  const bf16_t* __restrict__ A = reinterpret_cast<const bf16_t*>(p.A[b]);
-  const bf16_t* __restrict__ V = reinterpret_cast<const bf16_t*>(p.Vin[b]);
+  const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
+  const T* __restrict__ V = reinterpret_cast<const T*>(p.Vin[b]);
   if (tid < NLB_K) rs[tid] = p.plain ? 1.f : vmm_row_scale(p, b, tid, nbk, normalize);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * K * 2);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * 2);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * K * sizeof(T));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * sizeof(T));
   // A staging: thread t owns the 16-byte piece t % 32 of rows t / 32 + 8 i (i < 8) of the chunk
   const int rr = tid >> 5, pc = tid & 31;
   int ao[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    ao[i] = c0 + rr + 8 * i < n ? (int)(((long long)(c0 + rr + 8 * i) * p.lda + pc * 8) * 2) : kOob;
+    ao[i] = c0 + rr + 8 * i < n ? (int)(((long long)(c0 + rr + 8 * i) * p.lda + pc * CE) * sizeof(T)) : kOob;
   int vo[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * K + g * 8) * 2;
+  for (int i = 0; i < 2; ++i) vo[i] = ((i * 16 + r16) * K + g * CE) * (int)sizeof(T);
   uint4 st[8], vn[2][2];
   auto load = [&](int kc) {  // chunk at k = kc: A pieces into st, this wave's V fragments into vn
-    const bool kin = kc + pc * 8 < K;
+    const bool kin = kc + pc * CE < K;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      st[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, kin ? ao[i] : kOob, kc * 2, 0));
+      st[i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, kin ? ao[i] : kOob, kc * (int)sizeof(T), 0));
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int kk = kc + wave * 64 + s * 32;
-      const bool vin = kk + g * 8 < K;
+      const int kk = kc + wave * (VRK / 4) + s * KS;
+      const bool vin = kk + g * CE < K;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        vn[s][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vin ? vo[i] : kOob, kk * 2, 0));
+        vn[s][i] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vin ? vo[i] : kOob, kk * (int)sizeof(T), 0));
     }
   };
   f32x4_t acc[2][4];
@@ -860,7 +868,7 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
   load(0);
   for (int kc = 0; kc < K; kc += VRK) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(As + (rr + 8 * i) * VR_LD + pc * 8) = st[i];
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(As + (rr + 8 * i) * VR_LD + pc * CE) = st[i];
     uint4 vc[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -870,16 +878,27 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     if (kc + VRK < K) load(kc + VRK);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int kl = wave * 64 + s * 32 + g * 8;
-      bf16x8_t af[4];
+      const int kl = wave * (VRK / 4) + s * KS + g * CE;
+      uint4 af[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) af[j] = *reinterpret_cast<const bf16x8_t*>(As + (j * 16 + r16) * VR_LD + kl);
+      for (int j = 0; j < 4; ++j) af[j] = *reinterpret_cast<const uint4*>(As + (j * 16 + r16) * VR_LD + kl);
+      if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vc[s][i]), af[j], acc[i][j],
-                                                              0, 0, 0);
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vc[s][i]),
+                                                                __builtin_bit_cast(bf16x8_t, af[j]), acc[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float((&vc[s][i].x)[s4]),
+                                                               __uint_as_float((&af[j].x)[s4]), acc[i][j], 0, 0, 0);
+      }
     }
     __syncthreads();
   }
@@ -912,13 +931,13 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     w[e] *= sc;
     if (col + e < n) sq += w[e] * w[e];
   }
-  bf16_t* __restrict__ W = reinterpret_cast<bf16_t*>(p.Vout[b]) + (long long)row * n + col;
+  T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
   if (col + 8 <= n) {
     store8(W, w);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (col + e < n) W[e] = f32_to_bf16(w[e]);
+      if (col + e < n) W[e] = from_f32<T>(w[e]);
   }
   if (p.plain) return;
   sq += __shfl_xor(sq, 1, 64);
@@ -1028,8 +1047,9 @@ hipError_t nlb_full_launch(const NlbArgs& a, int stage, int a_bf16, int normaliz
     else hipLaunchKernelGGL(nlb_init_full_kernel<float>, dim3(a.nb * NLB_K), dim3(256), 0, st, a);
   } else if (a.vmm_cols) {
     const dim3 grid(((a.n + VMC - 1) / VMC) * a.nb);
-    if (a_bf16 && a.vmm_cols == 2) {
-      hipLaunchKernelGGL(vmm_rows_kernel, grid, dim3(256), 0, st, a, normalize);
+    if (a.vmm_cols == 2) {
+      if (a_bf16) hipLaunchKernelGGL(vmm_rows_kernel<bf16_t>, grid, dim3(256), 0, st, a, normalize);
+      else hipLaunchKernelGGL(vmm_rows_kernel<float>, grid, dim3(256), 0, st, a, normalize);
     } else if (a_bf16) {
       if (a.vmm_u == 2) hipLaunchKernelGGL((vmm_cols_kernel<bf16_t, 2>), grid, dim3(256), 0, st, a, normalize);
       else hipLaunchKernelGGL((vmm_cols_kernel<bf16_t, 4>), grid, dim3(256), 0, st, a, normalize);

@@ -224,8 +224,8 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, ta
     """Full-storage bound (psgd_pro.py:19-65) of two matrices in one call, against the float64 oracle on the same
     (storage-rounded) matrices. cols = 1: the column-block V A kernel where the layout allows it (n and lda
     multiples of 16 bytes: fp32 n = 100 with a ragged last block, 768, 1000, 3072), else the split-K kernel;
-    cols = 2: the same with A staged through LDS for bf16 (n = 1000: ragged last k chunk and column block), the
-    column-block kernel for fp32; cols = -1: the library's choice by shape;
+    cols = 2: the same with A staged through LDS (n = 1000: ragged last k chunk and column block; fp32 n = 100:
+    one partial chunk); cols = -1: the library's choice by shape;
     cols = 0: the split-K kernel, whose workgroup target 1 gives one k slice, 2^20 the most slices, 1024 the
     default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path). fp32:
     rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
