@@ -203,111 +203,137 @@ hipError_t rowsq_launch(const EwArgs& a, hipStream_t st) {
 // both tiles are staged in LDS (16-byte loads when rows are 16-byte aligned), each output tile is written
 // row-major from there, 4 consecutive columns per thread (16-byte fp32 / 8-byte bf16 stores). Outputs: R fp32
 // (out, optional) and R bf16 (out2, optional); with sc[b] set, sc[b][pair] = sum of R_ij Q_ij over the pair's
-// elements (fp32 values, a fixed-order block sum; the r2 Procrustes trace). grid: nb * T (T + 1) / 2,
-// T = ceil(d / 64).
+// elements (fp32 values, a fixed-order block sum; the r2 Procrustes trace). Pairs are numbered p = b np + pair
+// (np = T (T + 1) / 2, T = ceil(d / 64)); workgroup w takes p = w, w + G, w + 2 G, ... (G = the grid) and loads
+// the next pair's two tiles into registers while it writes the current one, so that every workgroup keeps loads
+// in flight through its output phase. grid: min(nb np, RF_GRID).
+constexpr int RF_GRID = 1024;  // 4 workgroups (34 KB of LDS each) on each of 256 CUs
+
 __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
   constexpr int TP = 65;        // LDS pitch (floats): column reads of the transposed tile are conflict-free
   __shared__ float qa[64 * TP];  // Q[I block][J block]
   __shared__ float qb[64 * TP];  // Q[J block][I block]
-  const int d = (int)a.m, T = (d + 63) / 64, np = T * (T + 1) / 2;
-  const int b = blockIdx.x / np;
-  int t = blockIdx.x % np, I = 0;
-  while (t >= T - I) { t -= T - I; ++I; }
-  const int J = I + t;
-  const int pair = blockIdx.x % np;
-  const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
-  float* __restrict__ R = a.out[b];
-  bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
+  __shared__ float rsq[2][64], rmx[2][64];  // row statistics of the two tiles, written out as 256-byte runs
+  __shared__ float red[16];
+  const int d = (int)a.m, T = (d + 63) / 64, np = T * (T + 1) / 2, total = np * a.nb;
   const long long ld = a.ld;
   const float sg = (float)a.i0;
   const int tid = threadIdx.x, c4 = (tid & 15) * 4, r0 = tid >> 4;  // 4 columns, rows r0 + 16 k
-  const bool full = (I + 1) * 64 <= d && (J + 1) * 64 <= d;
-  const bool vec = full && (ld & 3) == 0 && (reinterpret_cast<uintptr_t>(Q) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(R) & 15) == 0 && (reinterpret_cast<uintptr_t>(Rb) & 7) == 0;
-  auto stage = [&](float* dst, int rb, int cb) {  // Q[rb block][cb block] -> dst
+  auto decode = [&](int p, int& b, int& I, int& J) {
+    b = p / np;
+    int t = p % np, i = 0;
+    while (t >= T - i) { t -= T - i; ++i; }
+    I = i;
+    J = i + t;
+  };
+  float pv[2][4][4];  // the pair's tiles (I, J) and (J, I) as this thread stages them: [tile][k][column]
+  auto fetch = [&](int p) {
+    int b, I, J;
+    decode(p, b, I, J);
+    const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
+    const bool vec = (I + 1) * 64 <= d && (J + 1) * 64 <= d && (ld & 3) == 0 &&
+                     (reinterpret_cast<uintptr_t>(Q) & 15) == 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
-      float v[4];
-      if (vec) {
-        const float4 q = *reinterpret_cast<const float4*>(Q + (long long)gi * ld + gj);
-        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-      } else {
+    for (int h = 0; h < 2; ++h) {
+      const int rb = h ? J : I, cb = h ? I : J;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (gi < d && gj + e < d) ? Q[(long long)gi * ld + gj + e] : 0.f;
+      for (int k = 0; k < 4; ++k) {
+        const int gi = rb * 64 + r0 + 16 * k, gj = cb * 64 + c4;
+        if (vec) {
+          const float4 q = *reinterpret_cast<const float4*>(Q + (long long)gi * ld + gj);
+          pv[h][k][0] = q.x; pv[h][k][1] = q.y; pv[h][k][2] = q.z; pv[h][k][3] = q.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pv[h][k][e] = (gi < d && gj + e < d) ? Q[(long long)gi * ld + gj + e] : 0.f;
+        }
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[r * TP + c4 + e] = v[e];
     }
   };
-  stage(qa, I, J);
-  stage(qb, J, I);
-  __syncthreads();
-  // out(rb, cb)[r][c] = sg (src_t[c][r] - src[r][c]): (I, J) from (qb, qa), (J, I) from (qa, qb)
-  float tr = 0.f;  // sum of R_ij Q_ij (out-of-range elements are zero in both staged tiles)
-  float* __restrict__ st = a.aux[b];
-  __shared__ float rsq[2][64], rmx[2][64];  // row statistics of the two tiles, written out as 256-byte runs
-  auto emit = [&](const float* src, const float* srct, int rb, int cb) {
+  if ((int)blockIdx.x < total) fetch(blockIdx.x);
+  for (int p = blockIdx.x; p < total; p += gridDim.x) {
+    int b, I, J;
+    decode(p, b, I, J);
+    const int pair = p - b * np;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
-      float v[4];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
-        tr += v[e] * src[r * TP + c4 + e];
-      }
-      if (st) {  // row statistics of the bf16 R over this tile's 64 columns (the 16 lanes of row r), fixed tree
-        float s2 = 0.f, mx = 0.f;
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) (h ? qb : qa)[(r0 + 16 * k) * TP + c4 + e] = pv[h][k][e];
+    __syncthreads();
+    if (p + (int)gridDim.x < total) fetch(p + gridDim.x);
+    const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
+    float* __restrict__ R = a.out[b];
+    bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
+    const bool vec = (I + 1) * 64 <= d && (J + 1) * 64 <= d && (ld & 3) == 0 &&
+                     (reinterpret_cast<uintptr_t>(Q) & 15) == 0 && (reinterpret_cast<uintptr_t>(R) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(Rb) & 7) == 0;
+    // out(rb, cb)[r][c] = sg (src_t[c][r] - src[r][c]): (I, J) from (qb, qa), (J, I) from (qa, qb)
+    float tr = 0.f;  // sum of R_ij Q_ij (out-of-range elements are zero in both staged tiles)
+    float* __restrict__ st = a.aux[b];
+    auto emit = [&](const float* src, const float* srct, int rb, int cb) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = r0 + 16 * k, gi = rb * 64 + r, gj = cb * 64 + c4;
+        float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float q = bf16_to_f32(f32_to_bf16(v[e]));
-          s2 += q * q;
-          mx = fmaxf(mx, fabsf(q));
+          v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
+          tr += v[e] * src[r * TP + c4 + e];
         }
-        row16_sum_max(s2, mx);
-        if ((tid & 15) == 0) {
-          const int t = rb == I ? 0 : 1;  // tile (I, J) or (J, I)
-          rsq[t][r] = s2;
-          rmx[t][r] = mx;
-        }
-      }
-      const long long o = (long long)gi * ld + gj;
-      if (vec) {
-        if (R) *reinterpret_cast<float4*>(R + o) = make_float4(v[0], v[1], v[2], v[3]);
-        if (Rb)
-          *reinterpret_cast<uint2*>(Rb + o) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
-                                                        pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
-      } else if (gi < d) {
+        if (st) {  // row statistics of the bf16 R over this tile's 64 columns (the 16 lanes of row r), fixed tree
+          float s2 = 0.f, mx = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (gj + e < d) {
-            if (R) R[o + e] = v[e];
-            if (Rb) Rb[o + e] = f32_to_bf16(v[e]);
+          for (int e = 0; e < 4; ++e) {
+            const float q = bf16_to_f32(f32_to_bf16(v[e]));
+            s2 += q * q;
+            mx = fmaxf(mx, fabsf(q));
           }
+          row16_sum_max(s2, mx);
+          if ((tid & 15) == 0) {
+            const int t = rb == I ? 0 : 1;  // tile (I, J) or (J, I)
+            rsq[t][r] = s2;
+            rmx[t][r] = mx;
+          }
+        }
+        const long long o = (long long)gi * ld + gj;
+        if (vec) {
+          if (R) *reinterpret_cast<float4*>(R + o) = make_float4(v[0], v[1], v[2], v[3]);
+          if (Rb)
+            *reinterpret_cast<uint2*>(Rb + o) = make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])),
+                                                          pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+        } else if (gi < d) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (gj + e < d) {
+              if (R) R[o + e] = v[e];
+              if (Rb) Rb[o + e] = f32_to_bf16(v[e]);
+            }
+        }
+      }
+    };
+    emit(qa, qb, I, J);
+    if (I != J) emit(qb, qa, J, I);
+    if (st) {
+      __syncthreads();
+      const int t = tid >> 6, r = tid & 63;  // threads 0-63: tile (I, J), 64-127: tile (J, I)
+      const int rb = t ? J : I, cb = t ? I : J, gi = rb * 64 + r;
+      if (t < 2 && (t == 0 || I != J) && gi < d) {
+        st[(long long)cb * d + gi] = rsq[t][r];
+        st[(long long)(T + cb) * d + gi] = rmx[t][r];
       }
     }
-  };
-  emit(qa, qb, I, J);
-  if (I != J) emit(qb, qa, J, I);
-  if (st) {
-    __syncthreads();
-    const int t = tid >> 6, r = tid & 63;  // threads 0-63: tile (I, J), 64-127: tile (J, I)
-    const int rb = t ? J : I, cb = t ? I : J, gi = rb * 64 + r;
-    if (t < 2 && (t == 0 || I != J) && gi < d) {
-      st[(long long)cb * d + gi] = rsq[t][r];
-      st[(long long)(T + cb) * d + gi] = rmx[t][r];
+    if (a.sc[b]) {
+      tr = block_sum(tr, red);
+      if (tid == 0) a.sc[b][pair] = tr;
     }
-  }
-  if (a.sc[b]) {
-    __shared__ float red[16];
-    tr = block_sum(tr, red);
-    if (tid == 0) a.sc[b][pair] = tr;
+    __syncthreads();  // the next pair rewrites qa, qb, rsq, rmx and red
   }
 }
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
-  const long long T = (a.m + 63) / 64;
-  hipLaunchKernelGGL(rform_kernel, dim3((unsigned)(T * (T + 1) / 2 * a.nb)), dim3(256), 0, st, a);
+  const long long T = (a.m + 63) / 64, total = T * (T + 1) / 2 * a.nb;
+  if (total > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rform_kernel, dim3((unsigned)(total < RF_GRID ? total : RF_GRID)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
