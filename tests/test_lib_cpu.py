@@ -64,6 +64,20 @@ def test_argument_validation():
     assert lib.psgdk_symm(0, 0, 3, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
 
 
+def test_option_ranges():
+    """psgdk_set_option accepts each option's documented values and refuses the rest (host state only)."""
+    lib = L.lib()
+    for opt, good, bad in [(1, [-1, 0, 1, 2], [3, -2]), (3, [2, 4, 8], [1, 16]), (4, [-1, 0, 1, 2], [3]),
+                           (5, [0, 1], [2]), (6, [0, 3, 8], [9, -1]), (7, [0, 1], [2]), (8, [0, 1], [2])]:
+        for v in bad:
+            assert lib.psgdk_set_option(opt, v) == L.EINVAL, (opt, v)
+        for v in good:
+            assert lib.psgdk_set_option(opt, v) == 0, (opt, v)
+    for opt, v in [(1, -1), (3, 4), (4, -1), (5, 1), (6, 3), (7, 1), (8, 1)]:  # the defaults
+        assert lib.psgdk_set_option(opt, v) == 0
+    assert lib.psgdk_set_option(99, 0) == L.EINVAL
+
+
 def test_factor_step_entry_points_reject_aliasing_without_device_work():
     """psgdk_factor_update / psgdk_procrustes write Q_out from Q in one pass, so Q_out may not alias Q: refused
     after the size query and before any launch (fake device addresses are never touched)."""
