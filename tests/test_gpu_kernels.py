@@ -464,6 +464,29 @@ def test_gemm_bf16_grouped(hip, b16cfg, order, nb, m, n, k):
         check_gemm_bound(C, A.double().cpu(), B.double().cpu().T)
 
 
+def test_syrk_bf16_microbench_shape(hip):
+    """One bf16 SYRK at n = k = 4096 (136 triangle tiles of 256: the size rule takes the 256-tile kernel because
+    K >= 4096) against float64, and bitwise equal to the 256-tile configuration forced."""
+    n = 4096
+    A = rnd(n, n, seed=4096).to(torch.bfloat16).to(DEV)
+    C = torch.full((n, n), float("nan"), device=DEV)
+    C0 = torch.full((n, n), float("nan"), device=DEV)
+    st = L.stream_of(A)
+    L.check(hip.psgdk_syrk(1, 0, L.OUT_UPPER, n, n, 1, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+    try:
+        L.check(hip.psgdk_set_option(1, 0))
+        L.check(hip.psgdk_syrk(1, 0, L.OUT_UPPER, n, n, 1, 1, L.ptrs([A]), n, L.ptrs([C0]), n, st))
+    finally:
+        L.check(hip.psgdk_set_option(1, -1))
+    triu = torch.ones(n, n, dtype=torch.bool, device=DEV).triu()
+    assert torch.equal(C[triu], C0[triu])
+    Cc = C.cpu()
+    triu = triu.cpu()
+    assert bool(torch.isnan(Cc[~triu]).all())
+    X = A.double().cpu()
+    check_gemm_bound(torch.where(triu, Cc, Cc.T), X, X.T)
+
+
 @pytest.mark.parametrize("nb,n,k", [(1, 768, 2304), (1, 3072, 768), (16, 1024, 256), (1, 200, 72)])
 def test_syrk_bf16_k_contiguous(hip, b16cfg, nb, n, k):
     As = [rnd(n, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]
