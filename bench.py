@@ -108,19 +108,33 @@ def launch_classes(recs, steps, top=12):
              "tflops": round(k[3] / (v[1] / v[0] * 1e-3) / 1e12, 1)} for k, v in rows]
 
 
+def cpu_threads():
+    """The host threads the CPU leg may use: the CPUs this process may run on, capped by OMP_NUM_THREADS when set
+    (the GPU box gives one GPU's job a share of the host, announced there through OMP_NUM_THREADS)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
 def cpu_baseline(precision, skew, seconds):
-    """The CPU oracle (float32) on one ViT-B block (4 weights), 1 warmup step, then timed steps until `seconds` of
-    work; scaled x12 to the 48-weight set."""
+    """The CPU oracle (float32) on one ViT-B block (4 weights): with every host thread the process may use, 1 warmup
+    step, then timed steps until `seconds` of work (median); with one thread, one timed step. Both scaled x12 to
+    the 48-weight set (the 12 blocks are identical, and the oracle steps the weights one after another)."""
     import torch
     from oracle import psgd_oracle as O
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    threads = cpu_threads()
     gen = torch.Generator().manual_seed(7)
     grads = [(0.01 * torch.randn(s, generator=gen)).to(torch.bfloat16).float() for s in VIT_B]
-    W = [torch.zeros(s) for s in VIT_B]
     eps = torch.finfo(torch.bfloat16).eps if precision == "bf16" else None
-    ora = O.OracleKron(W, preconditioner_max_size=8192, preconditioner_max_skew=skew, preconditioner_init_scale=1.0,
-                       seed=0, dtype=torch.float32, grad_eps=eps)
+
+    def oracle():
+        return O.OracleKron([torch.zeros(s) for s in VIT_B], preconditioner_max_size=8192,
+                            preconditioner_max_skew=skew, preconditioner_init_scale=1.0, seed=0, dtype=torch.float32,
+                            grad_eps=eps)
+    torch.set_num_threads(threads)
+    ora = oracle()
     ora.step(grads)
     times = []
     t_start = time.perf_counter()
@@ -132,9 +146,30 @@ def cpu_baseline(precision, skew, seconds):
             break
     times.sort()
     med = times[len(times) // 2]
+    torch.set_num_threads(1)
+    ora1 = oracle()
+    t0 = time.perf_counter()
+    ora1.step(grads)
+    one = time.perf_counter() - t0
+    torch.set_num_threads(threads)
     return dict(value=round(med * 1e3 * 12, 2), unit="ms/step", cores=threads, kind="port",
-                sample=f"oracle float32 on 1 ViT-B block (4 of 48 weights), median of {len(times)} steps after 1 "
-                       f"warmup, x12")
+                host_cpus=os.cpu_count(), value_1_thread=round(one * 1e3 * 12, 2),
+                sample=f"oracle float32 on 1 ViT-B block (4 of 48 weights) x12: median of {len(times)} steps after "
+                       f"1 warmup on {threads} threads; 1 step on 1 thread for value_1_thread")
+
+
+def check_finite(opt, params):
+    """Fails the run when any parameter, factor or L is not finite after the timed steps."""
+    import torch
+    bad = [i for i, p in enumerate(params) if not bool(torch.isfinite(p).all())]
+    for i in range(len(params)):
+        Qs, Ls = opt.factors(i)
+        if not all(bool(torch.isfinite(t).all()) for t in Qs + Ls):
+            bad.append(i)
+    if bad:
+        print(f"bench.py: non-finite parameters or factors after the timed steps (weights {sorted(set(bad))[:8]})",
+              file=sys.stderr)
+        sys.exit(3)
 
 
 def bench_vitb(args):
@@ -175,6 +210,7 @@ def bench_vitb(args):
     t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3 / args.steps
     ev_ms = e0.elapsed_time(e1) / args.steps
+    check_finite(opt, params)
     # Per-launch figures come from a second pass on one stream, eager, so that each kernel's HIP-event duration is
     # its own and not shared with another group's kernels.
     opt._nstreams, opt._use_graphs = 0, False
@@ -215,6 +251,7 @@ def bench_vitb(args):
         "dtype": args.precision,
         "data": "synthetic",
         "config": {"workload": "vit-b16-kron-update-apply", "weights": "12 x {768x2304, 768x768, 768x3072, 3072x768}",
+                   "cpu_baseline_sample": "one ViT-B block, x12",
                    "blocks": args.blocks, "grad_dtype": "bf16", "factor_dtype": "fp32", "max_size": 8192,
                    "max_skew": args.skew, "update_probability": 1.0, "procrustes": "r2" if args.r2 else "step2",
                    "term1_q": "pg" if args.t1q_pg else "term1", "fuse_groups": bool(args.fuse),
@@ -260,28 +297,56 @@ def bench_syrk(args):
             A = torch.randn(n, n, device=dev).to(dt)
             C = torch.empty(n, n, device=dev)
             adt = L.dtype_code(dt)
-            for _ in range(3):
+
+            def syrk():
                 L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+            for _ in range(3):
+                syrk()
             torch.cuda.synchronize()
-            reps = max(5, int(2e10 / (n ** 3)))
+            reps = max(20, int(2e10 / (n ** 3)))
+            # us: back-to-back launches between two events (the per-launch event pairs of the library's profiler,
+            # event_us, add a few microseconds of their own to a small launch)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            for _ in range(reps):
+                syrk()
+            ev[1].record()
+            torch.cuda.synchronize()
+            ms = ev[0].elapsed_time(ev[1]) / reps
             L.profile_start()
             for _ in range(reps):
-                L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+                syrk()
             recs = L.profile_stop()
-            ms = sum(r[3] for r in recs) / len(recs)
+            ms_ev = sum(r[3] for r in recs) / len(recs)
             tf = n * (n + 1) * n / (ms * 1e-3) / 1e12
             lines.append({"op": "syrk", "n": n, "k": n, "dtype": name, "us": round(ms * 1e3, 2),
-                          "tflops": round(tf, 2), "frac": round(tf / PEAK[name], 4)})
+                          "tflops": round(tf, 2), "frac": round(tf / PEAK[name], 4), "event_us": round(ms_ev * 1e3, 2)})
             B = torch.randn(n, n, device=dev)
             Af = A.float()
+            ws = L.Workspace()
+
+            def trmm():
+                L.call_ws(L.lib().psgdk_trmm_ws, prec, n, n, 0, 1, L.ptrs([Af]), n, L.ptrs([B]), n, L.ptrs([C]), n,
+                          ws=ws, device=dev, stream=st)
+            for _ in range(3):
+                trmm()
+            torch.cuda.synchronize()
+            # back-to-back whole calls (operand copies + product) between two events, and the product alone from the
+            # library's per-launch events
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             L.profile_start()
+            ev[0].record()
             for _ in range(reps):
-                L.check(L.lib().psgdk_trmm(prec, n, n, 0, 1, L.ptrs([Af]), n, L.ptrs([B]), n, L.ptrs([C]), n, st))
+                trmm()
+            ev[1].record()
+            torch.cuda.synchronize()
             recs = L.profile_stop()
-            ms = sum(r[3] for r in recs) / len(recs)
+            ms = ev[0].elapsed_time(ev[1]) / reps
+            ms_mm = sum(r[3] for r in recs) / len(recs)
             tf = n * n * (n + 1) / (ms * 1e-3) / 1e12
             lines.append({"op": "trmm", "n": n, "dtype": name, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                          "frac": round(tf / PEAK[name], 4)})
+                          "frac": round(tf / PEAK[name], 4), "product_us": round(ms_mm * 1e3, 2),
+                          "note": "us: whole psgdk_trmm_ws call (triu(Q) and B^T copies + product)"})
     return lines
 
 
@@ -310,6 +375,7 @@ def bench_llama(args):
         opt.step_math(grads)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
+    check_finite(opt, params)
     opt._nstreams, opt._use_graphs = 0, False
     L.check(L.lib().psgdk_set_option(6, 0))  # one stream: each launch's event time is its own
     L.profile_start()

@@ -69,6 +69,14 @@ int psgdk_symm(int prec, int side, int sign, int64_t n, int64_t p, int b_dtype, 
 int psgdk_trmm(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
                const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream);
 
+/* psgdk_trmm with a workspace: the operands are converted once (triu(Q) with zeros below the diagonal, and for
+ * prec bf16 B^T, in bf16) and multiplied on the k-contiguous MFMA kernel, each output tile's k loop starting at the
+ * diagonal (n(n+1)p flops in place of 2 n^2 p). Needs n and p multiples of 8 (bf16) or 4 (fp32, with fp32 B and n
+ * > 32); other shapes take psgdk_trmm and need no workspace. Q's strict lower triangle is never read. */
+int psgdk_trmm_ws(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
+                  const void* const* B, int64_t ldb, float* const* C, int64_t ldc, void* ws, size_t* ws_bytes,
+                  psgdk_stream_t stream);
+
 /* C (m x n) = alpha op(A) op(B) + beta C, op(X) = X (trans = 0) or X^T (trans = 1); A is m x k (or k x m),
  * B is k x n (or n x k). The dense contractions of the reference's hot path that have no custom kernel there
  * (R @ Q and R @ RQ in procrustes_step2, psgd_pro.py:89-90; term1 @ q, psgd_pro.py:135; the exprP chain,
@@ -172,10 +180,14 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
  * group and either dimension). Every group must be on the bf16 path (prec bf16, two factors, dense or diagonal with
  * at least one dense, every dense factor with its Qt16 / P16 shadows, sides multiples of 8, tri = 0); lr, betaL,
  * r2 and tri must agree across opts[]; damping and grad_eps
- * are per group. noise[g] and V[g] are the group's arrays as in psgdk_kron2d_update. Results are bitwise those of
- * one psgdk_kron2d_update per group. The work runs on side streams the library creates once per device (default
- * priority; psgdk_set_option 6), forked from and joined back to `stream` with events; while `stream` is being
- * captured into a HIP graph, everything runs on `stream` itself. Replaces the per-parameter
+ * are per group. noise[g] and V[g] are the group's arrays as in psgdk_kron2d_update. Each factor goes through the
+ * operations of psgdk_kron2d_update; a launch that batches more problems may take another tile configuration or k
+ * split (the size rule looks at the whole launch), which changes only the order of the sums, so the results match
+ * one psgdk_kron2d_update per group to the bf16 path's rounding (bitwise where the launches take the same
+ * configurations). The work runs on side streams the library creates once per device (default priority;
+ * psgdk_set_option 6), forked from and joined back to `stream` with events (concurrent calls from several host
+ * threads take turns on them); while `stream` is being captured into a HIP graph, everything runs on `stream`
+ * itself. Results do not depend on the number of side streams. Replaces the per-parameter
  * loop of update_2d calls
  * (psgd_pro_fast.py:351-368; the reference's batch=True stacks same-shape parameters, psgd_pro_fast.py:327-349). */
 int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
@@ -230,7 +242,7 @@ int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri,
 int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const* mom, const void* const* g,
                    psgdk_stream_t stream);
 
-/* Launch profiling (diagnostic, single host thread): after psgdk_profile_start every MFMA-engine launch is
+/* Launch profiling (diagnostic, per host thread): after psgdk_profile_start every MFMA-engine launch the thread makes is
  * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
  * waits for the recorded events and fills one record per launch: the kernel instantiation id
  * (general engine: cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype, cfg 0 = 128 x 128 tiles, 1 = 32 x 128;
@@ -248,7 +260,8 @@ typedef struct psgdk_prof_record {
 int psgdk_profile_start(void);
 int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);
 
-/* Tuning switches (process-wide): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
+/* Tuning switches, one set per host thread (a thread's settings apply to the calls it makes and never change
+ * another thread's results; a new thread starts from the defaults): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
  * XCD, 2 = 1 with tile rows grouped by 4 so that the tiles an XCD runs at once share operand panels; default 2);
  * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256 on 8 waves, 1 = 128 x 128, 2 = 256 x 256 on 4
  * waves; other values are refused); option 2 = workgroups
@@ -264,6 +277,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * products; option 8 = whether fp32 products with k- or m/n-contiguous operands (M > 32, one k range, no packed
  * output) take the k-contiguous kernel's fp32 twin (1, default) or the general engine (0). */
 int psgdk_set_option(int option, int value);
+/* The calling thread's value of a psgdk_set_option switch. */
+int psgdk_get_option(int option, int* value);
 
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
  * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B. Checks the compiler builtins' lane layout. */

@@ -170,37 +170,111 @@ def gram(Pg, i, dense):
     return X @ X.T if dense else (X * X).sum(dim=1)
 
 
+def smoothness_ema(L, ell, betaL):
+    """The Lipschitz smoothness estimate of psgd_pro.py:129,134: L <- max(betaL L + (1 - betaL) ell, ell)."""
+    return torch.maximum(betaL * L + (1 - betaL) * ell, ell)
+
+
+def momentum_beta(counter, momentum):
+    """psgd_pro.py:335: the momentum EMA factor of step `counter` (0-based), min(c / (1 + c), momentum): the buffer
+    is the running mean of the gradients while c / (1 + c) < momentum."""
+    return min(counter / (1 + counter), momentum)
+
+
+def round_bf16(x):
+    """x rounded to bfloat16 (round to nearest even) and returned in x's dtype."""
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+def precondition_rounded(Q, X, rd, final):
+    """P1 X P2 of a 2-D tensor with the operands of each product rounded by rd, where bf16-operand kernels round
+    them: a dense factor's P = rd(rd(Q)^T rd(Q)) (P is formed from the rounded Q and stored rounded), a diagonal
+    factor's p = q * q scales X before the rounding (the scaled X is the product's operand), X P2 is rounded (the
+    second product's operand), and the result is rounded when `final` (Pg, stored rounded) but not for the apply
+    (its output is the float32 preconditioned gradient). Tensors that are not 2-D, and weights whose factors are
+    both diagonal (no product), take `precondition`."""
+    if X.dim() != 2 or len(Q) != 2 or (Q[0].dim() < 2 and Q[1].dim() < 2):
+        return precondition(Q, X)
+    d1, d2 = Q[0].dim() == 2, Q[1].dim() == 2
+    P1 = rd(rd(Q[0]).T @ rd(Q[0])) if d1 else Q[0] * Q[0]
+    P2 = rd(rd(Q[1]).T @ rd(Q[1])) if d2 else Q[1] * Q[1]
+    if d1 and d2:
+        out = P1 @ rd(rd(X) @ P2)
+    elif d1:
+        out = P1 @ rd(X * P2[None, :])
+    else:
+        out = rd(P1[:, None] * X) @ P2
+    return rd(out) if final else out
+
+
+def procrustes_step2_rounded(Q, V, rd, max_step=MAX_PROCRUSTES):
+    """procrustes_step2 with rounded operands: R = rd(Q^T - Q) (stored rounded), its bound's start V rounded,
+    RQ = rs R rd(Q) with rs = 1 / (bound + smallest normal), tr(RQ) from RQ before rounding, RRQ = rs R rd(RQ) and
+    Q += a (rd(RQ) + a/2 RRQ) (the second product reads RQ rounded, the update adds that same RQ)."""
+    R = rd(Q.T - Q)
+    rs = 1.0 / (norm_lower_bound(R, V, skew=True) + smallest_normal(R.dtype))
+    RQ = (R @ rd(Q)) * rs
+    t1 = RQ.diagonal().sum()
+    RQ = rd(RQ)
+    RRQ = (R @ RQ) * rs
+    t2 = RRQ.diagonal().sum()
+    a = torch.where(t2 < 0, torch.clamp(-t1 / t2, max=max_step), torch.tensor(max_step, dtype=Q.dtype))
+    Q.add_(a * (RQ + 0.5 * a * RRQ))
+    return a
+
+
+def procrustes_step_r2_rounded(Q, V, rd, max_step=MAX_PROCRUSTES):
+    """procrustes_step_r2 with rounded operands: Rn = rd(Q - Q^T), S = rd(rs^2 Rn^T Rn) (stored rounded),
+    M = rd(a rs Rn + a^2/2 S) and Q -= M rd(Q)."""
+    Rn = rd(Q - Q.T)
+    rs = 1.0 / (norm_lower_bound(Rn, V, skew=True) + smallest_normal(Rn.dtype))
+    S = rd((Rn.T @ Rn) * rs * rs)
+    t1 = (Rn * Q).sum() * rs
+    t2 = -(S * Q).sum()
+    a = torch.where(t2 < 0, torch.clamp(-t1 / t2, max=max_step), torch.tensor(max_step, dtype=Q.dtype))
+    Q.sub_(rd(a * rs * Rn + 0.5 * a * a * S) @ rd(Q))
+    return a
+
+
 def update_preconditioner(Q, L, G, draws, lr=0.1, betaL=0.9, damping=1e-9, grad_eps=None, r2=False, trace=None,
-                          draw_dtype=torch.float32, noise_dtype=None):
+                          draw_dtype=torch.float32, noise_dtype=None, rd=None):
     """psgd_pro.py:114-139 (update_precond_kron_whiten_q0p5eq1p5), in place on Q and L, with the draws taken from
     `draws` in psgd_pro.py's order. The normals are drawn in draw_dtype (psgd_pro.py draws them in the gradient's
     dtype: float32 for the float32 models every comparison here uses) and cast to the working dtype; noise_dtype
     (default draw_dtype) overrides the dtype of the gradient-shaped noise alone, as psgd_pro_fast.draw_normals draws
     it like the gradient and the 32 x d starts like the factors (psgd_pro_fast.py:200-206): a bfloat16 gradient
     upcast for this oracle passes bfloat16. grad_eps overrides finfo(G.dtype).eps in the damping scale (the
-    reference uses the gradient's own dtype; a bfloat16 gradient upcast for this oracle passes bfloat16's eps)."""
+    reference uses the gradient's own dtype; a bfloat16 gradient upcast for this oracle passes bfloat16's eps).
+    rd (optional, e.g. round_bf16) rounds the operands of every product and the stored intermediates at the points
+    where bf16-operand kernels round them (see precondition_rounded, procrustes_step2_rounded); None computes in the
+    working dtype throughout, as the reference does."""
     eps = torch.finfo(G.dtype).eps if grad_eps is None else grad_eps
     numel = G.numel()
     damp = damping + eps * G.abs()
     noise = draws.normal(G.shape, noise_dtype or draw_dtype).to(G.dtype)
-    Pg = precondition(Q, G + damp * noise)
+    Pg = precondition(Q, G + damp * noise) if rd is None else precondition_rounded(Q, G + damp * noise, rd, True)
     for i, q in enumerate(Q):
         if q.dim() < 2:
             term1 = gram(Pg, i, dense=False)
             term2 = numel / max(q.numel(), 1)
             ell = term1.amax() + term2
-            L[i].copy_(torch.maximum(betaL * L[i] + (1 - betaL) * ell, ell))
+            L[i].copy_(smoothness_ema(L[i], ell, betaL))
             q.mul_(1 - lr / L[i] * (term1 - term2))
         else:
             d = q.shape[0]
             term1 = gram(Pg, i, dense=True)
             term2 = numel / d
             V1 = draws.normal((K_SUBSPACE, d), draw_dtype).to(q.dtype)
+            if rd is not None:
+                term1, V1 = rd(term1), rd(V1)
             ell = norm_lower_bound(term1, V1, skew=False) + term2
-            L[i].copy_(torch.maximum(betaL * L[i] + (1 - betaL) * ell, ell))
-            q.sub_(lr / L[i] * (term1 @ q - term2 * q))
+            L[i].copy_(smoothness_ema(L[i], ell, betaL))
+            q.sub_(lr / L[i] * (term1 @ (q if rd is None else rd(q)) - term2 * q))
             V2 = draws.normal((K_SUBSPACE, d), draw_dtype).to(q.dtype)
-            a = (procrustes_step_r2 if r2 else procrustes_step2)(q, V2)
+            if rd is None:
+                a = (procrustes_step_r2 if r2 else procrustes_step2)(q, V2)
+            else:
+                a = (procrustes_step_r2_rounded if r2 else procrustes_step2_rounded)(q, rd(V2), rd)
             if trace is not None:
                 trace.append(dict(factor=i, ell=float(ell), L=float(L[i]), a=float(a)))
     if draws.coin() < BALANCE_PROB:
@@ -223,13 +297,15 @@ def clip_and_update(param, g, lr_params, max_avg_amp=2.0, max_element_amp=10.0):
 class OracleKron:
     """KronWhiten.step of psgd_pro.py:251-384 on the CPU with the gradients passed in (no closure), for 0-D, 1-D,
     2-D and higher-order parameters. `pre` keeps the unclipped preconditioned gradients of the last step,
-    `clipped` the clipped ones."""
+    `clipped` the clipped ones. rounding=round_bf16 gives the floor a bf16-operand implementation cannot beat: the
+    same step with every product's operands rounded to bfloat16 where those kernels round them (its distance from
+    the float32 oracle measures what bf16 operands alone cost)."""
 
     def __init__(self, params, preconditioner_max_size=math.inf, preconditioner_max_skew=1.0,
                  preconditioner_init_scale=None, lr_params=0.001, lr_preconditioner=0.1, betaL=0.9, damping=1e-9,
                  momentum=0.0, grad_clip_max_amps=(2.0, 10.0), preconditioner_update_probability=1.0,
                  update_preconditioner_first=True, whiten_grad=True, seed=0, dtype=None, grad_eps=None, r2=False,
-                 noise_dtype=None):
+                 noise_dtype=None, rounding=None):
         self.params = list(params)  # updated in place
         self.max_size, self.max_skew = preconditioner_max_size, preconditioner_max_skew
         self.lr_params, self.lr_preconditioner = lr_params, lr_preconditioner
@@ -242,6 +318,7 @@ class OracleKron:
         self.dtype = dtype
         self.grad_eps, self.r2 = grad_eps, r2
         self.noise_dtype = noise_dtype
+        self.rounding = rounding  # e.g. round_bf16: operands rounded where bf16-operand kernels round them
         self.draws = Draws(seed)
         self.Q = self.L = None
         self.ms, self.counter_m = None, 0
@@ -260,7 +337,7 @@ class OracleKron:
         for Q, L, g in zip(self.Q, self.L, srcs):
             update_preconditioner(Q, L, g, self.draws, lr=self.lr_preconditioner, betaL=self.betaL,
                                   damping=self.damping, grad_eps=self.grad_eps, r2=self.r2, trace=self.trace,
-                                  noise_dtype=self.noise_dtype)
+                                  noise_dtype=self.noise_dtype, rd=self.rounding)
 
     @torch.no_grad()
     def step(self, grads):
@@ -270,7 +347,7 @@ class OracleKron:
         if self.Q is None:
             self._init(grads, init_scale_on_the_fly(grads, self.damping))
         if self.momentum > 0:  # psgd_pro.py:334-343
-            beta = min(self.counter_m / (1 + self.counter_m), self.momentum)
+            beta = momentum_beta(self.counter_m, self.momentum)
             self.counter_m += 1
             if self.ms is None:
                 self.ms = [torch.zeros_like(g) for g in grads]
@@ -282,7 +359,8 @@ class OracleKron:
         src = grads if self.whiten_grad else self.ms
         if upd and self.update_first:
             self._update(src)
-        self.pre = [precondition(Q, m) for Q, m in zip(self.Q, self.ms if self.momentum > 0 else grads)]
+        pc = precondition if self.rounding is None else (lambda Q, m: precondition_rounded(Q, m, self.rounding, False))
+        self.pre = [pc(Q, m) for Q, m in zip(self.Q, self.ms if self.momentum > 0 else grads)]
         if upd and not self.update_first:
             self._update(src)
         max_avg, max_el = self.grad_clip_max_amps

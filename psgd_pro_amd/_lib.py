@@ -56,6 +56,7 @@ _SIGS = {
     "psgdk_syrk": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vp]),
     "psgdk_symm": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vpa, _i64, _vp]),
     "psgdk_trmm": (_i32, [_i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vpa, _i64, _vp]),
+    "psgdk_trmm_ws": (_i32, [_i32, _i64, _i64, _i32, _i32, _vpa, _i64, _vpa, _i64, _vpa, _i64, _vp, _szp, _vp]),
     "psgdk_gemm": (_i32, [_i32, _i32, _i32, _i64, _i64, _i64, _f, _i32, _i32, _i32, _vpa, _i64, _vpa, _i64, _f,
                           _vpa, _i64, _vp]),
     "psgdk_tri_rownorm2": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
@@ -77,6 +78,7 @@ _SIGS = {
     "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
     "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),
     "psgdk_set_option": (_i32, [_i32, _i32]),
+    "psgdk_get_option": (_i32, [_i32, C.POINTER(C.c_int)]),
     "psgdk_profile_start": (_i32, []),
     "psgdk_profile_stop": (_i32, [C.POINTER(ProfRecord), _i32, C.POINTER(C.c_int)]),
     "psgdk_debug_mfma": (_i32, [_i32, _vp, _vp, _vp, _vp]),

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -18,6 +19,7 @@
 namespace psgdk {
 hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
+int set_error(int code, const char* msg);  // for entry points defined in other source files
 }  // namespace psgdk
 
 using namespace psgdk;
@@ -106,7 +108,7 @@ struct ProfRec {
   double flops;
   hipEvent_t a, b;
 };
-struct Prof {
+struct Prof {  // one per host thread: a thread's records cover its own launches
   bool on = false;
   std::vector<ProfRec> recs;
   std::vector<hipEvent_t> pool;
@@ -116,7 +118,8 @@ struct Prof {
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
   }
-} g_prof;
+};
+thread_local Prof g_prof;
 
 // Instantiation id of gemm_kernel<PREC, TA, TB, tile config>: cfg * 1000 + prec * 100 + adt * 10 + bdt.
 int kernel_id(int prec, int adt, int bdt, int cfg) { return cfg * 1000 + prec * 100 + adt * 10 + bdt; }
@@ -204,24 +207,33 @@ struct B16Out {
   int64_t ldc = 0, ldcb = 0, ldct = 0;
 };
 
-int g_tile_order = 2;  // psgdk_set_option 0: 0 problem-major, 1 XCD-contiguous runs, 2 runs + grouped rows
-int g_force_cfg = -1;  // psgdk_set_option 1: -1 by size, else the bf16 kernel's tile config
-int g_nlb_target = 1024;  // psgdk_set_option 2: workgroups per full-storage V A product (split-K target)
-int g_vmm_u = 4;          // psgdk_set_option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
-int g_vmm_cols = -1;      // psgdk_set_option 4: V A kernel: -1 by shape (2 where the layout holds, else 0),
-                          // 0 split-K + reduce, 1 column blocks, 2 column blocks with A staged through LDS
-int g_t1q_pg = 1;         // psgdk_set_option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
-int g_upd_streams = 3;    // psgdk_set_option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
-int g_rq16 = 1;           // psgdk_set_option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
-int g_f32kc = 1;          // psgdk_set_option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
+// Tuning options (psgdk_set_option): one set per host thread, so that a thread's settings never change another
+// thread's results.
+thread_local int g_tile_order = 2;  // option 0: 0 problem-major, 1 XCD-contiguous runs, 2 runs + grouped rows
+thread_local int g_force_cfg = -1;  // option 1: -1 by size, else the bf16 kernel's tile config
+thread_local int g_nlb_target = 1024;  // option 2: workgroups per full-storage V A product (split-K target)
+thread_local int g_vmm_u = 4;          // option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
+thread_local int g_vmm_cols = -1;      // option 4: V A kernel: -1 by shape (2 where the layout holds, else 0),
+                                       // 0 split-K + reduce, 1 column blocks, 2 column blocks with A staged in LDS
+thread_local int g_t1q_pg = 1;  // option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
+thread_local int g_upd_streams = 3;  // option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
+thread_local int g_rq16 = 1;   // option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
+thread_local int g_f32kc = 1;  // option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
-// side stream, so it stays ordered with the caller's other work and can be captured into a HIP graph.
+// side stream, so it stays ordered with the caller's other work. The table is shared by every host thread: a call
+// holds side_stream_mutex() from its fork to its join, so concurrent calls from several threads queue their side
+// work one call after the other instead of mixing their events.
 struct SideStreams {
   std::vector<hipStream_t> s;
   std::vector<hipEvent_t> ev;  // 1 fork + per side stream 2 (phase join, final join)
 };
+std::mutex& side_stream_mutex() {
+  static std::mutex m;
+  return m;
+}
+// Caller holds side_stream_mutex().
 int side_streams(int n, SideStreams** out) {
   static std::vector<SideStreams> per_dev;
   int dev = 0;
@@ -270,9 +282,10 @@ bool b16_operands_ok(int nb, int64_t M, int64_t N, int64_t K, P const* A, int64_
 }
 
 // The k-contiguous kernel on bf16 (esz 2) or fp32 (esz 4) operands.
+// kbeg: A is upper-triangular with its zeros stored; each tile starts its k loop at its first row (TRMM).
 int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64_t lda, const void* const* B,
             int64_t ldb, const B16Out& o, const EpiSpec& e, int tri, int out_mode, int* ntiles, hipStream_t st,
-            int esz = 2, bool amc = false, bool bmc = false) {
+            int esz = 2, bool amc = false, bool bmc = false, int kbeg = 0) {
   if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb, esz, amc, tri ? amc : bmc))
     return fail(PSGDK_EINVAL, "k-contiguous kernel operand contract violated (K, leading dimensions, alignment or size)");
   GB16Args a;
@@ -282,6 +295,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   a.alpha = e.alpha; a.epi = e.epi; a.tri = tri; a.out_mode = out_mode; a.nb = nb;
   a.vec = g_tile_order;
   a.amc = amc; a.bmc = tri ? amc : bmc;
+  a.kbeg = kbeg;
   for (int b = 0; b < nb; ++b) {
     a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
     a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
@@ -297,7 +311,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   r.kernel_id = (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
-  r.flops = tri ? (double)M * (M + 1) * K * nb : 2.0 * M * N * K * nb;
+  r.flops = tri ? (double)M * (M + 1) * K * nb : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * K * nb;
   r.a = g_prof.ev();
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
@@ -1045,7 +1059,9 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   PSGDK_HIP(hipStreamIsCapturing(st, &cap), "capture status");
   const int S = cap != hipStreamCaptureStatusNone ? 1 : std::min<int>(g_upd_streams, std::max<int>(ng, (int)batches.size()));
   SideStreams* ss = nullptr;
+  std::unique_lock<std::mutex> ss_lock;
   if (S > 1) {
+    ss_lock = std::unique_lock<std::mutex>(side_stream_mutex());
     PSGDK_TRY(side_streams(S, &ss));
     PSGDK_HIP(hipEventRecord(ss->ev[0], st), "fork");
     for (int i = 0; i < S; ++i) PSGDK_HIP(hipStreamWaitEvent(ss->s[i], ss->ev[0], 0), "fork wait");
@@ -1422,6 +1438,8 @@ int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* co
 
 }  // namespace
 
+int psgdk::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
 // ==============================================================================================================
 extern "C" {
 
@@ -1490,6 +1508,64 @@ int psgdk_symm(int prec, int side, int sign, int64_t n, int64_t p, int b_dtype, 
 int psgdk_trmm(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
                const void* const* B, int64_t ldb, float* const* C, int64_t ldc, psgdk_stream_t stream) {
   return psgdk_symm(prec, 0, 0, n, p, b_dtype, nb, Q, ldq, B, ldb, C, ldc, stream);
+}
+
+int psgdk_trmm_ws(int prec, int64_t n, int64_t p, int b_dtype, int nb, const float* const* Q, int64_t ldq,
+                  const void* const* B, int64_t ldb, float* const* C, int64_t ldc, void* ws, size_t* ws_bytes,
+                  psgdk_stream_t stream) {
+  PSGDK_TRY(check_nb(nb));
+  PSGDK_TRY(check_prec(prec));
+  PSGDK_TRY(check_dt(b_dtype, "B"));
+  PSGDK_TRY(check_dims(n, "n"));
+  PSGDK_TRY(check_dims(p, "p"));
+  if (!ws_bytes) return fail(PSGDK_EINVAL, "ws_bytes is null");
+  if (ldq < n || ldb < p || ldc < p) return fail(PSGDK_ESHAPE, "leading dimension too small");
+  // The k-contiguous kernel with the triangle's k range: bf16 takes bf16 copies of triu(Q) (zeros below the
+  // diagonal) and of B^T; fp32 takes an fp32 copy of triu(Q) and reads B as it is (n-contiguous rows of k).
+  const bool bf = prec == PSGDK_PREC_BF16;
+  const bool fast = (bf ? (n % 8 == 0 && p % 8 == 0) : (b_dtype == PSGDK_F32 && n % 4 == 0 && p % 4 == 0 && n > 32 &&
+                                                        g_f32kc && (ldb * 4) % 16 == 0)) &&
+                    n * n * 4 < ((int64_t)1 << 31) && n * p * 4 < ((int64_t)1 << 31);
+  Ws w(ws);
+  void *Qc[MAXB], *Bt[MAXB];
+  for (int b = 0; b < nb; ++b) {
+    Qc[b] = fast ? (bf ? (void*)w.take<bf16_t>(n * n) : (void*)w.take<float>(n * n)) : nullptr;
+    Bt[b] = fast && bf ? (void*)w.take<bf16_t>(p * n) : nullptr;
+  }
+  if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
+  if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  PSGDK_TRY(check_ptrs(Q, nb, "Q"));
+  PSGDK_TRY(check_ptrs(B, nb, "B"));
+  PSGDK_TRY(check_ptrs(C, nb, "C"));
+  bool b_aligned = true;  // the fp32 route reads B in place
+  for (int b = 0; b < nb; ++b) b_aligned = b_aligned && aligned16(B[b]);
+  if (!fast || (!bf && !b_aligned)) return psgdk_trmm(prec, n, p, b_dtype, nb, Q, ldq, B, ldb, C, ldc, stream);
+  hipStream_t st = (hipStream_t)stream;
+  {  // triu(Q), zeros below the diagonal (never read there)
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = n; a.n = n; a.ld = ldq; a.dt = PSGDK_F32; a.i1 = 1;
+    for (int b = 0; b < nb; ++b) {
+      a.in[b] = Q[b];
+      if (bf) a.out2[b] = Qc[b];
+      else a.out[b] = static_cast<float*>(Qc[b]);
+    }
+    PSGDK_HIP(to_bf16_launch(a, st), "triu(Q) copy");
+  }
+  if (bf) {  // B^T in bf16 (p x n)
+    EwArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.nb = nb; a.m = p; a.n = n; a.ld = ldb; a.dt = b_dtype; a.i0 = 1;
+    for (int b = 0; b < nb; ++b) { a.in[b] = B[b]; a.out2[b] = Bt[b]; }
+    PSGDK_HIP(to_bf16_launch(a, st), "B^T to bf16");
+  }
+  B16Out o;
+  o.ldc = ldc;
+  const void *Ac[MAXB], *Bc[MAXB];
+  for (int b = 0; b < nb; ++b) { o.C[b] = C[b]; Ac[b] = Qc[b]; Bc[b] = bf ? (const void*)Bt[b] : B[b]; }
+  EpiSpec e;
+  if (bf) return run_b16(nb, n, p, n, Ac, n, Bc, n, o, e, 0, 0, nullptr, st, 2, false, false, 1);
+  return run_b16(nb, n, p, n, Ac, n, Bc, ldb, o, e, 0, 0, nullptr, st, 4, false, true, 1);
 }
 
 int psgdk_gemm(int prec, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, int a_dtype,
@@ -1972,7 +2048,11 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
 }
 
 int psgdk_set_option(int option, int value) {
-  if (option == 0) { g_tile_order = value; return PSGDK_OK; }
+  if (option == 0) {
+    if (value < 0 || value > 2) return fail(PSGDK_EINVAL, "option 0 (bf16 tile order) must be 0 .. 2");
+    g_tile_order = value;
+    return PSGDK_OK;
+  }
   if (option == 1) {
     if (value < -1 || value > 2) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 2");
     g_force_cfg = value;
@@ -2014,6 +2094,15 @@ int psgdk_set_option(int option, int value) {
     return PSGDK_OK;
   }
   return fail(PSGDK_EINVAL, "unknown option %d", option);
+}
+
+int psgdk_get_option(int option, int* value) {
+  if (!value) return fail(PSGDK_EINVAL, "value is null");
+  const int* opts[] = {&g_tile_order, &g_force_cfg, &g_nlb_target, &g_vmm_u, &g_vmm_cols,
+                       &g_t1q_pg,     &g_upd_streams, &g_rq16,     &g_f32kc};
+  if (option < 0 || option >= (int)(sizeof opts / sizeof opts[0])) return fail(PSGDK_EINVAL, "unknown option %d", option);
+  *value = *opts[option];
+  return PSGDK_OK;
 }
 
 int psgdk_profile_start(void) {

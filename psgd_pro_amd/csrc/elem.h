@@ -59,8 +59,9 @@ hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
 hipError_t sumsq_launch(const EwArgs& a, hipStream_t st);
 // full symmetric matrix from the packed upper triangle
 hipError_t unpack_launch(const EwArgs& a, hipStream_t st);
-// bf16 copy (i0 = 0) or bf16 transposed copy (i0 = 1) of an fp32 matrix into out2 (m x n, leading dimension n); with
-// out set, the fp32 copy into out
+// bf16 copy (i0 = 0) or bf16 transposed copy (i0 = 1) of an fp32 (dt 0) or bf16 (dt 1) matrix with leading dimension
+// ld into out2 (m x n, leading dimension n); with out set, the fp32 copy into out. i1 = 1 (with i0 = 0): the upper
+// triangle only, zeros written below the diagonal without reading the input there
 hipError_t to_bf16_launch(const EwArgs& a, hipStream_t st);
 
 }  // namespace psgdk

@@ -538,6 +538,13 @@ hipError_t diag_update_launch(const EwArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Clamp to [-amp, amp] with torch.clamp's semantics (psgd_pro.py:380): NaN stays NaN (fminf / fmaxf would replace
+// it by a bound), +-inf goes to the bound.
+__device__ __forceinline__ float clamp_keep_nan(float x, float amp) { return x < -amp ? -amp : (x > amp ? amp : x); }
+
+// pre -> clip -> param update (psgd_pro.py:371-381): RMS from the sum-of-squares partials; rescale by amp / RMS when
+// RMS > amp (a NaN RMS does not rescale, an inf RMS rescales by 0, as the reference's comparison and multiply do),
+// then the elementwise clamp.
 // in = param (dtype dt, m*n), in2 = pre (fp32), in3 = sum-of-squares partials (value at [2 t], i0 partials),
 // out2 (optional) = the clipped gradient. f0 = max average amplitude, f1 = max element amplitude, f2 = lr.
 __global__ void __launch_bounds__(EW_THREADS) clip_update_kernel(const EwArgs a, int blocks_per) {
@@ -564,7 +571,7 @@ __global__ void __launch_bounds__(EW_THREADS) clip_update_kernel(const EwArgs a,
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (scale) g[e] *= sc;
-        g[e] = fminf(fmaxf(g[e], -a.f1), a.f1);
+        g[e] = clamp_keep_nan(g[e], a.f1);
         w[e] = w[e] - a.f2 * g[e];
       }
       if (gout) ew_store8(gout + 8 * v, g);
@@ -577,7 +584,7 @@ __global__ void __launch_bounds__(EW_THREADS) clip_update_kernel(const EwArgs a,
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     float g = pre[i];
     if (scale) g *= sc;
-    g = fminf(fmaxf(g, -a.f1), a.f1);
+    g = clamp_keep_nan(g, a.f1);
     if (gout) gout[i] = g;
     if (a.dt) {
       bf16_t* p = reinterpret_cast<bf16_t*>(prm);
@@ -747,7 +754,10 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
   const int TM = (int)((a.m + 63) / 64), TN = (int)((a.n + 63) / 64);
   const int b = blockIdx.x / (TM * TN), tile = blockIdx.x % (TM * TN);
   const int I = tile / TN, J = tile % TN;  // output tile (rows I, cols J)
-  const float* __restrict__ X = reinterpret_cast<const float*>(a.in[b]);
+  const void* __restrict__ X = a.in[b];
+  auto xat = [&](long long idx) {
+    return a.dt ? bf16_to_f32(reinterpret_cast<const bf16_t*>(X)[idx]) : reinterpret_cast<const float*>(X)[idx];
+  };
   bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
   float* __restrict__ Yf = a.out[b];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -755,8 +765,9 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
     for (int r = ty; r < 64; r += 4) {
       const long long gi = (long long)I * 64 + r, gj = (long long)J * 64 + tx;
       if (gi < a.m && gj < a.n) {
-        if (Yf) Yf[gi * a.n + gj] = X[gi * a.ld + gj];
-        else Y[gi * a.n + gj] = f32_to_bf16(X[gi * a.ld + gj]);
+        const float v = a.i1 && gj < gi ? 0.f : xat(gi * a.ld + gj);  // i1: the strict lower part is not read
+        if (Yf) Yf[gi * a.n + gj] = v;
+        else Y[gi * a.n + gj] = f32_to_bf16(v);
       }
     }
     return;
@@ -764,7 +775,7 @@ __global__ void __launch_bounds__(256) to_bf16_kernel(const EwArgs a) {
   // transposed: output (gi, gj) = in (gj, gi); load in rows J-block, cols I-block
   for (int r = ty; r < 64; r += 4) {
     const long long si = (long long)J * 64 + r, sj = (long long)I * 64 + tx;
-    t[r][tx] = (si < a.n && sj < a.m) ? X[si * a.ld + sj] : 0.f;
+    t[r][tx] = (si < a.n && sj < a.m) ? xat(si * a.ld + sj) : 0.f;
   }
   __syncthreads();
   for (int r = ty; r < 64; r += 4) {

@@ -18,6 +18,8 @@ struct GB16Args {
   int vec;            // 0: problem-major order (WG id = tile); 1: tiles dealt to XCDs in contiguous runs; 2: as 1,
                       // with tile rows grouped by 4 inside each problem
   int amc, bmc;       // fp32 kernel: A / B stored m- / n-contiguous (rows of the buffer are k; M / N a multiple of 4)
+  int kbeg;           // 1: A is upper-triangular (A[i][k] = 0 for k < i, zeros stored): a tile of rows m0.. starts its
+                      // k loop at the k tile holding m0 (TRMM)
   const bf16_t* A[MAXB];
   const bf16_t* B[MAXB];
   float* C[MAXB];

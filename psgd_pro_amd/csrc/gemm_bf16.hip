@@ -167,7 +167,10 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     for (int j = 0; j < FN; ++j) acc[i][j] = part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto& dst = BLK ? part : acc;  // the MFMA accumulators of the main loop
 
-  const int nk = (p.K + BK - 1) / BK;
+  // k tiles of this output tile: all of K, or (kbeg: A upper-triangular, zero left of the tile's first row) from the
+  // k tile holding m0; kb is the k origin of the first one
+  const int kfirst = p.kbeg ? m0 / BK : 0, kb = kfirst * BK;
+  const int nk = (p.K + BK - 1) / BK - kfirst;
   // fp32 operands may be stored m- / n-contiguous (amc, bmc: the buffer's rows are k)
   constexpr bool amc = (LAY & 1) != 0, bmc = (LAY & 2) != 0;  // a SYRK (B = A) has both bits or neither
   static_assert(LAY == 0 || std::is_same_v<T, float>, "m/n-contiguous operands: fp32 only");
@@ -262,13 +265,13 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       if constexpr (bmc) lb.store_mc(bs, tid);
       else lb.store(bs, tid);
     };
-    load(0);
+    load(kb);
     store(As0, Bs0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
       const bool more = kt + 1 < nk;
-      if (more) load((kt + 1) * BK);
+      if (more) load(kb + (kt + 1) * BK);
       mma_tile(As0 + cur * BM * KP, Bs0 + cur * BN * KP);
       if constexpr (BLK) {
         if ((kt + 1) % KC_TILES == 0 || !more) {
@@ -301,19 +304,19 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * CE) * (long long)sizeof(T));
     Ld<T, BM / 2, NT / 2> la;
     Ld<T, BN / 2, NT / 2> lb;
-    la.load(rsA, voffA, p.lda, m0, p.M, 0, p.K, t);
-    lb.load(rsB, voffB, p.ldb, n0, rowsB, 0, p.K, t);
+    la.load(rsA, voffA, p.lda, m0, p.M, kb, p.K, t);
+    lb.load(rsB, voffB, p.ldb, n0, rowsB, kb, p.K, t);
     la.store(As0, t);
     lb.store(Bs0, t);
-    la.load(rsA, voffA, p.lda, m0, p.M, BK, p.K, t);
-    lb.load(rsB, voffB, p.ldb, n0, rowsB, BK, p.K, t);
+    la.load(rsA, voffA, p.lda, m0, p.M, kb + BK, p.K, t);
+    lb.load(rsB, voffB, p.ldb, n0, rowsB, kb + BK, p.K, t);
     __syncthreads();
     auto memory = [&](int kt) {
       const int nxt = (kt + 1) & 1;
       la.store(As0 + nxt * BM * KP, t);
       lb.store(Bs0 + nxt * BN * KP, t);
-      la.load(rsA, voffA, p.lda, m0, p.M, (kt + 2) * BK, p.K, t);
-      lb.load(rsB, voffB, p.ldb, n0, rowsB, (kt + 2) * BK, p.K, t);
+      la.load(rsA, voffA, p.lda, m0, p.M, kb + (kt + 2) * BK, p.K, t);
+      lb.load(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 2) * BK, p.K, t);
     };
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
@@ -716,12 +719,10 @@ static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   void (*fn)(GB16Args) = nullptr;
   if constexpr (std::is_same_v<T, bf16_t>) fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
   else fn = gemm_f32kc_kernel<BM, BN, WGM, WGN, EPI, LAY>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  // once per instantiation (a function-local static is initialised once, also under concurrent first calls)
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (attr != hipSuccess) return attr;
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;

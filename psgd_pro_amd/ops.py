@@ -18,7 +18,18 @@ from torch.library import custom_op
 
 from . import _lib as L
 
-_WS = L.Workspace()
+_WS = {}
+
+
+def _ws(t):
+    """The workspace of t's device and its current stream. Calls on one stream run in order, so they share one
+    buffer; calls on another stream get their own, and a buffer that grows goes back to torch's caching allocator on
+    the one stream that used it."""
+    key = (t.device, torch.cuda.current_stream(t.device).cuda_stream)
+    w = _WS.get(key)
+    if w is None:
+        w = _WS[key] = L.Workspace()
+    return w
 
 
 def _prec(bf16):
@@ -103,8 +114,8 @@ def trmm(Q: Tensor, B: Tensor, bf16: bool) -> Tensor:
     B = _as_2d(B, "B")
     n, p = Q.shape[0], B.shape[1]
     C = torch.empty(n, p, device=B.device, dtype=torch.float32)
-    L.check(L.lib().psgdk_trmm(_prec(bf16), n, p, L.dtype_code(B.dtype), 1, L.ptrs([Q]), Q.stride(0), L.ptrs([B]),
-                               B.stride(0), L.ptrs([C]), p, L.stream_of(B)))
+    L.call_ws(L.lib().psgdk_trmm_ws, _prec(bf16), n, p, L.dtype_code(B.dtype), 1, L.ptrs([Q]), Q.stride(0),
+              L.ptrs([B]), B.stride(0), L.ptrs([C]), p, ws=_ws(B), device=B.device, stream=L.stream_of(B))
     return C
 
 
@@ -144,7 +155,7 @@ def tri_rownorm2(A: Tensor, sign: int) -> tuple[Tensor, Tensor]:
     rn2 = torch.empty(n, device=A.device, dtype=torch.float32)
     amax = torch.empty((), device=A.device, dtype=torch.float32)
     L.call_ws(L.lib().psgdk_tri_rownorm2, n, sign, 1, L.ptrs([A]), A.stride(0), L.ptrs([rn2]), L.ptrs([amax]),
-              ws=_WS, device=A.device, stream=L.stream_of(A))
+              ws=_ws(A), device=A.device, stream=L.stream_of(A))
     return rn2, amax
 
 
@@ -163,7 +174,7 @@ def tri_vmm(V: Tensor, A: Tensor, sign: int) -> Tensor:
     if V.shape != (L.NLB_K, n):
         raise RuntimeError(f"V: expected shape ({L.NLB_K}, {n}), got {tuple(V.shape)}")
     W = torch.empty_like(V)
-    L.call_ws(L.lib().psgdk_tri_vmm, n, sign, 1, L.ptrs([V]), L.ptrs([A]), A.stride(0), L.ptrs([W]), ws=_WS,
+    L.call_ws(L.lib().psgdk_tri_vmm, n, sign, 1, L.ptrs([V]), L.ptrs([A]), A.stride(0), L.ptrs([W]), ws=_ws(A),
               device=A.device, stream=L.stream_of(A))
     return W
 
@@ -185,7 +196,7 @@ def norm_lower_bound(A: Tensor, V: Tensor, sign: int) -> Tensor:
         raise RuntimeError(f"V: expected shape ({L.NLB_K}, {n}), got {tuple(V.shape)}")
     out = torch.empty((), device=A.device, dtype=torch.float32)
     L.call_ws(L.lib().psgdk_norm_lower_bound, n, sign, 1, L.ptrs([A]), A.stride(0), L.ptrs([V]), L.ptrs([out]),
-              ws=_WS, device=A.device, stream=L.stream_of(A))
+              ws=_ws(A), device=A.device, stream=L.stream_of(A))
     return out
 
 

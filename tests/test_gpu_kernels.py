@@ -146,11 +146,33 @@ def test_symm_reads_only_the_upper_triangle(hip, n, p, sign, prec):
 @pytest.mark.parametrize("n,p", [(256, 256), (200, 77), (512, 512)])
 @pytest.mark.parametrize("prec", [0, 1])
 def test_trmm(hip, n, p, prec):
+    """triu(Q) B through psgdk_trmm_ws (the k-contiguous kernel with the triangle's k range where the shape allows,
+    psgdk_trmm otherwise: 200 x 77) and psgdk_trmm itself, Q's strict lower triangle NaN-poisoned."""
     Q = rnd(n, n, seed=3)
     B = rnd(n, p, seed=4)
-    C = K.trmm(poison_lower(Q).to(DEV), B.to(DEV), bool(prec))
+    Qd, Bd = poison_lower(Q).to(DEV), B.to(DEV)
+    C = K.trmm(Qd, Bd, bool(prec))
     Q64 = torch.triu((bf(Q) if prec else Q).double())
-    check_gemm_bound(C, Q64, (bf(B) if prec else B).double())
+    B64 = (bf(B) if prec else B).double()
+    check_gemm_bound(C, Q64, B64)
+    C2 = torch.empty(n, p, device=DEV)
+    L.check(hip.psgdk_trmm(prec, n, p, 0, 1, L.ptrs([Qd]), n, L.ptrs([Bd]), p, L.ptrs([C2]), p, L.stream_of(Bd)))
+    check_gemm_bound(C2, Q64, B64)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_trmm_ws_grouped_and_bf16_b(hip, prec):
+    """psgdk_trmm_ws on a group of 3 problems with leading dimensions wider than the matrices, B in bf16 storage."""
+    n, p, nb = 264, 136, 3
+    Qs = [poison_lower(rnd(n, n + 8, seed=i)[:, :n]).contiguous() for i in range(nb)]
+    Qf = [torch.cat([q, torch.zeros(n, 8)], 1).to(DEV) for q in Qs]  # ldq = n + 8
+    Bs = [rnd(n, p + 8, seed=10 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]  # ldb = p + 8
+    Cs = [torch.empty(n, p + 16, device=DEV) for _ in range(nb)]  # ldc = p + 16
+    L.call_ws(hip.psgdk_trmm_ws, prec, n, p, 1, nb, L.ptrs(Qf), n + 8, L.ptrs(Bs), p + 8, L.ptrs(Cs), p + 16,
+              ws=L.Workspace(), device=Qf[0].device, stream=L.stream_of(Qf[0]))
+    for q, b, c in zip(Qs, Bs, Cs):
+        Q64 = torch.triu((bf(q) if prec else q).double().nan_to_num(0.0))
+        check_gemm_bound(c[:, :p], Q64, b.float().cpu()[:, :p].double())
 
 
 # --------------------------------------------------------------------------------------------------------------
@@ -209,7 +231,7 @@ def nlb_full(As, Vs, sign):
     n = As[0].shape[0]
     outs = [torch.empty((), device=DEV, dtype=torch.float32) for _ in As]
     L.call_ws(L.lib().psgdk_norm_lower_bound_full, n, sign, len(As), L.ptrs(As), As[0].stride(0),
-              L.dtype_code(As[0].dtype), L.ptrs(Vs), L.ptrs(outs), ws=K._WS, device=As[0].device,
+              L.dtype_code(As[0].dtype), L.ptrs(Vs), L.ptrs(outs), ws=L.Workspace(), device=As[0].device,
               stream=L.stream_of(As[0]))
     return [float(o) for o in outs]
 
@@ -274,7 +296,7 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k, cols):
 
     def run():
         L.call_ws(L.lib().psgdk_norm_lower_bound_gram, d, k, len(Ps), L.ptrs(Pd), L.ptrs(Ptd), L.ptrs(Vd), L.ptrs(outs),
-                  ws=K._WS, device=Pd[0].device, stream=L.stream_of(Pd[0]))
+                  ws=L.Workspace(), device=Pd[0].device, stream=L.stream_of(Pd[0]))
         return [float(o) for o in outs]
     assert L.lib().psgdk_set_option(4, cols) == 0
     try:
@@ -330,7 +352,7 @@ def test_factor_update_matches_oracle(hip, d, tri, L0):
     Ld = [torch.full((1,), L0, device=DEV) for _ in range(2)]
     Vd = [v.to(DEV) for v in Vs]
     L.call_ws(L.lib().psgdk_factor_update, 0, d, 2, L.ptrs(T1d), tri, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Ld),
-              L.ptrs(Vd), lr, betaL, term2, ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+              L.ptrs(Vd), lr, betaL, term2, ws=L.Workspace(), device=Qd[0].device, stream=L.stream_of(Qd[0]))
     for b in range(2):
         T, Q = T1s[b].double(), Qs[b].double()
         ell = float(norm_lower_bound(T, Vs[b].double(), skew=False)) + term2
@@ -352,7 +374,7 @@ def test_procrustes_matches_oracle(hip, d, prec):
     Qo = [torch.empty_like(q) for q in Qd]
     Vd = [v.to(DEV) for v in Vs]  # held until the kernels have run (a freed block can become the workspace)
     L.call_ws(L.lib().psgdk_procrustes, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Vd),
-              ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+              ws=L.Workspace(), device=Qd[0].device, stream=L.stream_of(Qd[0]))
     for b in range(2):
         ref = Qs[b].double().clone()
         procrustes_step2(ref, Vs[b].double())
@@ -372,7 +394,7 @@ def test_procrustes_r2_matches_oracle(hip, d, prec):
     Qo = [torch.empty_like(q) for q in Qd]
     Vd = [v.to(DEV) for v in Vs]  # held until the kernels have run (a freed block can become the workspace)
     L.call_ws(L.lib().psgdk_procrustes_r2, prec, d, 2, L.ptrs(Qd), L.ptrs(Qo), L.ptrs(Vd),
-              ws=K._WS, device=Qd[0].device, stream=L.stream_of(Qd[0]))
+              ws=L.Workspace(), device=Qd[0].device, stream=L.stream_of(Qd[0]))
     tol = 1e-5 if prec == 0 else 5e-3
     for b in range(2):
         ref = Qs[b].double().clone()
@@ -498,3 +520,26 @@ def test_syrk_bf16_k_contiguous(hip, b16cfg, nb, n, k):
         Cc = C.cpu()
         assert bool(torch.isnan(Cc[~triu]).all())
         check_gemm_bound(torch.where(triu, Cc, Cc.T), X, X.T)
+
+
+@pytest.mark.parametrize("n", [512, 1024, 2048, 4096])
+@pytest.mark.parametrize("prec", [0, 1], ids=["fp32", "bf16"])
+def test_microbench_cells(hip, n, prec):
+    """Every cell of the SYRK / TRMM microbenchmark as `bench.py --config syrk` runs it: C = triu(A A^T) with A n x n
+    (n = k) stored in the precision's dtype, one problem per call, against float64 with the strict lower triangle
+    left untouched; and triu(Q) B with fp32 Q (its strict lower triangle NaN-poisoned) and B, n x n."""
+    dt = torch.bfloat16 if prec else torch.float32
+    A = rnd(n, n, seed=n).to(dt)
+    Ad = A.to(DEV)
+    C = torch.full((n, n), float("nan"), device=DEV)
+    L.check(hip.psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, L.dtype_code(dt), 1, L.ptrs([Ad]), n, L.ptrs([C]), n,
+                           L.stream_of(Ad)))
+    triu = torch.ones(n, n, dtype=torch.bool).triu()
+    Cc = C.cpu()
+    assert bool(torch.isnan(Cc[~triu]).all())
+    X = A.double()
+    check_gemm_bound(torch.where(triu, Cc, Cc.T), X, X.T)
+    Q = rnd(n, n, seed=n + 1)
+    B = rnd(n, n, seed=n + 2)
+    Ct = K.trmm(poison_lower(Q).to(DEV), B.to(DEV), bool(prec))
+    check_gemm_bound(Ct, torch.triu((bf(Q) if prec else Q).double()), (bf(B) if prec else B).double())

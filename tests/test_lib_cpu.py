@@ -64,18 +64,72 @@ def test_argument_validation():
     assert lib.psgdk_symm(0, 0, 3, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
 
 
+DEFAULTS = {0: 2, 1: -1, 2: 1024, 3: 4, 4: -1, 5: 1, 6: 3, 7: 1, 8: 1}
+
+
+def _get(opt):
+    v = C.c_int(-99)
+    assert L.lib().psgdk_get_option(opt, C.byref(v)) == 0
+    return v.value
+
+
 def test_option_ranges():
     """psgdk_set_option accepts each option's documented values and refuses the rest (host state only)."""
     lib = L.lib()
-    for opt, good, bad in [(1, [-1, 0, 1, 2], [3, -2]), (3, [2, 4, 8], [1, 16]), (4, [-1, 0, 1, 2], [3]),
-                           (5, [0, 1], [2]), (6, [0, 3, 8], [9, -1]), (7, [0, 1], [2]), (8, [0, 1], [2])]:
-        for v in bad:
-            assert lib.psgdk_set_option(opt, v) == L.EINVAL, (opt, v)
-        for v in good:
-            assert lib.psgdk_set_option(opt, v) == 0, (opt, v)
-    for opt, v in [(1, -1), (3, 4), (4, -1), (5, 1), (6, 3), (7, 1), (8, 1)]:  # the defaults
-        assert lib.psgdk_set_option(opt, v) == 0
+    try:
+        for opt, good, bad in [(0, [0, 1, 2], [3, -1]), (1, [-1, 0, 1, 2], [3, -2]), (2, [1, 4096], [0, -5]),
+                               (3, [2, 4, 8], [1, 16]), (4, [-1, 0, 1, 2], [3]), (5, [0, 1], [2]),
+                               (6, [0, 3, 8], [9, -1]), (7, [0, 1], [2]), (8, [0, 1], [2])]:
+            for v in bad:
+                assert lib.psgdk_set_option(opt, v) == L.EINVAL, (opt, v)
+            for v in good:
+                assert lib.psgdk_set_option(opt, v) == 0, (opt, v)
+                assert _get(opt) == v
+    finally:
+        for opt, v in DEFAULTS.items():
+            assert lib.psgdk_set_option(opt, v) == 0
     assert lib.psgdk_set_option(99, 0) == L.EINVAL
+    v = C.c_int(0)
+    assert lib.psgdk_get_option(99, C.byref(v)) == L.EINVAL and lib.psgdk_get_option(0, None) == L.EINVAL
+
+
+def test_options_and_errors_are_per_thread():
+    """Two host threads set different options, query workspace sizes (which depend on option 2) and trigger argument
+    errors at the same time: each sees its own options, sizes and error messages; a new thread starts from the
+    defaults; the main thread's options are untouched."""
+    import threading
+    lib = L.lib()
+    barrier = threading.Barrier(2)
+    out = {}
+
+    def worker(tag, target, nb):
+        barrier.wait()
+        assert lib.psgdk_set_option(2, target) == 0
+        assert lib.psgdk_set_option(1, 1 if tag == "a" else 0) == 0
+        sizes, errs = [], []
+        for _ in range(200):
+            sz = C.c_size_t(0)
+            assert lib.psgdk_norm_lower_bound_full(3072, 1, nb, None, 3072, 1, None, None, None, C.byref(sz),
+                                                   None) == 0
+            sizes.append(sz.value)
+            assert lib.psgdk_syrk(0, 0, 1, 64, 64, 0, 17 + nb, L.ptrs([0x1000]), 64, L.ptrs([0x1000]), 64,
+                                  None) == L.EINVAL
+            errs.append(lib.psgdk_last_error().decode())
+            barrier.wait()
+        out[tag] = (set(sizes), set(errs), _get(2), _get(1))
+
+    ta = threading.Thread(target=worker, args=("a", 64, 2))
+    tb = threading.Thread(target=worker, args=("b", 4096, 3))
+    ta.start(); tb.start(); ta.join(); tb.join()
+    (sa, ea, oa2, oa1), (sb, eb, ob2, ob1) = out["a"], out["b"]
+    assert len(sa) == 1 and len(sb) == 1 and sa != sb
+    assert ea == {"nb = 19: must be in 1..16"} and eb == {"nb = 20: must be in 1..16"}
+    assert (oa2, oa1, ob2, ob1) == (64, 1, 4096, 0)
+    assert all(_get(o) == v for o, v in DEFAULTS.items())
+    fresh = {}
+    t = threading.Thread(target=lambda: fresh.update({o: _get(o) for o in DEFAULTS}))
+    t.start(); t.join()
+    assert fresh == DEFAULTS
 
 
 def test_factor_step_entry_points_reject_aliasing_without_device_work():

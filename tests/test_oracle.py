@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import psgd_oracle as O
-from tests.metrics import rel_err_norm
+from tests.metrics import rel_err_floor, rel_err_norm
 
 torch.set_default_dtype(torch.float32)
 
@@ -287,3 +287,209 @@ def test_flops_formula():
     shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
     assert 12 * sum(O.flops_2d(m, n) for m, n in shapes) / 1e12 == pytest.approx(7.7236, rel=1e-4)
     assert O.flops_2d(1024, 1024) / 1e9 == pytest.approx(26.852, rel=1e-4)
+
+
+# --------------------------------------------------------------------------- closed forms of the step's remaining rules
+# Each check below is also run against the oracle with a planted mistake (a swapped betaL / 1 - betaL, a flipped
+# sign, the other update order), which it must reject: a check that a slip shared by two restatements passes pins
+# nothing.
+def _noised(G, N, damping):
+    return G + (damping + torch.finfo(G.dtype).eps * G.abs()) * N
+
+
+def _diag_first_step_err(seed=4, lr=0.1, damping=1e-9, oracle_lr=None):
+    """Both factors diagonal (12 x 10 with max_skew 0.5: 144, 100 > 60), q = ones, L = 0. The first update is
+    Pg = X, term1_0 = rowsum(X^2), term1_1 = colsum(X^2), ell_i = max term1_i + numel / d_i, L_i = ell_i and
+    q_i = 1 - (lr / ell_i)(term1_i - numel / d_i) (psgd_pro.py:126-130). Returns the worst relative error of the
+    oracle's q and L against that closed form."""
+    m, n = 12, 10
+    G = torch.randn(m, n, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+    W = torch.zeros(m, n, dtype=torch.float64)
+    ora = O.OracleKron([W], preconditioner_max_skew=0.5, preconditioner_init_scale=1.0, seed=seed,
+                       lr_preconditioner=oracle_lr if oracle_lr is not None else lr, damping=damping,
+                       dtype=torch.float64, grad_clip_max_amps=(1e9, 1e9))
+    ora.step([G])
+    assert ora.Q[0][0].dim() == 1 and ora.Q[0][1].dim() == 1
+    gen = torch.Generator().manual_seed(seed)
+    torch.rand([], generator=gen)
+    X = _noised(G, torch.randn(m, n, generator=gen, dtype=torch.float32).double(), damping)
+    err = 0.0
+    for i, (t1, d) in enumerate((((X * X).sum(1), m), ((X * X).sum(0), n))):
+        t2 = m * n / d
+        ell = float(t1.max()) + t2
+        q = 1.0 - lr / ell * (t1 - t2)
+        err = max(err, rel_err_norm(ora.Q[0][i], q), abs(float(ora.L[0][i]) - ell) / ell)
+    return err
+
+
+def test_diag_factor_first_step_closed_form():
+    assert _diag_first_step_err() < 1e-13
+    assert _diag_first_step_err(oracle_lr=-0.1) > 1e-3  # planted: the update's sign flipped
+
+
+def _second_step_err(betaL_oracle=0.9, shape=(12, 10), skew=0.5, lr=0.1, seed=6):
+    """Step 1 on a random gradient, then step 2 on G = 0 with damping 0: X = 0, so Pg = 0, term1 = 0 and the norm
+    bound of the zero matrix is 0, hence ell = numel / d for every factor. L_1 = ell_1 > numel / d, so the EMA takes
+    its first branch, L_2 = betaL L_1 + (1 - betaL) numel / d (psgd_pro.py:129,134), and the update scales the
+    factor: q_2 = q_1 (1 + lr (numel / d) / L_2) for diagonal (psgd_pro.py:130) and dense factors (psgd_pro.py:135;
+    Q_1 is symmetric up to rounding, the Procrustes fixed point). betaL 0.9 throughout; betaL_oracle plants a
+    swap."""
+    beta = 0.9
+    G = torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+    W = torch.zeros(shape, dtype=torch.float64)
+    ora = O.OracleKron([W], preconditioner_max_skew=skew, preconditioner_init_scale=1.0, seed=seed,
+                       betaL=betaL_oracle, lr_preconditioner=lr, dtype=torch.float64, grad_clip_max_amps=(1e9, 1e9))
+    ora.step([G])
+    L1 = [float(l) for l in ora.L[0]]
+    Q1 = [q.clone() for q in ora.Q[0]]
+    ora.damping = 0.0
+    ora.step([torch.zeros(shape, dtype=torch.float64)])
+    err = 0.0
+    numel = math.prod(shape)
+    for i, d in enumerate(shape):
+        t2 = numel / d
+        assert L1[i] > t2 * (1 + 1e-6)
+        L2 = beta * L1[i] + (1 - beta) * t2
+        err = max(err, abs(float(ora.L[0][i]) - L2) / L2,
+                  rel_err_norm(ora.Q[0][i], Q1[i] * (1 + lr * t2 / L2)))
+    return err
+
+
+@pytest.mark.parametrize("shape,skew", [((12, 10), 0.5), ((6, 9), math.inf)], ids=["diag", "dense"])
+def test_smoothness_ema_second_step_closed_form(shape, skew):
+    assert _second_step_err(shape=shape, skew=skew) < 1e-12
+    assert _second_step_err(betaL_oracle=0.1, shape=shape, skew=skew) > 1e-3  # planted: betaL and 1 - betaL swapped
+
+
+def test_smoothness_ema_planted_swap_in_the_rule(monkeypatch):
+    """The same closed form against the oracle whose EMA rule itself has betaL and 1 - betaL swapped."""
+    monkeypatch.setattr(O, "smoothness_ema", lambda L, ell, b: torch.maximum((1 - b) * L + b * ell, ell))
+    assert _second_step_err() > 1e-3
+
+
+def _momentum_err(steps=12, momentum=0.9):
+    """momentum 0.9 with no preconditioner update (probability 0) from Q = I: the buffer after step t is
+    m_t = beta_t m_{t-1} + (1 - beta_t) g_t with beta_t = min((t - 1) / t, 0.9) (psgd_pro.py:334-341), i.e. the
+    running mean of g_1..g_t for t <= 10, then 0.9 m_{t-1} + 0.1 g_t; the preconditioned gradient is m_t itself
+    (P = I) and the parameter moves by -lr m_t (no clipping at this scale). Returns the worst relative error."""
+    shape = (5, 7)
+    gen = torch.Generator().manual_seed(2)
+    gs = [0.01 * torch.randn(shape, generator=gen, dtype=torch.float64) for _ in range(steps)]
+    W = torch.zeros(shape, dtype=torch.float64)
+    ora = O.OracleKron([W], preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, momentum=momentum,
+                       preconditioner_update_probability=0.0, lr_params=0.5, dtype=torch.float64, seed=1)
+    err, Wref, mref = 0.0, torch.zeros(shape, dtype=torch.float64), None
+    for t, g in enumerate(gs, start=1):
+        ora.step([g])
+        mref = torch.stack(gs[:t]).mean(0) if t <= 10 else 0.9 * mref + 0.1 * g
+        Wref = Wref - 0.5 * mref
+        err = max(err, rel_err_norm(ora.ms[0], mref), rel_err_norm(ora.pre[0], mref), rel_err_norm(W, Wref))
+    return err
+
+
+def test_momentum_closed_form():
+    assert _momentum_err() < 1e-13
+
+
+def test_momentum_planted_swap(monkeypatch):
+    """The oracle with m = (1 - beta) m + beta g (beta and 1 - beta swapped) fails the closed form."""
+    monkeypatch.setattr(O, "momentum_beta", lambda c, mo: 1 - min(c / (1 + c), mo))
+    assert _momentum_err() > 1e-3
+
+
+def _first_step_dense(G, seed, lr=0.1, damping=1e-9):
+    """Closed-form Q_1, Q_2 and L after one optimizer step of a 2-D weight with two dense factors from Q = I,
+    replaying OracleKron's draws (update coin, noise, then per factor the SPD and skew starts)."""
+    m, n = G.shape
+    gen = torch.Generator().manual_seed(seed)
+    torch.rand([], generator=gen)
+    X = _noised(G, torch.randn(m, n, generator=gen, dtype=torch.float32).double(), damping)
+    Qs, Ls = [], []
+    for i, d in enumerate((m, n)):
+        T = X @ X.T if i == 0 else X.T @ X
+        T = (T + T.T) / 2
+        V1 = torch.randn(32, d, generator=gen, dtype=torch.float32).double()
+        torch.randn(32, d, generator=gen, dtype=torch.float32)
+        ell = float(O.norm_lower_bound(T, V1, skew=False)) + m * n / d
+        Qs.append(torch.eye(d, dtype=torch.float64) - lr / ell * (T - m * n / d * torch.eye(d, dtype=torch.float64)))
+        Ls.append(ell)
+    return Qs, Ls
+
+
+def _order_err(update_first_oracle, update_first_expected, seed=8):
+    """Two steps of a 6 x 9 weight with dense factors from Q = I. Update last (psgd_pro.py:363-369): step 1 applies
+    the identity preconditioner, pre_1 = G_1, and step 2 applies Q_1 (the closed-form first update), pre_2 =
+    Q_1a^T Q_1a G_2 Q_1b^T Q_1b. Update first: pre_1 = Q_1a^T Q_1a G_1 Q_1b^T Q_1b. W moves by -lr pre (no clipping
+    at this scale). Returns the worst relative error of pre and W against the expected order's closed form."""
+    m, n, lr = 6, 9, 0.01
+    gen = torch.Generator().manual_seed(seed)
+    G1 = 0.1 * torch.randn(m, n, generator=gen, dtype=torch.float64)
+    G2 = 0.1 * torch.randn(m, n, generator=gen, dtype=torch.float64)
+    W = torch.zeros(m, n, dtype=torch.float64)
+    ora = O.OracleKron([W], preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, seed=seed,
+                       lr_params=lr, dtype=torch.float64, update_preconditioner_first=update_first_oracle)
+    Qc, _ = _first_step_dense(G1, seed)
+    P = [q.T @ q for q in Qc]
+    ora.step([G1])
+    exp1 = P[0] @ G1 @ P[1] if update_first_expected else G1
+    err = max(rel_err_norm(ora.pre[0], exp1), rel_err_norm(W, -lr * exp1))
+    if not update_first_expected:
+        exp2 = P[0] @ G2 @ P[1]
+        ora.step([G2])
+        err = max(err, rel_err_norm(ora.pre[0], exp2), rel_err_norm(W, -lr * (exp1 + exp2)))
+    return err
+
+
+@pytest.mark.parametrize("first", [False, True], ids=["update_last", "update_first"])
+def test_update_order_closed_form(first):
+    assert _order_err(first, first) < 1e-12
+    assert _order_err(not first, first) > 1e-3  # planted: the other order
+
+
+def test_clip_passes_non_finite_values_through():
+    """psgd_pro.py:371-381 with torch semantics: a NaN element makes the RMS NaN, so no rescale, and the clamp
+    keeps the NaN (the parameter gets NaN there, the other elements their normal step); an inf element makes the
+    RMS inf, so the rescale multiplies by 2 / inf = 0 (inf * 0 = NaN at that element, 0 elsewhere)."""
+    g = torch.tensor([0.5, float("nan"), -30.0, 1.0])
+    p = torch.ones(4)
+    out = O.clip_and_update(p, g.clone(), 0.1, 2.0, 10.0)
+    assert math.isnan(float(out[1])) and math.isnan(float(p[1]))
+    assert torch.equal(out[[0, 2, 3]], torch.tensor([0.5, -10.0, 1.0]))
+    assert torch.allclose(p[[0, 2, 3]], torch.tensor([0.95, 2.0, 0.9]))
+    g = torch.tensor([0.5, float("inf"), -3.0, 1.0])
+    p = torch.ones(4)
+    out = O.clip_and_update(p, g.clone(), 0.1, 2.0, 10.0)
+    assert math.isnan(float(out[1])) and math.isnan(float(p[1]))
+    assert torch.equal(out[[0, 2, 3]], torch.zeros(3)) and torch.equal(p[[0, 2, 3]], torch.ones(3))
+
+
+# --------------------------------------------------------------------------- the rounded-operand oracle (bf16 floor)
+def _rounded_run(rounding, shapes=((24, 40), (40, 24), (16,)), skew=math.inf, steps=4, r2=False):
+    gen = torch.Generator().manual_seed(12)
+    W = [torch.zeros(s, dtype=torch.float64) for s in shapes]
+    ora = O.OracleKron(W, preconditioner_max_skew=skew, preconditioner_init_scale=1.0, seed=5, dtype=torch.float64,
+                       rounding=rounding, r2=r2)
+    for _ in range(steps):
+        ora.step([0.01 * torch.randn(s, generator=gen, dtype=torch.float64) for s in shapes])
+    return ora
+
+
+@pytest.mark.parametrize("skew", [math.inf, 1.0], ids=["dense", "mixed"])
+@pytest.mark.parametrize("r2", [False, True], ids=["step2", "r2"])
+def test_rounded_oracle_reduces_to_oracle_and_scales_with_unit_roundoff(skew, r2):
+    """With the identity as its rounding the rounded-operand oracle is the oracle (the same algebra, associated as
+    the bf16 kernels associate it); its distance from the oracle grows with the rounding's unit roundoff (float32:
+    ~1e-7, bfloat16: ~1e-3), so a rounding point that is missing or applied to the wrong operand shows up."""
+    base = _rounded_run(None, skew=skew, r2=r2)
+    ident = _rounded_run(lambda x: x, skew=skew, r2=r2)
+    f32 = _rounded_run(lambda x: x.float().double(), skew=skew, r2=r2)
+    b16 = _rounded_run(O.round_bf16, skew=skew, r2=r2)
+
+    def dist(o):  # per-element on Q (floor 1e-3 max), normwise on the preconditioned gradient
+        dq = max(max(rel_err_floor(q, qb) for q, qb in zip(Qa, Qb)) for Qa, Qb in zip(o.Q, base.Q))
+        return max(dq, max(rel_err_norm(a, b) for a, b in zip(o.pre, base.pre)))
+    assert dist(ident) < 1e-12
+    e32, e16 = dist(f32), dist(b16)
+    assert 1e-9 < e32 < 1e-6, e32
+    assert 1e-4 < e16 < 2e-2, e16
+    assert 1e3 < e16 / e32 < 1e6, (e16, e32)  # bf16 / fp32 unit roundoff = 2^16
