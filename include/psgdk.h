@@ -112,6 +112,17 @@ int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* 
                                 const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
                                 psgdk_stream_t stream);
 
+/* psgdk_norm_lower_bound_full without the workspace arguments, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Scratch comes from a static device array of PSGDK_NOALLOC_SCRATCH_MIB MiB that each GPU the library runs on holds
+ * until the process ends; a call allocates nothing. A problem whose workspace (the size psgdk_norm_lower_bound_full
+ * reports) exceeds the array is refused with PSGDK_ESHAPE (e.g. n = 3072 fits up to nb = 4 bf16 matrices). Every
+ * call on one GPU shares that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (two
+ * streams, or two host threads) race. */
+#define PSGDK_NOALLOC_SCRATCH_MIB 32
+int psgdk_norm_lower_bound_full_noalloc(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_dtype,
+                                        const float* const* V, float* const* out, psgdk_stream_t stream);
+
 /* norm_lower_bound_spd (psgd_pro.py:19-41) of P P^T (d x d) given P (d x k bf16, rows k-contiguous) and Pt = P^T
  * (k x d bf16), without forming P P^T: the squared row norms come from P (P^T P), the diagonal from the rows of P,
  * row j from P P_j^T, and each product V (P P^T) as (V P) P^T. The bound the bf16 update takes for term1 = Pg Pg^T

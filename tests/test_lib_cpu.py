@@ -132,6 +132,20 @@ def test_options_and_errors_are_per_thread():
     assert fresh == DEFAULTS
 
 
+def test_noalloc_norm_bound_refuses_oversized_problems_without_device_work():
+    """psgdk_norm_lower_bound_full_noalloc computes the workspace it needs before touching the device and refuses a
+    problem whose workspace exceeds its static scratch (PSGDK_NOALLOC_SCRATCH_MIB MiB), with a message."""
+    lib = L.lib()
+    limit = 32 << 20
+    sz = C.c_size_t(0)
+    assert lib.psgdk_norm_lower_bound_full(3072, 1, 16, None, 3072, 1, None, None, None, C.byref(sz), None) == 0
+    assert sz.value > limit
+    fake = L.ptrs([0x1000] * 16)
+    rc = lib.psgdk_norm_lower_bound_full_noalloc(3072, 1, 16, fake, 3072, 1, fake, fake, None)
+    assert rc == L.ESHAPE and "static scratch" in _err()
+    assert lib.psgdk_norm_lower_bound_full_noalloc(3072, 1, 0, fake, 3072, 1, fake, fake, None) == L.EINVAL
+
+
 def test_factor_step_entry_points_reject_aliasing_without_device_work():
     """psgdk_factor_update / psgdk_procrustes write Q_out from Q in one pass, so Q_out may not alias Q: refused
     after the size query and before any launch (fake device addresses are never touched)."""
