@@ -56,6 +56,8 @@ def parse_args():
                     help="bf16 GEMM tile configuration for every launch (library option 1; -1: chosen by size)")
     ap.add_argument("--upd-streams", type=int, default=3,
                     help="side streams of the grouped update inside the library (library option 6)")
+    ap.add_argument("--big-batch", type=int, default=64,
+                    help="items per batch of the grouped update for factor sides >= 2048 (library option 9)")
     ap.add_argument("--t1q-pg", type=int, default=1,
                     help="0: form term1 Q as the reference writes it, never through Pg (library option 5)")
     ap.add_argument("--r2", type=int, default=0,
@@ -185,6 +187,7 @@ def bench_vitb(args):
     L.check(L.lib().psgdk_set_option(7, args.rq16))
     L.check(L.lib().psgdk_set_option(4, args.vmm))
     L.check(L.lib().psgdk_set_option(8, args.f32kc))
+    L.check(L.lib().psgdk_set_option(9, args.big_batch))
     skew = math.inf if args.skew == "inf" else float(args.skew)
     shapes = VIT_B * args.blocks
     gen = torch.Generator().manual_seed(0)

@@ -286,7 +286,9 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * 1: everything on the caller's stream); option 7 = whether the bf16 update keeps R Q (the Procrustes correction)
  * in bf16 (1, default: only the bf16 (R Q)^T, which the Q update also reads) or fp32 (0) between its two
  * products; option 8 = whether fp32 products with k- or m/n-contiguous operands (M > 32, one k range, no packed
- * output) take the k-contiguous kernel's fp32 twin (1, default) or the general engine (0). */
+ * output) take the k-contiguous kernel's fp32 twin (1, default) or the general engine (0); option 9 = the most
+ * factors of one side >= 2048 that psgdk_kron2d_update_groups batches into one launch (1 .. 64, default 64; smaller
+ * batches of one side run on different side streams). */
 int psgdk_set_option(int option, int value);
 /* The calling thread's value of a psgdk_set_option switch. */
 int psgdk_get_option(int option, int* value);

@@ -219,6 +219,7 @@ thread_local int g_t1q_pg = 1;  // option 5: bf16 update forms term1 Q through P
 thread_local int g_upd_streams = 3;  // option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
 thread_local int g_rq16 = 1;   // option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
 thread_local int g_f32kc = 1;  // option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
+thread_local int g_big_batch = MAXB;  // option 9: items per batch of the grouped update for factor sides >= 2048
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -1040,7 +1041,8 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   for (size_t i = 0; i < order.size();) {
     std::vector<B16Item*> bt;
     const int64_t d = order[i]->d;
-    while (i < order.size() && order[i]->d == d && (int)bt.size() < MAXB) bt.push_back(order[i++]);
+    const int cap = d >= 2048 ? std::min(g_big_batch, MAXB) : MAXB;
+    while (i < order.size() && order[i]->d == d && (int)bt.size() < cap) bt.push_back(order[i++]);
     batches.push_back(bt);
   }
   std::vector<NlbWs> nws(batches.size());
@@ -2088,6 +2090,11 @@ int psgdk_set_option(int option, int value) {
     g_rq16 = value;
     return PSGDK_OK;
   }
+  if (option == 9) {
+    if (value < 1 || value > MAXB) return fail(PSGDK_EINVAL, "option 9 (items per large-side batch) must be 1 .. %d", MAXB);
+    g_big_batch = value;
+    return PSGDK_OK;
+  }
   if (option == 6) {
     if (value < 0 || value > 8) return fail(PSGDK_EINVAL, "option 6 (grouped update side streams) must be 0 .. 8");
     g_upd_streams = value;
@@ -2098,8 +2105,8 @@ int psgdk_set_option(int option, int value) {
 
 int psgdk_get_option(int option, int* value) {
   if (!value) return fail(PSGDK_EINVAL, "value is null");
-  const int* opts[] = {&g_tile_order, &g_force_cfg, &g_nlb_target, &g_vmm_u, &g_vmm_cols,
-                       &g_t1q_pg,     &g_upd_streams, &g_rq16,     &g_f32kc};
+  const int* opts[] = {&g_tile_order, &g_force_cfg,   &g_nlb_target, &g_vmm_u, &g_vmm_cols,
+                       &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch};
   if (option < 0 || option >= (int)(sizeof opts / sizeof opts[0])) return fail(PSGDK_EINVAL, "unknown option %d", option);
   *value = *opts[option];
   return PSGDK_OK;

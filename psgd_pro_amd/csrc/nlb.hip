@@ -336,6 +336,13 @@ __device__ __forceinline__ void store8(float* dst, const float (&x)[8]) {
   reinterpret_cast<float4*>(dst)[0] = make_float4(x[0], x[1], x[2], x[3]);
   reinterpret_cast<float4*>(dst)[1] = make_float4(x[4], x[5], x[6], x[7]);
 }
+__device__ __forceinline__ void store4(bf16_t* dst, const float (&x)[4]) {
+  *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(f32_to_bf16(x[0]), f32_to_bf16(x[1])),
+                                              pack2(f32_to_bf16(x[2]), f32_to_bf16(x[3])));
+}
+__device__ __forceinline__ void store4(float* dst, const float (&x)[4]) {
+  *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+}
 
 // One workgroup per (matrix, row r of V): argmax of rn2 (first maximum), nf = max diagonal (SPD) or max |A|
 // (skew) + smallest normal, then V0[r] = a_j + sgn(<a_j, V_r>) V_r with a_j = row j of A / nf (psgd_pro.py:25-33,
@@ -804,23 +811,25 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
 // The product of vmm_cols_kernel with A staged through LDS: the workgroup's 64 rows of A are read in chunks of
 // 64 rows x 512 bytes (256 bf16 or 128 fp32 of k), each row's 512 bytes by 32 consecutive lanes (row-contiguous
 // runs, as a row-norm pass reads them; the MFMA fragment layout would read 64-byte pieces of 16 rows per load),
-// stored with a 528-byte row pitch (16 fragment rows land on 16 distinct 16-byte bank groups) and read back as MFMA
-// fragments. Wave w multiplies the k quarter w of every chunk (2 MFMA steps, V fragments straight from global
-// memory; fp32: four 16x16x4 MFMAs per fragment pair, element s of every lane's piece at k = kk + 4 g + s for both
-// operands); the next chunk's A and V loads are in flight while a chunk is multiplied. The four waves' partial
-// blocks are summed through LDS in the fixed order w = 0..3 and the epilogue is vmm_cols_kernel's.
+// stored in unpadded 512-byte rows whose 16-byte pieces are XOR-swizzled by the row (piece p of row r at
+// p ^ (r % 16): the 16 fragment rows of a read land on 16 distinct 16-byte bank groups, and the 32 lanes writing
+// one row still cover its 32 slots) and read back as MFMA fragments. Wave w multiplies the k quarter w of every
+// chunk (2 MFMA steps, V fragments straight from global memory; fp32: four 16x16x4 MFMAs per fragment pair,
+// element s of every lane's piece at k = kk + 4 g + s for both operands); the next chunk's A and V loads are in
+// flight while a chunk is multiplied. The four waves' partial blocks are summed through LDS in the fixed order
+// w = 0..3, 16 rows of W at a time, and each row is scaled, stored and its sum of squares (of this column block)
+// written. The 32 KB of LDS (the staging buffer, which the epilogue reuses) let five workgroups share a CU, so the
+// 1152 workgroups of 24 matrices of 3072 columns run in one round.
 // grid: nb * ceil(n / 64).
 constexpr int VR_ROWB = 512;                   // bytes of one row per chunk
-constexpr int VR_PITCH = VR_ROWB + 16;         // LDS row pitch in bytes
-constexpr int VR_SMEM = VMC * VR_PITCH > 4 * NLB_K * VMC_LD * 4 ? VMC * VR_PITCH : 4 * NLB_K * VMC_LD * 4;
+constexpr int VR_SMEM = VMC * VR_ROWB;         // the staging buffer: 64 rows x 512 bytes
+static_assert(4 * 16 * VMC_LD * 4 + NLB_K * 4 <= VR_SMEM, "epilogue blocks and row scales fit in the staging buffer");
 
 template <typename T>
 __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int normalize) {
   constexpr int CE = 16 / sizeof(T);          // elements per 16-byte piece
   constexpr int VRK = VR_ROWB / sizeof(T);    // k per chunk
-  constexpr int VR_LD = VR_PITCH / sizeof(T);  // LDS row pitch (elements)
   constexpr int KS = 4 * CE;                  // k per MFMA step
-  __shared__ float rs[NLB_K];
   __shared__ __attribute__((aligned(16))) unsigned char sm[VR_SMEM];
   T* const As = reinterpret_cast<T*>(sm);
   const int n = p.n, nbk = (n + VMC - 1) / VMC;
@@ -831,7 +840,8 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
   const int c0 = cb * VMC;
   const T* __restrict__ A = reinterpret_cast<const T*>(p.A[b]);
   const T* __restrict__ V = reinterpret_cast<const T*>(p.Vin[b]);
-  if (tid < NLB_K) rs[tid] = p.plain ? 1.f : vmm_row_scale(p, b, tid, nbk, normalize);
+  // the row scale of V row tid (threads < 32), kept in a register until the epilogue
+  const float my_rs = tid < NLB_K ? (p.plain ? 1.f : vmm_row_scale(p, b, tid, nbk, normalize)) : 0.f;
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, (long long)NLB_K * K * sizeof(T));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (long long)n * p.lda * sizeof(T));
   // A staging: thread t owns the 16-byte piece t % 32 of rows t / 32 + 8 i (i < 8) of the chunk
@@ -867,8 +877,10 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   load(0);
   for (int kc = 0; kc < K; kc += VRK) {
+    // row rr + 8 i has (rr + 8 i) % 16 = rr + 8 (i % 2)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(As + (rr + 8 * i) * VR_LD + pc * CE) = st[i];
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<uint4*>(As + (rr + 8 * i) * VRK + ((pc ^ (rr + 8 * (i & 1))) * CE)) = st[i];
     uint4 vc[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -878,10 +890,10 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     if (kc + VRK < K) load(kc + VRK);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int kl = wave * (VRK / 4) + s * KS + g * CE;
+      const int piece = wave * 8 + s * 4 + g;  // 16-byte piece of the row this lane's fragment reads
       uint4 af[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) af[j] = *reinterpret_cast<const uint4*>(As + (j * 16 + r16) * VR_LD + kl);
+      for (int j = 0; j < 4; ++j) af[j] = *reinterpret_cast<const uint4*>(As + (j * 16 + r16) * VRK + (piece ^ r16) * CE);
       if constexpr (sizeof(T) == 2) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -902,48 +914,50 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     }
     __syncthreads();
   }
-  // lane holds rows i*16 + 4g + e of columns j*16 + r16; the staging buffer is free after the loop's last barrier
-  float (*red)[NLB_K][VMC_LD] = reinterpret_cast<float (*)[NLB_K][VMC_LD]>(sm);
+  // Epilogue in the staging buffer (free after the loop's last barrier): rows 16 h .. 16 h + 15 of the four waves'
+  // partial blocks, then the row scales after them. Lane holds rows i * 16 + 4 g + e of columns j * 16 + r16.
+  float (*red)[16][VMC_LD] = reinterpret_cast<float (*)[16][VMC_LD]>(sm);
+  float* const rsl = reinterpret_cast<float*>(sm) + 4 * 16 * VMC_LD;
+  if (tid < NLB_K) rsl[tid] = my_rs;
+  const int lr = tid >> 4, cl = (tid & 15) * 4, col = c0 + cl;  // this thread: row lr of the half, 4 columns
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int h = 0; h < 2; ++h) {
+    if (h) __syncthreads();  // the first half's reads are done
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[wave][i * 16 + 4 * g + e][j * 16 + r16] = acc[i][j][e];
-  __syncthreads();
-  const int row = tid >> 3, cl = (tid & 7) * 8, col = c0 + cl;
-  float w[8];
+      for (int e = 0; e < 4; ++e) red[wave][4 * g + e][j * 16 + r16] = acc[h][j][e];
+    __syncthreads();
+    const int row = 16 * h + lr;
+    const float4 x0 = *reinterpret_cast<const float4*>(&red[0][lr][cl]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&red[1][lr][cl]);
+    const float4 x2 = *reinterpret_cast<const float4*>(&red[2][lr][cl]);
+    const float4 x3 = *reinterpret_cast<const float4*>(&red[3][lr][cl]);
+    float w[4] = {((x0.x + x1.x) + x2.x) + x3.x, ((x0.y + x1.y) + x2.y) + x3.y, ((x0.z + x1.z) + x2.z) + x3.z,
+                  ((x0.w + x1.w) + x2.w) + x3.w};
+    const float sc = rsl[row];
+    float sq = 0.f;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float4 x0 = *reinterpret_cast<const float4*>(&red[0][row][cl + 4 * h]);
-    const float4 x1 = *reinterpret_cast<const float4*>(&red[1][row][cl + 4 * h]);
-    const float4 x2 = *reinterpret_cast<const float4*>(&red[2][row][cl + 4 * h]);
-    const float4 x3 = *reinterpret_cast<const float4*>(&red[3][row][cl + 4 * h]);
-    w[4 * h + 0] = ((x0.x + x1.x) + x2.x) + x3.x;
-    w[4 * h + 1] = ((x0.y + x1.y) + x2.y) + x3.y;
-    w[4 * h + 2] = ((x0.z + x1.z) + x2.z) + x3.z;
-    w[4 * h + 3] = ((x0.w + x1.w) + x2.w) + x3.w;
-  }
-  const float sc = rs[row];
-  float sq = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      w[e] *= sc;
+      if (col + e < n) sq += w[e] * w[e];
+    }
+    T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
+    if (col + 4 <= n) {
+      store4(W, w);
+    } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    w[e] *= sc;
-    if (col + e < n) sq += w[e] * w[e];
+      for (int e = 0; e < 4; ++e)
+        if (col + e < n) W[e] = from_f32<T>(w[e]);
+    }
+    if (!p.plain) {
+      sq += __shfl_xor(sq, 1, 64);
+      sq += __shfl_xor(sq, 2, 64);
+      sq += __shfl_xor(sq, 4, 64);
+      sq += __shfl_xor(sq, 8, 64);
+      if ((tid & 15) == 0) p.ssout[b][row * nbk + cb] = sq;
+    }
   }
-  T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
-  if (col + 8 <= n) {
-    store8(W, w);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (col + e < n) W[e] = from_f32<T>(w[e]);
-  }
-  if (p.plain) return;
-  sq += __shfl_xor(sq, 1, 64);
-  sq += __shfl_xor(sq, 2, 64);
-  sq += __shfl_xor(sq, 4, 64);
-  if ((tid & 7) == 0) p.ssout[b][row * nbk + cb] = sq;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
