@@ -9,6 +9,7 @@ MFMA path (fp32 accumulate). Synthetic data; weights random-initialised.
 
     python bench.py [--steps K] [--warmup W] [--precision bf16|fp32] [--skew inf|1] [--no-cpu]
     python bench.py --config syrk      # SYRK / TRMM microbenchmark lines (n = k in 512..4096, fp32 and bf16)
+    python bench.py --config ceiling   # hipBLASLt against the library's bf16 GEMM on the optimizer's shapes
 
 `roofline` is measured live: every MFMA-engine launch in the timed steps is bracketed by HIP events on its stream;
 the dominant kernel instantiation (largest total time) is reported with its algorithmic TFLOP/s against the bf16
@@ -40,7 +41,7 @@ def parse_args():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--skew", default="inf")
     ap.add_argument("--blocks", type=int, default=12)
-    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e"], default="vitb")
+    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e", "ceiling"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
@@ -81,33 +82,52 @@ def read_traffic(kernel):
     return b if (k == kernel and b is not None) else None
 
 
-def aggregate(recs):
-    """Per kernel instantiation: launches, total ms, total algorithmic flops; plus the SYRK subset."""
+PEAK_HBM = 8.0  # TB/s, MI355X HBM3E
+
+
+def roof_ms(fl, by, peak):
+    """The roofline model's time for a launch: its flops at the MFMA peak or its algorithmic bytes at the HBM peak,
+    whichever takes longer (ms)."""
+    return max(fl / (peak * 1e12), by / (PEAK_HBM * 1e12)) * 1e3
+
+
+def aggregate(recs, peak):
+    """Per kernel instantiation: launches, total ms, algorithmic flops and bytes, roofline-model ms; plus the SYRK
+    subset."""
     agg, syrk = {}, {}
-    for kid, tri, nb, ms, fl in recs:
-        a = agg.setdefault(kid, [0, 0.0, 0.0])
-        a[0] += 1
-        a[1] += ms
-        a[2] += fl
-        if tri:
-            s = syrk.setdefault(kid, [0, 0.0, 0.0])
-            s[0] += 1
-            s[1] += ms
-            s[2] += fl
+    for kid, tri, nb, ms, fl, by in recs:
+        for d in (agg, syrk) if tri else (agg,):
+            a = d.setdefault(kid, [0, 0.0, 0.0, 0.0, 0.0])
+            a[0] += 1
+            a[1] += ms
+            a[2] += fl
+            a[3] += by
+            a[4] += roof_ms(fl, by, peak)
     return agg, syrk
 
 
-def launch_classes(recs, steps, top=12):
-    """The most expensive (kernel, problems, flops per launch) classes of MFMA launches, per step."""
+def launch_classes(recs, steps, peak, top=12):
+    """The most expensive (kernel, problems, flops per launch) classes of MFMA launches, per step, each against its
+    own roof: its arithmetic intensity (algorithmic flops / algorithmic bytes) against the ridge (MFMA peak / HBM
+    peak) says whether the MFMA peak or the HBM peak bounds it, and roof_frac is the roofline model's time over the
+    measured time."""
     agg = {}
-    for kid, tri, nb, ms, fl in recs:
-        a = agg.setdefault((kid, tri, nb, round(fl)), [0, 0.0])
+    for kid, tri, nb, ms, fl, by in recs:
+        a = agg.setdefault((kid, tri, nb, round(fl), round(by)), [0, 0.0])
         a[0] += 1
         a[1] += ms
     rows = sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]
-    return [{"kernel": k[0], "syrk": bool(k[1]), "nb": k[2], "gflop": round(k[3] / 1e9, 2),
-             "launches_per_step": v[0] / steps, "us": round(v[1] * 1e3 / v[0], 1),
-             "tflops": round(k[3] / (v[1] / v[0] * 1e-3) / 1e12, 1)} for k, v in rows]
+    out = []
+    for k, v in rows:
+        us = v[1] * 1e3 / v[0]
+        ai = k[3] / k[4]
+        out.append({"kernel": k[0], "syrk": bool(k[1]), "nb": k[2], "gflop": round(k[3] / 1e9, 2),
+                    "gbyte": round(k[4] / 1e9, 3), "flop_per_byte": round(ai, 1),
+                    "bound": "mfma" if ai >= peak / PEAK_HBM else "hbm",
+                    "launches_per_step": v[0] / steps, "us": round(us, 1),
+                    "tflops": round(k[3] / (us * 1e-6) / 1e12, 1), "tbps": round(k[4] / (us * 1e-6) / 1e12, 2),
+                    "roof_frac": round(roof_ms(k[3], k[4], peak) * 1e3 / us, 3)})
+    return out
 
 
 def cpu_threads():
@@ -227,16 +247,20 @@ def bench_vitb(args):
     recs = L.profile_stop()
     opt._nstreams = args.streams
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
-    agg, syrk = aggregate(recs)
+    peak = PEAK[args.precision]
+    agg, syrk = aggregate(recs, peak)
     kid = max(agg, key=lambda k: agg[k][1])
-    n_l, ms_tot, fl_tot = agg[kid]
+    n_l, ms_tot, fl_tot, by_tot, roof_tot = agg[kid]
     prec_of = "bf16" if (kid >= 5000 or (kid % 1000) // 100 == 1) else "fp32"
-    achieved = fl_tot / (ms_tot * 1e-3) / 1e12
+    ai = fl_tot / by_tot
+    mfma_bound = ai >= PEAK[prec_of] / PEAK_HBM
+    achieved = fl_tot / (ms_tot * 1e-3) / 1e12 if mfma_bound else by_tot / (ms_tot * 1e-3) / 1e9
     kname = L.kernel_name(kid)
     traffic = read_traffic(kname)
     s_l = sum(v[0] for v in syrk.values())
     s_ms = sum(v[1] for v in syrk.values())
     s_fl = sum(v[2] for v in syrk.values())
+    s_roof = sum(v[4] for v in syrk.values())
     syrk_tf = s_fl / (s_ms * 1e-3) / 1e12 if s_ms else 0.0
     mfma_ms = sum(v[1] for v in agg.values()) / args.steps
     mfma_fl = sum(v[2] for v in agg.values()) / args.steps  # flops the MFMA launches execute (their own shapes)
@@ -270,15 +294,20 @@ def bench_vitb(args):
         "executed_mfma_tflop_per_step": round(mfma_fl / 1e12, 4),
         "executed_tflops": round(mfma_fl / (wall_ms * 1e-3) / 1e12, 2),
         "syrk": {"tflops": round(syrk_tf, 2), "frac": round(syrk_tf / PEAK[args.precision], 4),
+                 "roof_frac": round(s_roof / s_ms, 4) if s_ms else None,
                  "launches_per_step": s_l / args.steps, "ms_per_step": round(s_ms / args.steps, 3)},
-        "roofline": {"bound": "mfma", "kernel": kname, "launches_per_step": n_l / args.steps,
+        "roofline": {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname, "launches_per_step": n_l / args.steps,
                      "avg_launch_us": round(ms_tot * 1e3 / n_l, 2),
-                     "flops_per_launch": fl_tot / n_l,
-                     "achieved": round(achieved, 2), "peak": PEAK[prec_of], "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK[prec_of], 4), "traffic": traffic},
-        "launch_classes": launch_classes(recs, args.steps),
+                     "flops_per_launch": fl_tot / n_l, "algorithmic_bytes_per_launch": by_tot / n_l,
+                     "flop_per_byte": round(ai, 1), "ridge_flop_per_byte": round(PEAK[prec_of] / PEAK_HBM, 1),
+                     "achieved": round(achieved, 2), "peak": PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3,
+                     "unit": "TFLOP/s" if mfma_bound else "GB/s",
+                     "frac": round(achieved / (PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3), 4),
+                     "roof_frac": round(roof_tot / ms_tot, 4), "traffic": traffic},
+        "launch_classes": launch_classes(recs, args.steps, peak),
         "kernels": {L.kernel_name(k): {"launches_per_step": v[0] / args.steps, "ms_per_step": round(v[1] / args.steps, 3),
-                                       "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2)} for k, v in agg.items()},
+                                       "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2),
+                                       "roof_frac": round(v[4] / v[1], 4)} for k, v in agg.items()},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.precision, skew, args.cpu_seconds)
@@ -393,7 +422,7 @@ def bench_llama(args):
                                             "max_size": 16384, "max_skew": "inf", "streams": args.streams},
             "algorithmic_tflop_per_step": round(flops_step / 1e12, 3),
             "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2),
-            "launch_classes": launch_classes(recs, 2, top=8)}
+            "launch_classes": launch_classes(recs, 2, PEAK[args.precision], top=8)}
 
 
 def _vit(dim=512, depth=6, heads=8, dim_head=64, mlp=1024, patch=4, image=32, classes=10):
@@ -494,6 +523,45 @@ def bench_e2e(args):
                        "max_skew": 2, "momentum": 0.9, "streams": args.streams, "graphs": bool(args.graphs)}}
 
 
+def bench_ceiling(args):
+    """The bf16 GEMM ceiling of this GPU at the optimizer's shapes: hipBLASLt (torch.matmul, bf16 output) against
+    the library's k-contiguous kernel (fp32 output) on the same operands; back-to-back launches between events."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    dev = torch.device("cuda:0")
+    st = L.stream_of(torch.empty(1, device=dev))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def timeit(fn, reps=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps * 1e3
+    lines = []
+    for nb, m, n, k in [(12, 3072, 3072, 3072), (16, 3072, 3072, 3072), (12, 768, 3072, 3072), (12, 768, 2304, 2304),
+                        (1, 4096, 14336, 4096), (1, 8192, 8192, 8192), (1, 16384, 16384, 8192)]:
+        A = torch.randn(nb, m, k, device=dev).to(torch.bfloat16)
+        B = torch.randn(nb, n, k, device=dev).to(torch.bfloat16)
+        Bt = B.transpose(1, 2).contiguous()  # k x n, as torch.matmul takes it
+        C = torch.empty(nb, m, n, device=dev)
+        fl = 2.0 * nb * m * n * k
+        t_blas = timeit(lambda: torch.matmul(A, Bt))
+        t_ours = timeit(lambda: L.check(L.lib().psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(list(A)), k,
+                                                           L.ptrs(list(B)), k, 0.0, L.ptrs(list(C)), n, st)))
+        lines.append({"op": "gemm_bf16", "nb": nb, "m": m, "n": n, "k": k,
+                      "hipblaslt_us": round(t_blas, 1), "hipblaslt_tflops": round(fl / t_blas / 1e6, 1),
+                      "psgdk_us": round(t_ours, 1), "psgdk_tflops": round(fl / t_ours / 1e6, 1),
+                      "psgdk_over_hipblaslt": round(t_blas / t_ours, 3), "peak": PEAK["bf16"]})
+        del A, B, Bt, C
+        torch.cuda.empty_cache()
+    return lines
+
+
 def bench_copy(args):
     """Calibration for the HBM counters: one device-to-device copy of 256 MiB (read 256 MiB, write 256 MiB)."""
     import torch
@@ -528,6 +596,10 @@ def main():
         return
     if args.config == "syrk":
         for ln in bench_syrk(args):
+            print(json.dumps(ln), flush=True)
+        return
+    if args.config == "ceiling":
+        for ln in bench_ceiling(args):
             print(json.dumps(ln), flush=True)
         return
     print(json.dumps(bench_vitb(args)), flush=True)

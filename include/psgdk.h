@@ -26,7 +26,7 @@ extern "C" {
 
 typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
 
-#define PSGDK_VERSION 1
+#define PSGDK_VERSION 2
 #define PSGDK_MAXB 16 /* problems per grouped call */
 #define PSGDK_MAX_GROUPS 64 /* groups per psgdk_kron2d_update_groups call */
 #define PSGDK_NLB_K 32 /* rows of the random start of the norm lower bounds */
@@ -259,14 +259,15 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
  * (general engine: cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype, cfg 0 = 128 x 128 tiles, 1 = 32 x 128;
  * bf16 engine: 5000 + cfg * 10 + epilogue, cfg 0 = 256 x 256 tiles on 8 waves, 1 = 128 x 128 on 4, 2 = 256 x 256
  * on 4), whether it was a
- * SYRK (triangular grid), the problems in the launch, its device time and its algorithmic flop count
- * (SYRK n(n+1)k, TRMM n(n+1)p, GEMM 2mnk, per problem). With out NULL only *n_records is set (records kept). */
+ * SYRK (triangular grid), the problems in the launch, its device time, its algorithmic flop count (SYRK n(n+1)k,
+ * TRMM n(n+1)p, GEMM 2mnk, per problem) and its algorithmic bytes (operands read once, outputs written once). With out NULL only *n_records is set (records kept). */
 typedef struct psgdk_prof_record {
   int32_t kernel_id;
   int32_t tri;
   int32_t nb;
   float ms;
   double flops;
+  double bytes; /* algorithmic HBM bytes: each operand read once, each output written once, epilogue reads */
 } psgdk_prof_record_t;
 int psgdk_profile_start(void);
 int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);

@@ -47,7 +47,7 @@ class ApplyOpts(C.Structure):
 
 class ProfRecord(C.Structure):
     _fields_ = [("kernel_id", C.c_int32), ("tri", C.c_int32), ("nb", C.c_int32), ("ms", C.c_float),
-                ("flops", C.c_double)]
+                ("flops", C.c_double), ("bytes", C.c_double)]
 
 
 _SIGS = {
@@ -167,12 +167,12 @@ def profile_start():
 
 
 def profile_stop():
-    """List of (kernel_id, tri, nb, ms, flops) for the launches since profile_start()."""
+    """List of (kernel_id, tri, nb, ms, flops, bytes) for the launches since profile_start()."""
     n = C.c_int(0)
     check(lib().psgdk_profile_stop(None, 0, C.byref(n)))
     arr = (ProfRecord * max(1, n.value))()
     check(lib().psgdk_profile_stop(arr, n.value, C.byref(n)))
-    return [(r.kernel_id, r.tri, r.nb, r.ms, r.flops) for r in arr[:n.value]]
+    return [(r.kernel_id, r.tri, r.nb, r.ms, r.flops, r.bytes) for r in arr[:n.value]]
 
 
 def call_ws(fn, *args, ws, device, stream):

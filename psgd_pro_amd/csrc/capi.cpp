@@ -102,10 +102,10 @@ int check_dims(int64_t v, const char* name) {
 
 // ------------------------------------------------------------------------------------------------------------
 // Launch profiling (psgdk_profile_start / _stop): a HIP event pair around every MFMA-engine launch, recorded on the
-// launch's stream, with the launch's kernel instantiation and algorithmic flop count. Diagnostic; one thread.
+// launch's stream, with the launch's kernel instantiation and its algorithmic flop and byte counts. Diagnostic.
 struct ProfRec {
   int kernel_id, tri, nb;
-  double flops;
+  double flops, bytes;
   hipEvent_t a, b;
 };
 struct Prof {  // one per host thread: a thread's records cover its own launches
@@ -183,6 +183,17 @@ int run_gemm_general(int prec, int nb, int64_t M, int64_t N, int64_t K, const Op
   if (tri) r.flops = (double)M * (M + 1) * K * nb;                    // SYRK: n(n+1)k
   else if (kbeg_tri) r.flops = (double)M * (M + 1) * N * nb;         // TRMM: n(n+1)p
   else r.flops = 2.0 * M * N * K * nb;
+  {  // operands once (a triangle-read operand: its triangle), outputs once, epilogue reads and a beta read of C
+    auto opnd = [&](const Opnd& o, int64_t mn) {
+      const double el = o.mode == SYM ? (double)K * (K + 1) / 2 : (double)mn * K;
+      return el * (double)esize(o.dt);
+    };
+    const double out = tri ? (out_mode == PSGDK_OUT_MIRROR ? (double)M * M : (double)M * (M + 1) / 2) : (double)M * N;
+    double x = 0;
+    if (e.X1[0]) x += out;
+    if (e.X2[0]) x += out;
+    r.bytes = nb * (opnd(A, M) + (tri ? 0.0 : opnd(B, N)) + 4.0 * out * (1 + (e.beta != 0.f) + x / out));
+  }
   r.a = g_prof.ev();
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
@@ -313,6 +324,19 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   r.tri = tri;
   r.nb = nb;
   r.flops = tri ? (double)M * (M + 1) * K * nb : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * K * nb;
+  {  // operands once (kbeg: A's upper triangle), each output written once, each epilogue operand read once
+    const double out = tri ? (out_mode == PSGDK_OUT_MIRROR ? (double)M * M : (double)M * (M + 1) / 2) : (double)M * N;
+    const double a_el = kbeg ? (double)M * (M + 1) / 2 : (double)M * K;
+    double by = a_el * esz + (tri ? 0.0 : (double)N * K * esz);
+    if (o.C[0]) by += 4 * out;
+    if (o.Cb[0]) by += 2 * out;
+    if (o.CTb[0]) by += 2 * out;
+    if (o.CT[0]) by += 4 * out;
+    const int ep = e.epi;
+    if (e.X1[0]) by += (ep == EPI_RQ ? esz : 4) * out;  // EPI_RQ reads R in the operand type
+    if (e.X2[0]) by += (ep == EPI_PROCB ? 2 : 4) * out;  // EPI_PROCB reads the bf16 (R Q)^T
+    r.bytes = by * nb;
+  }
   r.a = g_prof.ev();
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
@@ -2136,6 +2160,7 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
     out[i].nb = r.nb;
     out[i].ms = ms;
     out[i].flops = r.flops;
+    out[i].bytes = r.bytes;
   }
   return PSGDK_OK;
 }
