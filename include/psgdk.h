@@ -253,6 +253,12 @@ int psgdk_kron2d_balance(const psgdk_kron2d_t* g, const int32_t* flags, int tri,
 int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const* mom, const void* const* g,
                    psgdk_stream_t stream);
 
+/* The same update for nb (1 .. 64) tensors of their own element counts numel[t] and gradient dtypes g_dtype[t]
+ * (host arrays), in one launch: the momentum EMA of every parameter of an optimizer step at once
+ * (psgd_pro.py:340-341 loops over the parameters). Each element's arithmetic is psgdk_momentum's. */
+int psgdk_momentum_multi(int nb, const int64_t* numel, float beta, const int32_t* g_dtype, float* const* mom,
+                         const void* const* g, psgdk_stream_t stream);
+
 /* Launch profiling (diagnostic, per host thread): after psgdk_profile_start every MFMA-engine launch the thread makes is
  * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
  * waits for the recorded events and fills one record per launch: the kernel instantiation id

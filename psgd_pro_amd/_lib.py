@@ -13,6 +13,7 @@ LIB_PATH = os.environ.get("PSGDK_LIB", os.path.join(_HERE, "libpsgdk.so"))
 
 MAXB = 16
 MAX_GROUPS = 64
+MAX_TENSORS = 64  # tensors per psgdk_momentum_multi call
 NLB_K = 32
 OK, EINVAL, ESHAPE, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 F32, BF16 = 0, 1
@@ -78,6 +79,7 @@ _SIGS = {
     "psgdk_kron2d_refresh_p": (_i32, [C.POINTER(Kron2d), _i32, _i32, _vp]),
     "psgdk_kron2d_balance": (_i32, [C.POINTER(Kron2d), C.POINTER(C.c_int32), _i32, _vp, _szp, _vp]),
     "psgdk_momentum": (_i32, [_i64, _f, _i32, _i32, _vpa, _vpa, _vp]),
+    "psgdk_momentum_multi": (_i32, [_i32, C.POINTER(C.c_int64), _f, C.POINTER(C.c_int32), _vpa, _vpa, _vp]),
     "psgdk_set_option": (_i32, [_i32, _i32]),
     "psgdk_get_option": (_i32, [_i32, C.POINTER(C.c_int)]),
     "psgdk_profile_start": (_i32, []),

@@ -2073,6 +2073,24 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
   return hip_check(momentum_launch(a, (hipStream_t)stream), "momentum");
 }
 
+int psgdk_momentum_multi(int nb, const int64_t* numel, float beta, const int32_t* g_dtype, float* const* mom,
+                         const void* const* g, psgdk_stream_t stream) {
+  if (nb < 1 || nb > MAXB) return fail(PSGDK_EINVAL, "nb = %d: must be in 1..%d", nb, MAXB);
+  if (!numel || !g_dtype) return fail(PSGDK_EINVAL, "null numel or g_dtype array");
+  PSGDK_TRY(check_ptrs(mom, nb, "mom"));
+  PSGDK_TRY(check_ptrs(g, nb, "g"));
+  MomList a;
+  std::memset(&a, 0, sizeof a);
+  a.nb = nb; a.beta = beta;
+  for (int t = 0; t < nb; ++t) {
+    PSGDK_TRY(check_dims(numel[t], "numel"));
+    PSGDK_TRY(check_dt(g_dtype[t], "g"));
+    a.off[t + 1] = a.off[t] + numel[t];
+    a.dt[t] = g_dtype[t]; a.g[t] = g[t]; a.m[t] = mom[t];
+  }
+  return hip_check(momentum_multi_launch(a, (hipStream_t)stream), "momentum (multi-tensor)");
+}
+
 int psgdk_set_option(int option, int value) {
   if (option == 0) {
     if (value < 0 || value > 2) return fail(PSGDK_EINVAL, "option 0 (bf16 tile order) must be 0 .. 2");

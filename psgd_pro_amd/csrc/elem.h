@@ -53,6 +53,17 @@ hipError_t balance_scalar_launch(const EwArgs& a, hipStream_t st);
 hipError_t scale_by_dev_launch(const EwArgs& a, hipStream_t st);
 // m = beta m + (1 - beta) g                           (psgd_pro.py:340-341)
 hipError_t momentum_launch(const EwArgs& a, hipStream_t st);
+// The same for nb tensors of their own sizes and gradient dtypes in one launch: tensor t holds elements
+// off[t] .. off[t + 1] - 1 of the concatenated index range.
+struct MomList {
+  int nb;
+  float beta;
+  long long off[MAXB + 1];
+  int dt[MAXB];
+  const void* g[MAXB];
+  float* m[MAXB];
+};
+hipError_t momentum_multi_launch(const MomList& a, hipStream_t st);
 // sum of the split partials: out[i] = sum_s in[s * m * n + i]
 hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
 // sum-of-squares partials in the GEMM's EPI_SUMSQ format (i0 blocks per problem)

@@ -683,6 +683,28 @@ hipError_t momentum_launch(const EwArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Each workgroup takes a contiguous slice of the concatenated index range; a thread's indices only grow, so the
+// tensor holding them is found by walking the offsets forward. The arithmetic is momentum_kernel's.
+__global__ void __launch_bounds__(EW_THREADS) momentum_multi_kernel(const MomList a) {
+  const long long total = a.off[a.nb];
+  const long long chunk = (total + gridDim.x - 1) / gridDim.x;
+  const long long beg = (long long)blockIdx.x * chunk, end = beg + chunk < total ? beg + chunk : total;
+  int t = 0;
+  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
+    while (i >= a.off[t + 1]) ++t;
+    const long long j = i - a.off[t];
+    float* m = a.m[t];
+    m[j] = m[j] * a.beta + (1.f - a.beta) * ldv(a.g[t], a.dt[t], j);
+  }
+}
+hipError_t momentum_multi_launch(const MomList& a, hipStream_t st) {
+  const long long total = a.off[a.nb];
+  const long long want = (total + EW_THREADS * 8 - 1) / (EW_THREADS * 8);
+  const int blocks = (int)(want < 1 ? 1 : want > 1024 ? 1024 : want);
+  hipLaunchKernelGGL(momentum_multi_kernel, dim3(blocks), dim3(EW_THREADS), 0, st, a);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(EW_THREADS) splitk_sum_kernel(const EwArgs a, int blocks_per) {
   const int b = blockIdx.x / blocks_per;

@@ -3,7 +3,8 @@
 Drop-in for psgd_pro.KronWhiten / psgd_pro_fast.KronWhiten (psgd_pro.py:251-384, psgd_pro_fast.py:239-499): the same
 constructor arguments, mutable attributes, step(closure) returning the closure's value and step_math(grads); plus
 state_dict() / load_state_dict() (absent in the reference). Every parameter's preconditioner update and gradient
-apply run through libpsgdk.so's grouped entry points (psgdk_kron2d_update / _apply / _balance, psgdk_momentum):
+apply run through libpsgdk.so's grouped entry points (psgdk_kron2d_update / _apply / _balance,
+psgdk_momentum_multi):
 parameters of one shape and factor structure form a group of up to 16 that every kernel launch covers at once, and
 no step synchronizes the host with the device.
 
@@ -120,7 +121,7 @@ class KronWhiten:
         self._nstreams, self._lanes = int(streams), None
         self._use_graphs = bool(graphs)
         # one psgdk_kron2d_update_groups call for every bf16-path group: the factor work of all groups is batched
-        # by factor side (results are bitwise those of one call per group)
+        # by factor side (the same operations as one call per group; larger launches may sum in another order)
         self._fuse = bool(fuse_groups)
         self._graphs, self._seen = {}, set()
         self._draw_buf = self._draw_buf16 = None
@@ -443,16 +444,13 @@ class KronWhiten:
 
     def _device_work(self, grads, beta, do_update, do_apply, noise, V):
         """Momentum (when beta is given), preconditioner update, apply: kernel launches only (capturable)."""
-        if beta is not None:
-            for dt in (torch.float32, torch.bfloat16):
-                idx = [i for i, g in enumerate(grads) if g.dtype == dt]
-                for c in range(0, len(idx), L.MAXB):
-                    ch = idx[c:c + L.MAXB]
-                    for sz in {grads[i].numel() for i in ch}:
-                        sel = [i for i in ch if grads[i].numel() == sz]
-                        L.check(L.lib().psgdk_momentum(sz, beta, L.dtype_code(dt), len(sel),
-                                                       L.ptrs([self._ms[i] for i in sel]),
-                                                       L.ptrs([grads[i] for i in sel]), L.stream_of(grads[0])))
+        if beta is not None:  # every parameter's momentum in one launch per 64 tensors
+            for c in range(0, len(grads), L.MAX_TENSORS):
+                ch = range(c, min(c + L.MAX_TENSORS, len(grads)))
+                numel = (ctypes.c_int64 * len(ch))(*[grads[i].numel() for i in ch])
+                dts = (ctypes.c_int32 * len(ch))(*[L.dtype_code(grads[i].dtype) for i in ch])
+                L.check(L.lib().psgdk_momentum_multi(len(ch), numel, beta, dts, L.ptrs([self._ms[i] for i in ch]),
+                                                     L.ptrs([grads[i] for i in ch]), L.stream_of(grads[0])))
         src = grads if self._whiten_grad else self._ms
         if do_update and self.update_preconditioner_first:
             self._update(src, noise, V)

@@ -543,3 +543,27 @@ def test_microbench_cells(hip, n, prec):
     B = rnd(n, n, seed=n + 2)
     Ct = K.trmm(poison_lower(Q).to(DEV), B.to(DEV), bool(prec))
     check_gemm_bound(Ct, torch.triu((bf(Q) if prec else Q).double()), (bf(B) if prec else B).double())
+
+
+def test_momentum_multi_matches_per_tensor(hip):
+    """psgdk_momentum_multi over tensors of different sizes and gradient dtypes in one launch equals
+    psgdk_momentum on each tensor bit for bit (the same arithmetic), and m = beta m + (1 - beta) g to fp32 rounding."""
+    import ctypes
+    sizes = [1, 7, 512, 65 * 512, 1000, 3, 1536 * 512]
+    dts = [torch.float32, torch.bfloat16, torch.float32, torch.bfloat16, torch.float32, torch.bfloat16, torch.float32]
+    g = [rnd(n, seed=i).to(dt).to(DEV) for i, (n, dt) in enumerate(zip(sizes, dts))]
+    m0 = [rnd(n, seed=50 + i).to(DEV) for i, n in enumerate(sizes)]
+    beta = 0.75
+    ma = [m.clone() for m in m0]
+    numel = (ctypes.c_int64 * len(sizes))(*sizes)
+    codes = (ctypes.c_int32 * len(sizes))(*[L.dtype_code(dt) for dt in dts])
+    L.check(hip.psgdk_momentum_multi(len(sizes), numel, beta, codes, L.ptrs(ma), L.ptrs(g), L.stream_of(g[0])))
+    mb = [m.clone() for m in m0]
+    for x, gx in zip(mb, g):
+        L.check(hip.psgdk_momentum(x.numel(), beta, L.dtype_code(gx.dtype), 1, L.ptrs([x]), L.ptrs([gx]),
+                                   L.stream_of(g[0])))
+    torch.cuda.synchronize()
+    for a, b, m, gx in zip(ma, mb, m0, g):
+        assert torch.equal(a, b)
+        ref = beta * m.double() + (1 - beta) * gx.double()
+        assert rel_err_norm(a, ref) < 1e-6
