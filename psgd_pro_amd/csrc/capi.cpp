@@ -231,6 +231,8 @@ thread_local int g_upd_streams = 3;  // option 6: side streams of psgdk_kron2d_u
 thread_local int g_rq16 = 1;   // option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
 thread_local int g_f32kc = 1;  // option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
 thread_local int g_big_batch = MAXB;  // option 9: items per batch of the grouped update for factor sides >= 2048
+thread_local int g_small = 128;       // option 10: plain-store products with fewer 128 x 128 tiles than this (over the
+                                      // launch) take the small-problem kernel (0: never)
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -316,11 +318,18 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   }
   int cfg = b16_cfg(M, N, K, tri, nb);
   if (esz == 4) cfg = 1;  // the fp32 kernel: the 128-tile configuration
-  if (ntiles) *ntiles = gemm_bf16_tiles(M, N, tri, cfg);
-  auto launch = [&]() { return esz == 4 ? gemm_f32kc_launch(a, cfg, st) : gemm_bf16_launch(a, cfg, st); };
+  // a plain store whose 128-tiles would leave most of the chip idle: the small-problem kernel (64-tiles, k in
+  // 512-byte chunks, two in flight)
+  const bool small = e.epi == EPI_STORE && !kbeg && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 &&
+                     (int64_t)gemm_bf16_tiles(M, N, tri, 1) * nb < g_small;
+  if (ntiles) *ntiles = small ? gemm_small_tiles(M, N, tri) : gemm_bf16_tiles(M, N, tri, cfg);
+  auto launch = [&]() {
+    if (small) return gemm_small_launch(a, esz, st);
+    return esz == 4 ? gemm_f32kc_launch(a, cfg, st) : gemm_bf16_launch(a, cfg, st);
+  };
   if (!g_prof.on) return hip_check(launch(), "k-contiguous gemm launch");
   ProfRec r;
-  r.kernel_id = (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
+  r.kernel_id = small ? 7000 + (esz == 4 ? 1 : 0) : (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
   r.flops = tri ? (double)M * (M + 1) * K * nb : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * K * nb;
@@ -2137,6 +2146,11 @@ int psgdk_set_option(int option, int value) {
     g_big_batch = value;
     return PSGDK_OK;
   }
+  if (option == 10) {
+    if (value < 0) return fail(PSGDK_EINVAL, "option 10 (small-problem kernel threshold) must be >= 0");
+    g_small = value;
+    return PSGDK_OK;
+  }
   if (option == 6) {
     if (value < 0 || value > 8) return fail(PSGDK_EINVAL, "option 6 (grouped update side streams) must be 0 .. 8");
     g_upd_streams = value;
@@ -2148,7 +2162,7 @@ int psgdk_set_option(int option, int value) {
 int psgdk_get_option(int option, int* value) {
   if (!value) return fail(PSGDK_EINVAL, "value is null");
   const int* opts[] = {&g_tile_order, &g_force_cfg,   &g_nlb_target, &g_vmm_u, &g_vmm_cols,
-                       &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch};
+                       &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch, &g_small};
   if (option < 0 || option >= (int)(sizeof opts / sizeof opts[0])) return fail(PSGDK_EINVAL, "unknown option %d", option);
   *value = *opts[option];
   return PSGDK_OK;

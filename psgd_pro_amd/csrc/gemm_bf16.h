@@ -39,5 +39,9 @@ hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
 // m- / n-contiguous; EPI_RQ reads R as fp32; every epilogue but EPI_PROCB, which reads a bf16 X operand)
 hipError_t gemm_f32kc_launch(GB16Args& a, int cfg, hipStream_t st);
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg);
+// Small products (plain-store epilogue, k-contiguous operands, bf16 (esz 2) or fp32 (esz 4)): 64 x 64 tiles, k in
+// chunks of 512 bytes per row with two chunks in flight (gemm_small.hip).
+hipError_t gemm_small_launch(GB16Args& a, int esz, hipStream_t st);
+int gemm_small_tiles(long long M, long long N, int tri);
 
 }  // namespace psgdk

@@ -567,3 +567,52 @@ def test_momentum_multi_matches_per_tensor(hip):
         assert torch.equal(a, b)
         ref = beta * m.double() + (1 - beta) * gx.double()
         assert rel_err_norm(a, ref) < 1e-6
+
+
+@pytest.mark.parametrize("kind,nb,m,n,k,dt", [("syrk_upper", 1, 512, 512, 512, torch.bfloat16),
+                                              ("syrk_mirror", 3, 300, 300, 1032, torch.bfloat16),
+                                              ("gemm", 2, 200, 136, 2056, torch.bfloat16),
+                                              ("gemm", 1, 64, 64, 8, torch.bfloat16),
+                                              ("syrk_upper", 1, 512, 512, 512, torch.float32),
+                                              ("syrk_mirror", 2, 130, 130, 260, torch.float32),
+                                              ("gemm", 4, 130, 260, 524, torch.float32)])
+def test_small_kernel(hip, kind, nb, m, n, k, dt):
+    """Products whose 128-tiles would leave most CUs idle take the small-problem kernel (64-tiles, k in chunks of
+    512 bytes per row, option 10): against float64 within the GEMM bound, a SYRK's lower triangle untouched in upper
+    mode, and within the same bound of the pipelined kernel's result (option 10 = 0)."""
+    prec = 1 if dt == torch.bfloat16 else 0
+    dcode = L.dtype_code(dt)
+    As = [rnd(m, k, seed=5 * i + 1).to(dt).to(DEV) for i in range(nb)]
+    Bs = [rnd(n, k, seed=5 * i + 2).to(dt).to(DEV) for i in range(nb)]
+    st = L.stream_of(As[0])
+
+    def run(thr):
+        Cs = [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)]
+        assert hip.psgdk_set_option(10, thr) == 0
+        L.profile_start()
+        if kind == "gemm":
+            L.check(hip.psgdk_gemm(prec, 0, 1, m, n, k, 1.0, dcode, dcode, nb, L.ptrs(As), k, L.ptrs(Bs), k, 0.0,
+                                   L.ptrs(Cs), n, st))
+        else:
+            mode = L.OUT_UPPER if kind == "syrk_upper" else L.OUT_MIRROR
+            L.check(hip.psgdk_syrk(prec, 0, mode, m, k, dcode, nb, L.ptrs(As), k, L.ptrs(Cs), m, st))
+        recs = L.profile_stop()
+        return Cs, recs
+    try:
+        small, recs = run(128)
+        pipe, _ = run(0)
+    finally:
+        hip.psgdk_set_option(10, 128)
+    assert [r[0] for r in recs] == [7000 if prec else 7001], recs
+    triu = torch.ones(m, n, dtype=torch.bool).triu()
+    for A, B, C, P in zip(As, Bs, small, pipe):
+        X = A.double().cpu()
+        Y = X if kind != "gemm" else B.double().cpu()
+        Cc, Pc = C.cpu(), P.cpu()
+        if kind == "syrk_upper":
+            assert bool(torch.isnan(Cc[~triu]).all()) and not bool(torch.isnan(Cc[triu]).any())
+            Cc, Pc = torch.where(triu, Cc, Cc.T), torch.where(triu, Pc, Pc.T)
+        else:
+            assert not bool(torch.isnan(Cc).any())
+        check_gemm_bound(Cc, X, Y.T)
+        check_gemm_bound(Pc, X, Y.T)
