@@ -295,9 +295,10 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * products; option 8 = whether fp32 products with k- or m/n-contiguous operands (M > 32, one k range, no packed
  * output) take the k-contiguous kernel's fp32 twin (1, default) or the general engine (0); option 9 = the most
  * factors of one side >= 2048 that psgdk_kron2d_update_groups batches into one launch (1 .. 64, default 64; smaller
- * batches of one side run on different side streams); option 10 = plain-store products on k-contiguous operands
+ * batches of one side run on different side streams); option 10 = plain-store bf16 GEMMs on k-contiguous operands
  * whose launch has fewer 128 x 128 tiles than this take the small-problem kernel (64 x 64 tiles, k in chunks of 512
- * bytes per row with two in flight; default 128, 0: never; not with a forced tile configuration, option 1). */
+ * bytes per row with two in flight); bf16 SYRKs below 1.5 times it and fp32 products below 3 times it (default 128,
+ * 0: never; not with a forced tile configuration, option 1). */
 int psgdk_set_option(int option, int value);
 /* The calling thread's value of a psgdk_set_option switch. */
 int psgdk_get_option(int option, int* value);

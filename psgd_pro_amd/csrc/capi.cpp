@@ -231,8 +231,9 @@ thread_local int g_upd_streams = 3;  // option 6: side streams of psgdk_kron2d_u
 thread_local int g_rq16 = 1;   // option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
 thread_local int g_f32kc = 1;  // option 8: fp32 products with k-contiguous operands take the k-contiguous kernel
 thread_local int g_big_batch = MAXB;  // option 9: items per batch of the grouped update for factor sides >= 2048
-thread_local int g_small = 128;       // option 10: plain-store products with fewer 128 x 128 tiles than this (over the
-                                      // launch) take the small-problem kernel (0: never)
+thread_local int g_small = 128;       // option 10: bf16 plain-store GEMMs with fewer 128 x 128 tiles than this (over
+                                      // the launch) take the small-problem kernel; bf16 SYRKs below 1.5 times it, fp32
+                                      // products below 3 times it (0: never)
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -319,9 +320,12 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   int cfg = b16_cfg(M, N, K, tri, nb);
   if (esz == 4) cfg = 1;  // the fp32 kernel: the 128-tile configuration
   // a plain store whose 128-tiles would leave most of the chip idle: the small-problem kernel (64-tiles, k in
-  // 512-byte chunks, two in flight)
-  const bool small = e.epi == EPI_STORE && !kbeg && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 &&
-                     (int64_t)gemm_bf16_tiles(M, N, tri, 1) * nb < g_small;
+  // 512-byte chunks, two in flight). Measured crossovers against the pipelined kernels (launch of nb problems, in
+  // 128-tiles): bf16 GEMMs about 130, bf16 SYRKs (whose triangle the 64-tiles follow more closely) about 200, fp32
+  // products about 400 (the fp32 twin's main loop is the slower one there).
+  const int64_t t128 = (int64_t)gemm_bf16_tiles(M, N, tri, 1) * nb;
+  const int64_t small_max = esz == 4 ? 3 * (int64_t)g_small : tri ? 3 * (int64_t)g_small / 2 : g_small;
+  const bool small = e.epi == EPI_STORE && !kbeg && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 && t128 < small_max;
   if (ntiles) *ntiles = small ? gemm_small_tiles(M, N, tri) : gemm_bf16_tiles(M, N, tri, cfg);
   auto launch = [&]() {
     if (small) return gemm_small_launch(a, esz, st);
