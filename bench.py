@@ -14,10 +14,13 @@ MFMA path (fp32 accumulate). Synthetic data; weights random-initialised.
 `roofline` is measured live: every MFMA-engine launch in the timed steps is bracketed by HIP events on its stream;
 the dominant kernel instantiation (largest total time) is reported with its algorithmic TFLOP/s against the bf16
 (or fp32) MFMA peak. `traffic` (HBM bytes per launch of that kernel) comes from the committed rocprofv3 counter
-summary when present. `cpu_baseline` times the CPU oracle (oracle/psgd_oracle.py, float32, torch CPU threads) on
+summary when present. `sustained_peak` is the bf16 MFMA rate measured live on the same GPU by a kernel of
+independent MFMAs with no memory traffic (the ceiling at the box's engine clock under load), and
+`frac_of_sustained` the dominant kernel's rate over it; `peak` and `frac` stay the published figures. `cpu_baseline` times the CPU oracle (oracle/psgd_oracle.py, float32, torch CPU threads) on
 one ViT-B block (4 of the 48 weights) and scales it to the whole set.
 """
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -83,6 +86,28 @@ def read_traffic(kernel):
 
 
 PEAK_HBM = 8.0  # TB/s, MI355X HBM3E
+
+
+def mfma_sustained(dev):
+    """The bf16 MFMA rate the GPU sustains now (psgdk_mfma_rate: 2 workgroups of 4 waves per CU, each wave issuing
+    32 independent 16 x 16 x 32 MFMAs per round with no memory traffic), in TFLOP/s: the ceiling at the box's current
+    engine clock under a dense MFMA load."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs, iters = 2 * cus, 20000
+    out = torch.empty(4 * wgs, device=dev)
+    st = L.stream_of(out)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    L.check(L.lib().psgdk_mfma_rate(iters, wgs, C.c_void_p(out.data_ptr()), st))
+    torch.cuda.synchronize(dev)
+    ev[0].record()
+    for _ in range(3):
+        L.check(L.lib().psgdk_mfma_rate(iters, wgs, C.c_void_p(out.data_ptr()), st))
+    ev[1].record()
+    torch.cuda.synchronize(dev)
+    sec = ev[0].elapsed_time(ev[1]) * 1e-3 / 3
+    return 4 * wgs * iters * 32 * 16384 / sec / 1e12
 
 
 def roof_ms(fl, by, peak):
@@ -247,6 +272,7 @@ def bench_vitb(args):
     recs = L.profile_stop()
     opt._nstreams = args.streams
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
+    sustained = mfma_sustained(dev)
     peak = PEAK[args.precision]
     agg, syrk = aggregate(recs, peak)
     kid = max(agg, key=lambda k: agg[k][1])
@@ -303,7 +329,9 @@ def bench_vitb(args):
                      "achieved": round(achieved, 2), "peak": PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3,
                      "unit": "TFLOP/s" if mfma_bound else "GB/s",
                      "frac": round(achieved / (PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3), 4),
-                     "roof_frac": round(roof_tot / ms_tot, 4), "traffic": traffic},
+                     "roof_frac": round(roof_tot / ms_tot, 4), "traffic": traffic,
+                     "sustained_peak": round(sustained, 1) if mfma_bound and prec_of == "bf16" else None,
+                     "frac_of_sustained": round(achieved / sustained, 4) if mfma_bound and prec_of == "bf16" else None},
         "launch_classes": launch_classes(recs, args.steps, peak),
         "kernels": {L.kernel_name(k): {"launches_per_step": v[0] / args.steps, "ms_per_step": round(v[1] / args.steps, 3),
                                        "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2),

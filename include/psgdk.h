@@ -303,8 +303,15 @@ int psgdk_set_option(int option, int value);
 /* The calling thread's value of a psgdk_set_option switch. */
 int psgdk_get_option(int option, int* value);
 
+/* Measurement (no counterpart in the reference): wgs workgroups of 4 waves, each wave issuing iters x 32
+ * independent bf16 MFMAs of 16 x 16 x 32 (16384 flops each) with no memory traffic; out receives one float per wave
+ * (4 wgs). Timed at two workgroups per CU it gives the bf16 MFMA rate the GPU sustains at its current clock, the
+ * ceiling a kernel can reach there. */
+int psgdk_mfma_rate(int iters, int wgs, float* out, psgdk_stream_t stream);
+
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
- * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B. Checks the compiler builtins' lane layout. */
+ * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B; prec 2: the 32 x 32 x 16 bf16 shape (A 32 x 16, B 16 x 32,
+ * C 32 x 32). Checks the compiler builtins' lane layout. */
 int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream);
 
 #ifdef __cplusplus

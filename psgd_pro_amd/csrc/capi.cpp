@@ -19,6 +19,7 @@
 namespace psgdk {
 hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
+hipError_t mfma_rate_launch(int iters, int wgs, float* out, hipStream_t st);
 int set_error(int code, const char* msg);  // for entry points defined in other source files
 }  // namespace psgdk
 
@@ -2201,8 +2202,14 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
   return PSGDK_OK;
 }
 
+int psgdk_mfma_rate(int iters, int wgs, float* out, psgdk_stream_t stream) {
+  if (iters < 1 || wgs < 1) return fail(PSGDK_EINVAL, "iters = %d, wgs = %d: both must be >= 1", iters, wgs);
+  if (!out) return fail(PSGDK_EINVAL, "null pointer");
+  return hip_check(mfma_rate_launch(iters, wgs, out, (hipStream_t)stream), "mfma rate");
+}
+
 int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream) {
-  PSGDK_TRY(check_prec(prec));
+  if (prec != 2) PSGDK_TRY(check_prec(prec));
   if (!A || !B || !C) return fail(PSGDK_EINVAL, "null pointer");
   return hip_check(debug_mfma_launch(A, B, C, prec, (hipStream_t)stream), "debug mfma");
 }

@@ -8,6 +8,7 @@ namespace psgdk {
 typedef uint16_t bf16_t;  // bfloat16 storage (raw bits)
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr float kSmallestNormal = 1.17549435e-38f;  // torch.finfo(torch.float32).smallest_normal
 

@@ -386,8 +386,23 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(const GemmArgs p) {
 // One MFMA on a single wave with operands placed by the lane layout the GEMM assumes; the host compares C with
 // A @ B (layout check of the compiler builtins).
 __global__ void psgdk_debug_mfma_kernel(const float* A, const float* B, float* C, int prec) {
-  // A: 16 x K row-major, B: K x 16 row-major, C: 16 x 16, K = 32 (bf16) or 4 (fp32); one wave.
+  // A: 16 x K row-major, B: K x 16 row-major, C: 16 x 16, K = 32 (bf16) or 4 (fp32); one wave. prec 2: the 32 x 32
+  // bf16 shape, A 32 x 16, B 16 x 32, C 32 x 32: lane l holds A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32],
+  // and accumulator m of lane l is C[8 (m / 4) + 4 (l / 32) + m % 4][l % 32].
   const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+  if (prec == 2) {
+    const int c = lane & 31, h = lane >> 5;
+    bf16x8_t a, b;
+    for (int e = 0; e < 8; ++e) {
+      a[e] = __builtin_bit_cast(__bf16, f32_to_bf16(A[c * 16 + 8 * h + e]));
+      b[e] = __builtin_bit_cast(__bf16, f32_to_bf16(B[(8 * h + e) * 32 + c]));
+    }
+    f32x16_t acc;
+    for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+    for (int m = 0; m < 16; ++m) C[(8 * (m >> 2) + 4 * h + (m & 3)) * 32 + c] = acc[m];
+    return;
+  }
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (prec == 1) {
     bf16x8_t a, b;
@@ -400,6 +415,32 @@ __global__ void psgdk_debug_mfma_kernel(const float* A, const float* B, float* C
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[r * 4 + g], B[g * 16 + r], acc, 0, 0, 0);
   }
   for (int e = 0; e < 4; ++e) C[(g * 4 + e) * 16 + r] = acc[e];
+}
+
+// The bf16 MFMA rate this GPU sustains at the moment of the call: each wave issues `iters` rounds of 32
+// independent v_mfma_f32_16x16x32_bf16 (no memory traffic in the loop; operands from the lane index), and lane 0 of
+// each wave writes the sum of its accumulators' first element to out[wave id] so that nothing is optimised away.
+// 16384 flops per MFMA. One wave per SIMD issuing this instruction stays near 1.4-1.55 PFLOP/s however many
+// independent accumulators it cycles through; two waves per SIMD with 32 each reach about 2.36 (measured): launch
+// two workgroups per CU.
+__global__ void __launch_bounds__(256, 2) psgdk_mfma_rate_kernel(int iters, float* out) {
+  const int lane = threadIdx.x & 63;
+  bf16x8_t a, b;
+  for (int e = 0; e < 8; ++e) {
+    a[e] = __builtin_bit_cast(__bf16, f32_to_bf16(1.f + 1e-3f * (lane + e)));
+    b[e] = __builtin_bit_cast(__bf16, f32_to_bf16(1.f - 1e-3f * (lane ^ e)));
+  }
+  f32x4_t acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[i], 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) t += acc[i][0];
+  if (lane == 0) out[blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = t;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -445,6 +486,11 @@ hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStre
   if (adt == 0 && bdt == 1) return launch_prec<0, float, bf16_t>(a, cfg, st);
   if (adt == 1 && bdt == 0) return launch_prec<0, bf16_t, float>(a, cfg, st);
   return launch_prec<0, bf16_t, bf16_t>(a, cfg, st);
+}
+
+hipError_t mfma_rate_launch(int iters, int wgs, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(psgdk_mfma_rate_kernel, dim3(wgs), dim3(256), 0, st, iters, out);
+  return hipGetLastError();
 }
 
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st) {

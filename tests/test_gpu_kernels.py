@@ -41,15 +41,16 @@ def poison_lower(S):
 
 
 # --------------------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("prec", [0, 1, 2])
 def test_mfma_lane_layout(hip, prec):
-    k = 32 if prec else 4
-    A = rnd(16, k, seed=1)
-    B = rnd(k, 16, seed=2)
+    t = 32 if prec == 2 else 16
+    k = {0: 4, 1: 32, 2: 16}[prec]
+    A = rnd(t, k, seed=1)
+    B = rnd(k, t, seed=2)
     if prec:
         A, B = bf(A), bf(B)
     Ad, Bd = A.to(DEV), B.to(DEV)
-    Cd = torch.empty(16, 16, device=DEV)
+    Cd = torch.empty(t, t, device=DEV)
     L.check(hip.psgdk_debug_mfma(prec, C_ptr(Ad), C_ptr(Bd), C_ptr(Cd), L.stream_of(Ad)))
     torch.cuda.synchronize()
     check_gemm_bound(Cd, A.double(), B.double(), tol=8)
@@ -616,3 +617,17 @@ def test_small_kernel(hip, kind, nb, m, n, k, dt):
             assert not bool(torch.isnan(Cc).any())
         check_gemm_bound(Cc, X, Y.T)
         check_gemm_bound(Pc, X, Y.T)
+
+
+def test_mfma_rate_kernel(hip):
+    """The MFMA-rate calibration kernel: every wave computes the same sums from the same lane operands (lane 0 of
+    each of the 4 waves of each workgroup writes one), so the output is finite and uniform, and grows with iters."""
+    outs = []
+    for iters in (1, 3):
+        out = torch.full((4 * 8,), float("nan"), device=DEV)
+        L.check(hip.psgdk_mfma_rate(iters, 8, C_ptr(out), L.stream_of(out)))
+        o = out.cpu()
+        assert bool(torch.isfinite(o).all()) and bool((o == o[0]).all()), o
+        outs.append(float(o[0]))
+    assert abs(outs[1] - 3 * outs[0]) <= 1e-3 * abs(outs[1])
+    assert hip.psgdk_mfma_rate(0, 8, C_ptr(out), L.stream_of(out)) == L.EINVAL
