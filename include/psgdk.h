@@ -259,6 +259,15 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
 int psgdk_momentum_multi(int nb, const int64_t* numel, float beta, const int32_t* g_dtype, float* const* mom,
                          const void* const* g, psgdk_stream_t stream);
 
+/* out[0 .. n) = standard normal samples (fp32 or bf16 storage, dtype) from the counter-based Philox4x32-10
+ * generator (Salmon et al., SC 2011) keyed by seed on stream stream_id, through the Box-Muller transform (fp32 with
+ * the hardware log2, square root, sine and cosine: within 2e-5 (1 + |z|) of the exact transform): element i
+ * depends only on (seed, stream_id, i), so a call is reproducible and calls with different (seed, stream_id) are
+ * independent. The device draws of an optimizer step (the noise and the norm bounds' random starts, which
+ * psgd_pro_fast.py:200-206 and 482-483 draw with torch.randn on the device). out: 16-byte aligned (fp32) or 8-byte
+ * (bf16). */
+int psgdk_fill_normal(void* out, int64_t n, int dtype, uint64_t seed, uint64_t stream_id, psgdk_stream_t stream);
+
 /* Launch profiling (diagnostic, per host thread): after psgdk_profile_start every MFMA-engine launch the thread makes is
  * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
  * waits for the recorded events and fills one record per launch: the kernel instantiation id

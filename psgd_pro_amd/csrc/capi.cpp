@@ -2087,6 +2087,16 @@ int psgdk_momentum(int64_t numel, float beta, int g_dtype, int nb, float* const*
   return hip_check(momentum_launch(a, (hipStream_t)stream), "momentum");
 }
 
+int psgdk_fill_normal(void* out, int64_t n, int dtype, uint64_t seed, uint64_t stream_id, psgdk_stream_t stream) {
+  PSGDK_TRY(check_dt(dtype, "out"));
+  if (n < 0) return fail(PSGDK_ESHAPE, "n = %lld: must be >= 0", (long long)n);
+  if (n == 0) return PSGDK_OK;
+  if (!out) return fail(PSGDK_EINVAL, "null out");
+  if (reinterpret_cast<uintptr_t>(out) % (dtype == PSGDK_BF16 ? 8 : 16))
+    return fail(PSGDK_EINVAL, "out must be %d-byte aligned", dtype == PSGDK_BF16 ? 8 : 16);
+  return hip_check(normal_fill_launch(out, n, dtype, seed, stream_id, (hipStream_t)stream), "normal fill");
+}
+
 int psgdk_momentum_multi(int nb, const int64_t* numel, float beta, const int32_t* g_dtype, float* const* mom,
                          const void* const* g, psgdk_stream_t stream) {
   if (nb < 1 || nb > MAXB) return fail(PSGDK_EINVAL, "nb = %d: must be in 1..%d", nb, MAXB);

@@ -64,6 +64,10 @@ struct MomList {
   float* m[MAXB];
 };
 hipError_t momentum_multi_launch(const MomList& a, hipStream_t st);
+// out[0 .. n) = standard normals (fp32 or bf16 storage, dt) from Philox4x32-10 keyed by seed on stream stream_id,
+// four per counter value (Box-Muller); out 16-byte aligned for fp32, 8-byte for bf16
+hipError_t normal_fill_launch(void* out, long long n, int dt, unsigned long long seed, unsigned long long stream_id,
+                              hipStream_t st);
 // sum of the split partials: out[i] = sum_s in[s * m * n + i]
 hipError_t splitk_sum_launch(const EwArgs& a, hipStream_t st);
 // sum-of-squares partials in the GEMM's EPI_SUMSQ format (i0 blocks per problem)

@@ -706,6 +706,75 @@ hipError_t momentum_multi_launch(const MomList& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Standard normals from a counter-based generator: Philox4x32 with 10 rounds (Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011), key = the 64-bit seed, counter = (block b of four
+// outputs, as two 32-bit words; the 64-bit stream id as two words). A round multiplies words 0 and 2 by the
+// published constants 0xD2511F53 and 0xCD9E8D57, keeps the low halves and XORs the high halves with words 1, 3 and
+// the key; the key is bumped by the Weyl increments 0x9E3779B9 and 0xBB67AE85 between rounds. Each word x gives
+// the uniform u = (floor(x / 256) + 1/2) 2^-24 in (0, 1), exact in fp32 (so ln u keeps its precision next to 1),
+// and each pair (u0, u1) two normals by the Box-Muller transform,
+// sqrt(-2 ln u0) (cos 2 pi u1, sin 2 pi u1). Output b covers elements 4 b .. 4 b + 3 (fp32, or bf16 rounded from
+// the fp32 value).
+__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
+    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
+    c[0] = hi1 ^ c[1] ^ k0;
+    c[1] = lo1;
+    c[2] = hi0 ^ c[3] ^ k1;
+    c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+__global__ void __launch_bounds__(EW_THREADS) normal_fill_kernel(void* out, long long n, int dt, uint32_t k0,
+                                                                   uint32_t k1, uint32_t s0, uint32_t s1) {
+  const long long nblk = (n + 3) / 4;
+  for (long long blk = (long long)blockIdx.x * EW_THREADS + threadIdx.x; blk < nblk;
+       blk += (long long)gridDim.x * EW_THREADS) {
+    uint32_t c[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), s0, s1};
+    philox4x32_10(c, k0, k1);
+    float z[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float u0 = ((float)(c[2 * h] >> 8) + 0.5f) * 5.9604644775390625e-8f;  // 2^-24
+      const float u1 = ((float)(c[2 * h + 1] >> 8) + 0.5f) * 5.9604644775390625e-8f;
+      // the hardware transcendentals: v_log_f32 (log2), v_sqrt_f32, and v_sin_f32 / v_cos_f32, which take their
+      // argument in revolutions (sin 2 pi u1 directly); -2 ln u0 = -2 ln 2 log2 u0
+      const float r = __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(u0));
+      z[2 * h] = r * __builtin_amdgcn_cosf(u1);
+      z[2 * h + 1] = r * __builtin_amdgcn_sinf(u1);
+    }
+    const long long i0 = 4 * blk;
+    if (dt == 1) {  // bf16 storage (dtype codes: 0 fp32, 1 bf16)
+      bf16_t* o = reinterpret_cast<bf16_t*>(out) + i0;
+      if (i0 + 4 <= n) {
+        *reinterpret_cast<uint2*>(o) = make_uint2(pack2(f32_to_bf16(z[0]), f32_to_bf16(z[1])),
+                                                  pack2(f32_to_bf16(z[2]), f32_to_bf16(z[3])));
+      } else {
+        for (int e = 0; i0 + e < n; ++e) o[e] = f32_to_bf16(z[e]);
+      }
+    } else {
+      float* o = reinterpret_cast<float*>(out) + i0;
+      if (i0 + 4 <= n) *reinterpret_cast<float4*>(o) = make_float4(z[0], z[1], z[2], z[3]);
+      else
+        for (int e = 0; i0 + e < n; ++e) o[e] = z[e];
+    }
+  }
+}
+hipError_t normal_fill_launch(void* out, long long n, int dt, unsigned long long seed, unsigned long long stream_id,
+                              hipStream_t st) {
+  const long long nblk = (n + 3) / 4;
+  const long long want = (nblk + EW_THREADS * 4 - 1) / (EW_THREADS * 4);
+  const int blocks = (int)(want < 1 ? 1 : want > 4096 ? 4096 : want);
+  hipLaunchKernelGGL(normal_fill_kernel, dim3(blocks), dim3(EW_THREADS), 0, st, out, n, dt, (uint32_t)seed,
+                     (uint32_t)(seed >> 32), (uint32_t)stream_id, (uint32_t)(stream_id >> 32));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(EW_THREADS) splitk_sum_kernel(const EwArgs a, int blocks_per) {
   const int b = blockIdx.x / blocks_per;
   long long beg, end;

@@ -14,7 +14,8 @@ factor). Tensors of order 3 or more are rejected (NotImplementedError).
 Random draws (psgd_pro.py:123,35,59,138,345): draws="host" reproduces psgd_pro.py's stream on a CPU generator
 (update coin, then per parameter the damping noise, two 32 x d starts per dense factor, the balancing coin) and
 uploads the normals; draws="device" draws the coins on the CPU (update coin, then one balancing coin per parameter,
-as psgd_pro_fast.py:482-483) and the normals on the device generator.
+as psgd_pro_fast.py:482-483), then a 62-bit seed, and the library fills the step's normals on the GPU from it
+(Philox4x32-10 and Box-Muller, psgdk_fill_normal: one launch per dtype buffer).
 """
 import ctypes
 
@@ -281,10 +282,16 @@ class KronWhiten:
                 if tot[dt]:
                     bufs[dt][:tot[dt]].copy_(host[dt][:tot[dt]].pin_memory(), non_blocking=True)
         else:
+            # the normals from the library's counter-based generator (Philox4x32-10), keyed by a seed drawn from the
+            # CPU generator after the coins: the step's whole draw is one launch per buffer, and the generator state
+            # that state_dict saves determines it
             coins = (torch.rand(len(self._params), generator=self._gen) < 0.01).tolist()
-            for dt in bufs:
+            seed = int(torch.randint(0, 2 ** 62, (1,), generator=self._gen))
+            st = L.stream_of(bufs[torch.float32])
+            for sid, dt in enumerate((torch.float32, torch.bfloat16)):
                 if tot[dt]:
-                    torch.randn(tot[dt], device=dev, dtype=dt, out=bufs[dt][:tot[dt]])
+                    L.check(L.lib().psgdk_fill_normal(ctypes.c_void_p(bufs[dt].data_ptr()), tot[dt], L.dtype_code(dt),
+                                                      seed, sid, st))
         noise, V = [], []
         for dt, (no, vo, a, b) in zip(ndt, lay):
             noise.append(bufs[dt][no:no + a])

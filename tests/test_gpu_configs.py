@@ -180,8 +180,9 @@ def test_vitb_full_set_first_step_and_paths(hip):
 
 
 def test_vitb_device_draws(hip):
-    """The benchmark's own configuration (draws on the device generator): after 3 steps every factor, L and
-    parameter is finite, L > 0, and the same device seed reproduces every value bit for bit."""
+    """The benchmark's own configuration (device draws: normals from the library's counter-based generator keyed by
+    the optimizer's CPU generator): after 3 steps every factor, L and parameter is finite, L > 0, and the same seed
+    reproduces every value bit for bit."""
     shapes = VIT_B * 12
     kw = dict(preconditioner_max_size=8192, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0)
     runs = []

@@ -631,3 +631,33 @@ def test_mfma_rate_kernel(hip):
         outs.append(float(o[0]))
     assert abs(outs[1] - 3 * outs[0]) <= 1e-3 * abs(outs[1])
     assert hip.psgdk_mfma_rate(0, 8, C_ptr(out), L.stream_of(out)) == L.EINVAL
+
+
+def test_fill_normal_matches_philox_reference(hip):
+    """psgdk_fill_normal against the Python Philox4x32-10 + Box-Muller checker (itself pinned to the published
+    known-answer vectors): the first 1003 fp32 normals of two (seed, stream) pairs within 2e-5 (1 + |z|) of the
+    float64 values; bf16 storage equals the fp32 values rounded; another stream gives other values; one million
+    normals have mean and variance within 5 standard errors of 0 and 1."""
+    from philox_ref import normals
+    st = L.stream_of(torch.empty(1, device=DEV))
+    for seed, sid in [(0, 0), ((1 << 61) + 12345, 3)]:
+        n = 1003
+        out = torch.full((n + 5,), float("nan"), device=DEV)
+        L.check(hip.psgdk_fill_normal(C_ptr(out), n, L.F32, seed, sid, st))
+        got = out.cpu().double()
+        ref = torch.tensor(normals(n, seed, sid), dtype=torch.float64)
+        assert bool(torch.isnan(got[n:]).all())
+        # fp32 with the hardware log2 / sqrt / sin / cos: within 2e-5 (1 + |z|) of the float64 values
+        assert bool(((got[:n] - ref).abs() <= 2e-5 * (1 + ref.abs())).all()), float((got[:n] - ref).abs().max())
+        o16 = torch.empty(n, device=DEV, dtype=torch.bfloat16)
+        L.check(hip.psgdk_fill_normal(C_ptr(o16), n, L.BF16, seed, sid, st))
+        assert torch.equal(o16.cpu(), out[:n].cpu().to(torch.bfloat16))
+    a = torch.empty(1 << 20, device=DEV)
+    b_ = torch.empty(1 << 20, device=DEV)
+    L.check(hip.psgdk_fill_normal(C_ptr(a), a.numel(), L.F32, 7, 0, st))
+    L.check(hip.psgdk_fill_normal(C_ptr(b_), b_.numel(), L.F32, 7, 1, st))
+    n = a.numel()
+    assert not torch.equal(a, b_)
+    assert abs(float(a.double().mean())) < 5 / math.sqrt(n)
+    assert abs(float(a.double().var()) - 1) < 5 * math.sqrt(2 / n)
+    assert hip.psgdk_fill_normal(C_ptr(a[1:]), 8, L.F32, 7, 0, st) == L.EINVAL  # misaligned
