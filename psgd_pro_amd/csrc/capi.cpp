@@ -2105,12 +2105,15 @@ int psgdk_momentum_multi(int nb, const int64_t* numel, float beta, const int32_t
   PSGDK_TRY(check_ptrs(g, nb, "g"));
   MomList a;
   std::memset(&a, 0, sizeof a);
-  a.nb = nb; a.beta = beta;
+  a.nb = nb; a.beta = beta; a.vec = 1;
   for (int t = 0; t < nb; ++t) {
     PSGDK_TRY(check_dims(numel[t], "numel"));
     PSGDK_TRY(check_dt(g_dtype[t], "g"));
-    a.off[t + 1] = a.off[t] + numel[t];
+    a.off[t + 1] = a.off[t] + (numel[t] + 3) / 4 * 4;
+    a.n[t] = numel[t];
     a.dt[t] = g_dtype[t]; a.g[t] = g[t]; a.m[t] = mom[t];
+    const uintptr_t ga = reinterpret_cast<uintptr_t>(g[t]), ma = reinterpret_cast<uintptr_t>(mom[t]);
+    if (ma % 16 || ga % (g_dtype[t] == PSGDK_BF16 ? 8 : 16)) a.vec = 0;
   }
   return hip_check(momentum_multi_launch(a, (hipStream_t)stream), "momentum (multi-tensor)");
 }

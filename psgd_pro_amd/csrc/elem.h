@@ -57,8 +57,11 @@ hipError_t momentum_launch(const EwArgs& a, hipStream_t st);
 // off[t] .. off[t + 1] - 1 of the concatenated index range.
 struct MomList {
   int nb;
+  int vec;                  // every m 16-byte and every g 16-byte (fp32) / 8-byte (bf16) aligned: 4 elements per access
   float beta;
-  long long off[MAXB + 1];
+  long long off[MAXB + 1];  // tensor t's elements at off[t] .. off[t] + n[t] of the concatenated range (off[t] a
+                            // multiple of 4: each tensor's length is rounded up to 4 there)
+  long long n[MAXB];
   int dt[MAXB];
   const void* g[MAXB];
   float* m[MAXB];

@@ -683,23 +683,45 @@ hipError_t momentum_launch(const EwArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Each workgroup takes a contiguous slice of the concatenated index range; a thread's indices only grow, so the
-// tensor holding them is found by walking the offsets forward. The arithmetic is momentum_kernel's.
+// Each workgroup takes a contiguous slice of the concatenated range in groups of 4 elements (a group never spans two
+// tensors: each tensor starts at a multiple of 4); a thread's groups only grow, so the tensor holding them is found by
+// walking the offsets forward. 16-byte m and g accesses where every tensor is aligned for them. The arithmetic is
+// momentum_kernel's.
 __global__ void __launch_bounds__(EW_THREADS) momentum_multi_kernel(const MomList a) {
-  const long long total = a.off[a.nb];
+  const long long total = a.off[a.nb] / 4;
   const long long chunk = (total + gridDim.x - 1) / gridDim.x;
   const long long beg = (long long)blockIdx.x * chunk, end = beg + chunk < total ? beg + chunk : total;
   int t = 0;
-  for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
-    while (i >= a.off[t + 1]) ++t;
-    const long long j = i - a.off[t];
+  for (long long q = beg + threadIdx.x; q < end; q += EW_THREADS) {
+    const long long e = 4 * q;
+    while (e >= a.off[t + 1]) ++t;
+    const long long j = e - a.off[t], n = a.n[t];
+    if (j >= n) continue;  // the padding of tensor t
     float* m = a.m[t];
-    m[j] = m[j] * a.beta + (1.f - a.beta) * ldv(a.g[t], a.dt[t], j);
+    if (a.vec && j + 4 <= n) {
+      float4 mv = *reinterpret_cast<const float4*>(m + j);
+      float gv[4];
+      if (a.dt[t]) {
+        const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16_t*>(a.g[t]) + j);
+        gv[0] = bf16_to_f32((bf16_t)(h.x & 0xffff)); gv[1] = bf16_to_f32((bf16_t)(h.x >> 16));
+        gv[2] = bf16_to_f32((bf16_t)(h.y & 0xffff)); gv[3] = bf16_to_f32((bf16_t)(h.y >> 16));
+      } else {
+        const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.g[t]) + j);
+        gv[0] = f.x; gv[1] = f.y; gv[2] = f.z; gv[3] = f.w;
+      }
+      mv.x = mv.x * a.beta + (1.f - a.beta) * gv[0];
+      mv.y = mv.y * a.beta + (1.f - a.beta) * gv[1];
+      mv.z = mv.z * a.beta + (1.f - a.beta) * gv[2];
+      mv.w = mv.w * a.beta + (1.f - a.beta) * gv[3];
+      *reinterpret_cast<float4*>(m + j) = mv;
+    } else {
+      for (long long i = j; i < j + 4 && i < n; ++i) m[i] = m[i] * a.beta + (1.f - a.beta) * ldv(a.g[t], a.dt[t], i);
+    }
   }
 }
 hipError_t momentum_multi_launch(const MomList& a, hipStream_t st) {
-  const long long total = a.off[a.nb];
-  const long long want = (total + EW_THREADS * 8 - 1) / (EW_THREADS * 8);
+  const long long total = a.off[a.nb] / 4;  // groups of 4 elements
+  const long long want = (total + EW_THREADS * 4 - 1) / (EW_THREADS * 4);
   const int blocks = (int)(want < 1 ? 1 : want > 1024 ? 1024 : want);
   hipLaunchKernelGGL(momentum_multi_kernel, dim3(blocks), dim3(EW_THREADS), 0, st, a);
   return hipGetLastError();
