@@ -26,7 +26,7 @@ extern "C" {
 
 typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
 
-#define PSGDK_VERSION 2
+#define PSGDK_VERSION 3
 #define PSGDK_MAXB 16 /* problems per grouped call */
 #define PSGDK_MAX_GROUPS 64 /* groups per psgdk_kron2d_update_groups call */
 #define PSGDK_NLB_K 32 /* rows of the random start of the norm lower bounds */
