@@ -47,7 +47,7 @@ def parse_args():
     ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e", "ceiling"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--streams", type=int, default=4, help="side streams for independent weight groups")
+    ap.add_argument("--streams", type=int, default=3, help="side streams for independent weight groups")
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
     ap.add_argument("--fuse", type=int, default=1,
                     help="0: one update call per weight group instead of one call batching all groups' factor work")

@@ -78,7 +78,7 @@ class KronWhiten:
                  draws="device",
                  seed=None,
                  tri=None,
-                 streams=4,
+                 streams=3,
                  graphs=False,
                  fuse_groups=True):
         self.lr_params = lr_params

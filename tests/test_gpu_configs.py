@@ -52,11 +52,11 @@ def _worst(Qs, Ls, pre, ref):
 
 
 def test_vitb_block_bf16_parity(hip):
-    """The benchmarked path (precision bf16, fuse_groups, streams=4) on one ViT-B block, host draws, 5 steps."""
+    """The benchmarked path (precision bf16, fuse_groups, streams=3) on one ViT-B block, host draws, 5 steps."""
     shapes = VIT_B
     W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
     kw = dict(preconditioner_max_size=8192, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0)
-    opt = KronWhiten(W, precision="bf16", draws="host", seed=0, streams=4, fuse_groups=True, **kw)
+    opt = KronWhiten(W, precision="bf16", draws="host", seed=0, streams=3, fuse_groups=True, **kw)
     opt.capture = True
     mk = lambda rounding: O.OracleKron([torch.zeros(s) for s in shapes], seed=0, dtype=torch.float32,
                                        grad_eps=EPS16, noise_dtype=torch.bfloat16, rounding=rounding, **kw)
@@ -190,7 +190,7 @@ def test_vitb_device_draws(hip):
         torch.cuda.manual_seed(1234)
         W = [(0.02 * torch.randn(s, generator=torch.Generator().manual_seed(7))).to(DEV).requires_grad_(True)
              for s in shapes]
-        opt = KronWhiten(W, precision="bf16", draws="device", seed=0, streams=4, fuse_groups=True, **kw)
+        opt = KronWhiten(W, precision="bf16", draws="device", seed=0, streams=3, fuse_groups=True, **kw)
         for t in range(3):
             opt.step_math([g.to(DEV) for g in _grads(shapes, t)])
         torch.cuda.synchronize()
