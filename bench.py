@@ -47,7 +47,9 @@ def parse_args():
     ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e", "ceiling"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--streams", type=int, default=3, help="side streams for independent weight groups")
+    ap.add_argument("--streams", type=int, default=None,
+                    help="side streams for independent weight groups (default: KronWhiten's, 3 for up to four groups, "
+                         "4 for more)")
     ap.add_argument("--graphs", type=int, default=0, help="1: replay captured HIP graphs of the step's device work")
     ap.add_argument("--fuse", type=int, default=1,
                     help="0: one update call per weight group instead of one call batching all groups' factor work")
@@ -66,6 +68,8 @@ def parse_args():
                     help="0: form term1 Q as the reference writes it, never through Pg (library option 5)")
     ap.add_argument("--r2", type=int, default=0,
                     help="1: the Procrustes step in the reference's r2 form (KronWhiten(r2=True), 3 d^3 instead of 4 d^3)")
+    ap.add_argument("--opt", action="append", default=[], metavar="N=V",
+                    help="set library option N to V before the run (psgdk_set_option; repeatable)")
     return ap.parse_args()
 
 
@@ -272,6 +276,7 @@ def bench_vitb(args):
     recs = L.profile_stop()
     opt._nstreams = args.streams
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
+    streams_used = opt.side_streams()
     sustained = mfma_sustained(dev)
     peak = PEAK[args.precision]
     agg, syrk = aggregate(recs, peak)
@@ -311,7 +316,7 @@ def bench_vitb(args):
                    "update_side_streams": args.upd_streams,
                    "parallelism": "none"},
         "gpu_ms_per_step": round(ev_ms, 3),
-        "streams": args.streams,
+        "streams": streams_used,
         "graphs": bool(args.graphs),
         "profile_pass": "per-launch figures (roofline, kernels, launch_classes) from a separate single-stream pass",
         "algorithmic_tflop_per_step": round(flops_step / 1e12, 4),
@@ -358,12 +363,29 @@ def bench_syrk(args):
             C = torch.empty(n, n, device=dev)
             adt = L.dtype_code(dt)
 
-            def syrk():
-                L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n, st))
+            def syrk(stream=st):
+                L.check(L.lib().psgdk_syrk(prec, 0, L.OUT_UPPER, n, n, adt, 1, L.ptrs([A]), n, L.ptrs([C]), n,
+                                           stream))
             for _ in range(3):
                 syrk()
             torch.cuda.synchronize()
             reps = max(20, int(2e10 / (n ** 3)))
+            # graph_us: the same launches replayed from a captured HIP graph, so that the host's per-launch cost
+            # (about 6 us of enqueue and Python) no longer paces a small launch
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(20):
+                    syrk(L.stream_of(A))
+            g.replay()
+            torch.cuda.synchronize()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            for _ in range(5):
+                g.replay()
+            ev[1].record()
+            torch.cuda.synchronize()
+            graph_ms = ev[0].elapsed_time(ev[1]) / 100
+            del g
             # us: back-to-back launches between two events (the per-launch event pairs of the library's profiler,
             # event_us, add a few microseconds of their own to a small launch)
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
@@ -380,7 +402,8 @@ def bench_syrk(args):
             ms_ev = sum(r[3] for r in recs) / len(recs)
             tf = n * (n + 1) * n / (ms * 1e-3) / 1e12
             lines.append({"op": "syrk", "n": n, "k": n, "dtype": name, "us": round(ms * 1e3, 2),
-                          "tflops": round(tf, 2), "frac": round(tf / PEAK[name], 4), "event_us": round(ms_ev * 1e3, 2)})
+                          "tflops": round(tf, 2), "frac": round(tf / PEAK[name], 4), "event_us": round(ms_ev * 1e3, 2),
+                          "graph_us": round(graph_ms * 1e3, 2)})
             B = torch.randn(n, n, device=dev)
             Af = A.float()
             ws = L.Workspace()
@@ -444,10 +467,11 @@ def bench_llama(args):
     torch.cuda.synchronize()
     recs = L.profile_stop()
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
+    opt._nstreams = args.streams
     return {"metric": "Kron update+apply ms/step at Llama shapes (4096x4096 + 4096x14336), 1 GPU", "value": round(ms, 3),
             "unit": "ms/step", "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": args.precision,
             "data": "synthetic", "config": {"workload": "llama-4096x4096+4096x14336-kron-update-apply",
-                                            "max_size": 16384, "max_skew": "inf", "streams": args.streams},
+                                            "max_size": 16384, "max_skew": "inf", "streams": opt.side_streams()},
             "algorithmic_tflop_per_step": round(flops_step / 1e12, 3),
             "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2),
             "launch_classes": launch_classes(recs, 2, PEAK[args.precision], top=8)}
@@ -548,7 +572,7 @@ def bench_e2e(args):
             "loss_first_last": [round(float(losses[0]), 4), round(float(losses[-1]), 4)],
             "dtype": args.precision, "data": "synthetic",
             "config": {"workload": "vit-dim512-depth6-heads8-mlp1024-patch4-batch512-e2e", "params": len(params),
-                       "max_skew": 2, "momentum": 0.9, "streams": args.streams, "graphs": bool(args.graphs)}}
+                       "max_skew": 2, "momentum": 0.9, "streams": opt.side_streams(), "graphs": bool(args.graphs)}}
 
 
 def bench_ceiling(args):
@@ -613,6 +637,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.opt:
+        from psgd_pro_amd import _lib as L
+        for kv in args.opt:
+            k, v = kv.split("=")
+            L.check(L.lib().psgdk_set_option(int(k), int(v)))
     if args.config == "copy":
         print(json.dumps(bench_copy(args)), flush=True)
         return

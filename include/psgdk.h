@@ -307,7 +307,9 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * batches of one side run on different side streams); option 10 = plain-store bf16 GEMMs on k-contiguous operands
  * whose launch has fewer 128 x 128 tiles than this take the small-problem kernel (64 x 64 tiles, k in chunks of 512
  * bytes per row with two in flight); bf16 SYRKs below 1.5 times it and fp32 products below 3 times it (default 128,
- * 0: never; not with a forced tile configuration, option 1). */
+ * 0: never; not with a forced tile configuration, option 1); option 11 = of those, a launch with fewer 64 x 64 tiles
+ * than this takes the tiny-product kernel (32 x 32 tiles whose four waves split k; results rounded in another
+ * order than the other kernels' k-order sums; default 64, 0: never). */
 int psgdk_set_option(int option, int value);
 /* The calling thread's value of a psgdk_set_option switch. */
 int psgdk_get_option(int option, int* value);

@@ -153,8 +153,9 @@ class Workspace:
 
 def kernel_name(kernel_id):
     """Kernel template name of a profiling kernel id."""
-    if kernel_id >= 7000:  # the small-problem kernel: 7000 bf16, 7001 fp32
-        return f"gemm_small_kernel<{'float' if kernel_id % 10 else 'unsigned short'}>"
+    if kernel_id >= 7000:  # the small-problem kernels: 7000 / 7001 64-tiles, 7002 / 7003 tiny (bf16 / fp32)
+        kind = "tiny" if kernel_id % 10 >= 2 else "small"
+        return f"gemm_{kind}_kernel<{'float' if kernel_id % 2 else 'unsigned short'}>"
     if kernel_id >= 5000:  # 5000 (bf16) or 6000 (fp32 k-contiguous) + 10 cfg + epilogue
         base = 6000 if kernel_id >= 6000 else 5000
         cfg, epi = divmod(kernel_id - base, 10)

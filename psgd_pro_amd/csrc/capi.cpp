@@ -235,6 +235,8 @@ thread_local int g_big_batch = MAXB;  // option 9: items per batch of the groupe
 thread_local int g_small = 128;       // option 10: bf16 plain-store GEMMs with fewer 128 x 128 tiles than this (over
                                       // the launch) take the small-problem kernel; bf16 SYRKs below 1.5 times it, fp32
                                       // products below 3 times it (0: never)
+thread_local int g_tiny = 64;         // option 11: of those, launches with fewer 64 x 64 tiles than this take the
+                                      // tiny-product kernel (32-tiles, k split over the four waves; 0: never)
 
 // Side streams (default priority, non-blocking) and events of the grouped update, created once per device and kept
 // until the process ends. A call forks from the caller's stream with an event and joins back with one event per
@@ -327,14 +329,18 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   const int64_t t128 = (int64_t)gemm_bf16_tiles(M, N, tri, 1) * nb;
   const int64_t small_max = esz == 4 ? 3 * (int64_t)g_small : tri ? 3 * (int64_t)g_small / 2 : g_small;
   const bool small = e.epi == EPI_STORE && !kbeg && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 && t128 < small_max;
-  if (ntiles) *ntiles = small ? gemm_small_tiles(M, N, tri) : gemm_bf16_tiles(M, N, tri, cfg);
+  // ... and one whose 64-tiles would still fill only a fraction of the CUs: the tiny-product kernel
+  const bool tiny = small && (int64_t)gemm_small_tiles(M, N, tri) * nb < g_tiny;
+  if (ntiles)
+    *ntiles = tiny ? gemm_tiny_tiles(M, N, tri) : small ? gemm_small_tiles(M, N, tri) : gemm_bf16_tiles(M, N, tri, cfg);
   auto launch = [&]() {
+    if (tiny) return gemm_tiny_launch(a, esz, st);
     if (small) return gemm_small_launch(a, esz, st);
     return esz == 4 ? gemm_f32kc_launch(a, cfg, st) : gemm_bf16_launch(a, cfg, st);
   };
   if (!g_prof.on) return hip_check(launch(), "k-contiguous gemm launch");
   ProfRec r;
-  r.kernel_id = small ? 7000 + (esz == 4 ? 1 : 0) : (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
+  r.kernel_id = small ? 7000 + (tiny ? 2 : 0) + (esz == 4 ? 1 : 0) : (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
   r.flops = tri ? (double)M * (M + 1) * K * nb : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * K * nb;
@@ -1100,11 +1106,24 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   const int S = cap != hipStreamCaptureStatusNone ? 1 : std::min<int>(g_upd_streams, std::max<int>(ng, (int)batches.size()));
   SideStreams* ss = nullptr;
   std::unique_lock<std::mutex> ss_lock;
+  // An error return between the fork and the join still joins: the caller's stream then waits for whatever was
+  // queued on the side streams, and a capture sees no unjoined stream.
+  struct Joiner {
+    SideStreams* ss = nullptr;
+    int S = 0;
+    hipStream_t st = nullptr;
+    ~Joiner() {
+      if (!ss) return;
+      for (int i = 0; i < S; ++i)
+        if (hipEventRecord(ss->ev[1 + S + i], ss->s[i]) == hipSuccess) (void)hipStreamWaitEvent(st, ss->ev[1 + S + i], 0);
+    }
+  } joiner;
   if (S > 1) {
     ss_lock = std::unique_lock<std::mutex>(side_stream_mutex());
     PSGDK_TRY(side_streams(S, &ss));
     PSGDK_HIP(hipEventRecord(ss->ev[0], st), "fork");
     for (int i = 0; i < S; ++i) PSGDK_HIP(hipStreamWaitEvent(ss->s[i], ss->ev[0], 0), "fork wait");
+    joiner.ss = ss; joiner.S = S; joiner.st = st;
   }
   auto lane = [&](int i) { return S > 1 ? ss->s[i % S] : st; };
   for (int gi = 0; gi < ng; ++gi) {
@@ -1185,6 +1204,7 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   }
   for (size_t k = 0; k < batches.size(); ++k) PSGDK_TRY(b16_items(batches[k], os[0], nws[k], lane((int)k)));
   if (S > 1) {
+    joiner.ss = nullptr;
     for (int i = 0; i < S; ++i) {
       PSGDK_HIP(hipEventRecord(ss->ev[1 + S + i], ss->s[i]), "join");
       PSGDK_HIP(hipStreamWaitEvent(st, ss->ev[1 + S + i], 0), "join wait");
@@ -2169,6 +2189,11 @@ int psgdk_set_option(int option, int value) {
     g_small = value;
     return PSGDK_OK;
   }
+  if (option == 11) {
+    if (value < 0) return fail(PSGDK_EINVAL, "option 11 (tiny-product kernel threshold) must be >= 0");
+    g_tiny = value;
+    return PSGDK_OK;
+  }
   if (option == 6) {
     if (value < 0 || value > 8) return fail(PSGDK_EINVAL, "option 6 (grouped update side streams) must be 0 .. 8");
     g_upd_streams = value;
@@ -2180,7 +2205,8 @@ int psgdk_set_option(int option, int value) {
 int psgdk_get_option(int option, int* value) {
   if (!value) return fail(PSGDK_EINVAL, "value is null");
   const int* opts[] = {&g_tile_order, &g_force_cfg,   &g_nlb_target, &g_vmm_u, &g_vmm_cols,
-                       &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch, &g_small};
+                       &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch, &g_small,
+                       &g_tiny};
   if (option < 0 || option >= (int)(sizeof opts / sizeof opts[0])) return fail(PSGDK_EINVAL, "unknown option %d", option);
   *value = *opts[option];
   return PSGDK_OK;

@@ -43,5 +43,9 @@ int gemm_bf16_tiles(long long M, long long N, int tri, int cfg);
 // chunks of 512 bytes per row with two chunks in flight (gemm_small.hip).
 hipError_t gemm_small_launch(GB16Args& a, int esz, hipStream_t st);
 int gemm_small_tiles(long long M, long long N, int tri);
+// Tiny products (same contract): 32 x 32 tiles whose four waves split k, fragments loaded straight into registers;
+// launches of more than 8 problems are split (gemm_small.hip).
+hipError_t gemm_tiny_launch(const GB16Args& a, int esz, hipStream_t st);
+int gemm_tiny_tiles(long long M, long long N, int tri);
 
 }  // namespace psgdk

@@ -17,6 +17,7 @@ uploads the normals; draws="device" draws the coins on the CPU (update coin, the
 as psgd_pro_fast.py:482-483), then a 62-bit seed, and the library fills the step's normals on the GPU from it
 (Philox4x32-10 and Box-Muller, psgdk_fill_normal: one launch per dtype buffer).
 """
+import contextlib
 import ctypes
 
 import torch
@@ -51,7 +52,9 @@ class KronWhiten:
     """See the module docstring. Arguments as psgd_pro_fast.KronWhiten; keyword-only extras:
     precision "fp32" | "bf16" (MFMA input precision of the contractions), draws "device" | "host", seed (a private
     CPU generator for the coins and host draws; None = torch's default generator, as the reference), tri (term1 and P
-    kept as upper triangles)."""
+    kept as upper triangles), streams (side streams for the groups' update and apply chains; None: 3 for up to four
+    groups, 4 for more, the faster count measured for each case), graphs (replay captured HIP graphs of the step's
+    device work), fuse_groups, r2."""
 
     def __init__(self, params_with_grad,
                  preconditioner_max_size=float("inf"),
@@ -78,7 +81,7 @@ class KronWhiten:
                  draws="device",
                  seed=None,
                  tri=None,
-                 streams=3,
+                 streams=None,
                  graphs=False,
                  fuse_groups=True):
         self.lr_params = lr_params
@@ -117,9 +120,9 @@ class KronWhiten:
         self._groups = None
         self._ms, self._counter_m = None, 0
         self._ws_upd, self._ws_app, self._ws_bal = L.Workspace(), L.Workspace(), L.Workspace()
-        if int(streams) < 0:
-            raise ValueError("streams: a count >= 0")
-        self._nstreams, self._lanes = int(streams), None
+        if streams is not None and int(streams) < 0:
+            raise ValueError("streams: a count >= 0 or None")
+        self._nstreams, self._lanes = (None if streams is None else int(streams)), None
         self._use_graphs = bool(graphs)
         # one psgdk_kron2d_update_groups call for every bf16-path group: the factor work of all groups is batched
         # by factor side (the same operations as one call per group; larger launches may sum in another order)
@@ -303,12 +306,21 @@ class KronWhiten:
     # and small kernels overlap another's GEMMs. The side streams start after the caller's stream reaches the
     # step and the caller's stream waits for all of them before it continues; results do not depend on the
     # number of streams.
+    def side_streams(self):
+        """The number of side streams the groups' chains use (streams=None: 3 for up to four groups, 4 for more;
+        the runtime serves a process's streams from four hardware queues, and with few groups a fourth side stream
+        only shares a queue (ViT-B, 4 groups: 10.36 against 10.39 ms/step), while many groups of small launches gain
+        from it (the end-to-end ViT's 78 parameters: 1.51 against 1.69 ms per optimizer step))."""
+        ng = len(self._groups) if self._groups else 0
+        n = self._nstreams if self._nstreams is not None else (3 if ng <= 4 else 4)
+        return 0 if ng < 2 else min(n, ng)
+
     def _lanes_for(self, dev):
-        if self._nstreams == 0 or len(self._groups) < 2:
+        if self.side_streams() == 0:
             return [_Lane(None, self._ws_upd, self._ws_app, self._ws_bal)]
-        if self._lanes is None:
+        if self._lanes is None or len(self._lanes) != self.side_streams():
             self._lanes = [_Lane(torch.cuda.Stream(device=dev), L.Workspace(), L.Workspace(), L.Workspace())
-                           for _ in range(min(self._nstreams, len(self._groups)))]
+                           for _ in range(self.side_streams())]
         return self._lanes
 
     def _fork(self, dev):
@@ -325,6 +337,15 @@ class KronWhiten:
             if ln.stream is not None:
                 cur.wait_stream(ln.stream)
 
+    @contextlib.contextmanager
+    def _forked(self, dev):
+        """The side streams forked from the caller's stream; joined back on leaving, also when a call raises."""
+        cur, lanes = self._fork(dev)
+        try:
+            yield cur, lanes
+        finally:
+            self._join(cur, lanes)
+
     @staticmethod
     def _b16(grp):
         """The group takes the library's bf16 path (its b16_group rule): two factors, dense or diagonal with at least
@@ -340,51 +361,49 @@ class KronWhiten:
     def _update(self, srcs, noise, V):
         o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))
         dev = srcs[0].device
-        cur, lanes = self._fork(dev)
-        fused = [g for g in self._groups if self._fuse and self._b16(g)][:L.MAX_GROUPS]
-        rest = [g for g in self._groups if not any(g is f for f in fused)]
-        if fused:
-            ln = lanes[0]
-            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                opts, nzs, vvs = [], [], []
-                for grp in fused:
-                    og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
-                    og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
-                    opts.append(og)
-                    nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
-                    vvs.append(L.ptrs([V[p.index] for p in grp.members]))
-                ng = len(fused)
-                garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
-                oarr = (ctypes.POINTER(L.UpdateOpts) * ng)(*[ctypes.pointer(x) for x in opts])
-                narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
-                varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
-                L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
-                          stream=L.stream_of(srcs[0]))
-        for gi, grp in enumerate(rest):
-            ln = lanes[(gi + (1 if fused else 0)) % len(lanes)]
-            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                s = grp.struct
-                gdt = self._bind_sources(grp, srcs)
-                o.grad_eps = torch.finfo(gdt).eps
-                nz = L.ptrs([noise[p.index] for p in grp.members])
-                vv = L.ptrs([V[p.index] for p in grp.members])
-                L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=ln.ws_upd, device=dev,
-                          stream=L.stream_of(srcs[0]))
-        self._join(cur, lanes)
+        with self._forked(dev) as (cur, lanes):
+            fused = [g for g in self._groups if self._fuse and self._b16(g)][:L.MAX_GROUPS]
+            rest = [g for g in self._groups if not any(g is f for f in fused)]
+            if fused:
+                ln = lanes[0]
+                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                    opts, nzs, vvs = [], [], []
+                    for grp in fused:
+                        og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
+                        og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
+                        opts.append(og)
+                        nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
+                        vvs.append(L.ptrs([V[p.index] for p in grp.members]))
+                    ng = len(fused)
+                    garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
+                    oarr = (ctypes.POINTER(L.UpdateOpts) * ng)(*[ctypes.pointer(x) for x in opts])
+                    narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
+                    varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
+                    L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
+                              stream=L.stream_of(srcs[0]))
+            for gi, grp in enumerate(rest):
+                ln = lanes[(gi + (1 if fused else 0)) % len(lanes)]
+                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                    s = grp.struct
+                    gdt = self._bind_sources(grp, srcs)
+                    o.grad_eps = torch.finfo(gdt).eps
+                    nz = L.ptrs([noise[p.index] for p in grp.members])
+                    vv = L.ptrs([V[p.index] for p in grp.members])
+                    L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=ln.ws_upd, device=dev,
+                              stream=L.stream_of(srcs[0]))
 
     def _balance(self, coins, dev):
         """psgd_pro.py:138-139: balance the factors of every parameter whose coin came up (eager, rare)."""
-        cur, lanes = self._fork(dev)
-        for gi, grp in enumerate(self._groups):
-            flags = [int(coins[p.index]) for p in grp.members]
-            if not any(flags):
-                continue
-            ln = lanes[gi % len(lanes)]
-            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                fl = (ctypes.c_int32 * len(flags))(*flags)
-                L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=ln.ws_bal, device=dev,
-                          stream=torch.cuda.current_stream(dev).cuda_stream)
-        self._join(cur, lanes)
+        with self._forked(dev) as (cur, lanes):
+            for gi, grp in enumerate(self._groups):
+                flags = [int(coins[p.index]) for p in grp.members]
+                if not any(flags):
+                    continue
+                ln = lanes[gi % len(lanes)]
+                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                    fl = (ctypes.c_int32 * len(flags))(*flags)
+                    L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=ln.ws_bal, device=dev,
+                              stream=torch.cuda.current_stream(dev).cuda_stream)
 
     def _apply(self, srcs):
         max_avg, max_el = self.grad_clip_max_amps
@@ -392,17 +411,16 @@ class KronWhiten:
         dev = srcs[0].device
         pre = [torch.empty(p.m, p.n, device=dev, dtype=torch.float32) for p in self._params] \
             if self.capture else None
-        cur, lanes = self._fork(dev)
-        for gi, grp in enumerate(self._groups):
-            ln = lanes[gi % len(lanes)]
-            with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                s = grp.struct
-                self._bind_sources(grp, srcs)
-                prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
-                po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
-                L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=ln.ws_app, device=dev,
-                          stream=L.stream_of(srcs[0]))
-        self._join(cur, lanes)
+        with self._forked(dev) as (cur, lanes):
+            for gi, grp in enumerate(self._groups):
+                ln = lanes[gi % len(lanes)]
+                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
+                    s = grp.struct
+                    self._bind_sources(grp, srcs)
+                    prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
+                    po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
+                    L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=ln.ws_app, device=dev,
+                              stream=L.stream_of(srcs[0]))
         if pre is not None:
             self.pre = [t.view(p.shape) for t, p in zip(pre, self._params)]
 

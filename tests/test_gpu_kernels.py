@@ -108,20 +108,29 @@ def test_gemm_grouped_and_alpha_beta(hip):
 @pytest.mark.parametrize("trans", [False, True])
 @pytest.mark.parametrize("prec", [0, 1])
 def test_syrk(hip, n, k, trans, prec):
+    """Every output mode against float64 within the GEMM bound; the mirrored result exactly symmetric; the upper and
+    mirrored modes (one kernel) bitwise equal on the upper triangle. With the tiny-product kernel off (option 11 = 0)
+    every kernel sums k in order, and the packed mode (the general engine) is bitwise the mirrored one."""
     A = rnd(*((k, n) if trans else (n, k)), seed=n * 7 + k)
     Ad = A.to(DEV)
     X64 = (bf(A) if prec else A).double()
     X64 = X64.T if trans else X64
-    full = K.syrk(Ad, trans, L.OUT_MIRROR, bool(prec))
-    check_gemm_bound(full, X64, X64.T)
-    assert torch.equal(full, full.T)  # mirrored: exactly symmetric
-    up = torch.full((n, n), float("nan"), device=DEV)
-    L.check(hip.psgdk_syrk(prec, int(trans), L.OUT_UPPER, n, k, 0, 1, L.ptrs([Ad]), Ad.stride(0), L.ptrs([up]), n,
-                           L.stream_of(Ad)))
     triu = torch.ones(n, n, dtype=torch.bool, device=DEV).triu()
-    assert torch.equal(up[triu], full[triu])
-    assert bool(torch.isnan(up[~triu]).all())  # the strict lower triangle is not written
+    try:
+        for tiny in (64, 0):
+            assert hip.psgdk_set_option(11, tiny) == 0
+            full = K.syrk(Ad, trans, L.OUT_MIRROR, bool(prec))
+            check_gemm_bound(full, X64, X64.T)
+            assert torch.equal(full, full.T)  # mirrored: exactly symmetric
+            up = torch.full((n, n), float("nan"), device=DEV)
+            L.check(hip.psgdk_syrk(prec, int(trans), L.OUT_UPPER, n, k, 0, 1, L.ptrs([Ad]), Ad.stride(0), L.ptrs([up]),
+                                   n, L.stream_of(Ad)))
+            assert torch.equal(up[triu], full[triu])
+            assert bool(torch.isnan(up[~triu]).all())  # the strict lower triangle is not written
+    finally:
+        hip.psgdk_set_option(11, 64)
     pk = K.syrk(Ad, trans, L.OUT_PACKED, bool(prec))
+    check_gemm_bound(K.unpack(pk, n), X64, X64.T)
     assert torch.equal(pk, K.pack_upper(full))
     assert torch.equal(K.unpack(pk, n), full)
 
@@ -581,22 +590,26 @@ def test_momentum_multi_matches_per_tensor(hip):
                                               ("syrk_mirror", 3, 300, 300, 1032, torch.bfloat16),
                                               ("gemm", 2, 200, 136, 2056, torch.bfloat16),
                                               ("gemm", 1, 64, 64, 8, torch.bfloat16),
+                                              ("gemm", 12, 40, 72, 264, torch.bfloat16),
                                               ("syrk_upper", 1, 512, 512, 512, torch.float32),
                                               ("syrk_mirror", 2, 130, 130, 260, torch.float32),
+                                              ("syrk_mirror", 9, 33, 33, 44, torch.float32),
                                               ("gemm", 4, 130, 260, 524, torch.float32)])
 def test_small_kernel(hip, kind, nb, m, n, k, dt):
     """Products whose 128-tiles would leave most CUs idle take the small-problem kernel (64-tiles, k in chunks of
-    512 bytes per row, option 10): against float64 within the GEMM bound, a SYRK's lower triangle untouched in upper
-    mode, and within the same bound of the pipelined kernel's result (option 10 = 0)."""
+    512 bytes per row, option 10), or, with option 11 above their 64-tile count, the tiny-product kernel (32-tiles,
+    k split over the four waves; launches of more than 8 problems split): each against float64 within the GEMM
+    bound, a SYRK's lower triangle untouched in upper mode, and the pipelined kernel's result (option 10 = 0) within
+    the same bound."""
     prec = 1 if dt == torch.bfloat16 else 0
     dcode = L.dtype_code(dt)
     As = [rnd(m, k, seed=5 * i + 1).to(dt).to(DEV) for i in range(nb)]
     Bs = [rnd(n, k, seed=5 * i + 2).to(dt).to(DEV) for i in range(nb)]
     st = L.stream_of(As[0])
 
-    def run(thr):
+    def run(small, tiny):
         Cs = [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)]
-        assert hip.psgdk_set_option(10, thr) == 0
+        assert hip.psgdk_set_option(10, small) == 0 and hip.psgdk_set_option(11, tiny) == 0
         L.profile_start()
         if kind == "gemm":
             L.check(hip.psgdk_gemm(prec, 0, 1, m, n, k, 1.0, dcode, dcode, nb, L.ptrs(As), k, L.ptrs(Bs), k, 0.0,
@@ -607,23 +620,27 @@ def test_small_kernel(hip, kind, nb, m, n, k, dt):
         recs = L.profile_stop()
         return Cs, recs
     try:
-        small, recs = run(128)
-        pipe, _ = run(0)
+        small, recs_s = run(128, 0)
+        tiny, recs_t = run(128, 1 << 20)
+        pipe, _ = run(0, 0)
     finally:
         hip.psgdk_set_option(10, 128)
-    assert [r[0] for r in recs] == [7000 if prec else 7001], recs
+        hip.psgdk_set_option(11, 64)
+    assert [r[0] for r in recs_s] == [7000 if prec else 7001], recs_s
+    assert {r[0] for r in recs_t} == {7002 if prec else 7003} and len(recs_t) == 1, recs_t
     triu = torch.ones(m, n, dtype=torch.bool).triu()
-    for A, B, C, P in zip(As, Bs, small, pipe):
+    for A, B, C, T, P in zip(As, Bs, small, tiny, pipe):
         X = A.double().cpu()
         Y = X if kind != "gemm" else B.double().cpu()
-        Cc, Pc = C.cpu(), P.cpu()
+        Cc, Tc, Pc = C.cpu(), T.cpu(), P.cpu()
         if kind == "syrk_upper":
-            assert bool(torch.isnan(Cc[~triu]).all()) and not bool(torch.isnan(Cc[triu]).any())
-            Cc, Pc = torch.where(triu, Cc, Cc.T), torch.where(triu, Pc, Pc.T)
+            for Z in (Cc, Tc):
+                assert bool(torch.isnan(Z[~triu]).all()) and not bool(torch.isnan(Z[triu]).any())
+            Cc, Tc, Pc = (torch.where(triu, Z, Z.T) for Z in (Cc, Tc, Pc))
         else:
-            assert not bool(torch.isnan(Cc).any())
-        check_gemm_bound(Cc, X, Y.T)
-        check_gemm_bound(Pc, X, Y.T)
+            assert not bool(torch.isnan(Cc).any()) and not bool(torch.isnan(Tc).any())
+        for Z in (Cc, Tc, Pc):
+            check_gemm_bound(Z, X, Y.T)
 
 
 def test_mfma_rate_kernel(hip):
