@@ -322,19 +322,20 @@ def test_fused_groups_bitwise_identical(hip, r2, skew):
                 assert torch.equal(x, y), key
 
 
+@pytest.mark.parametrize("draws", ["host", "device"])
 @pytest.mark.parametrize("first", [True, False])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
-def test_graph_replay_matches_eager(hip, prec, first):
+def test_graph_replay_matches_eager(hip, prec, first, draws):
     """graphs=True replays captured HIP graphs of the step's device segments; every step must equal the eager
     optimizer bit for bit. 16 steps: momentum's beta settles after 9 (new graph keys until then), the update coin
     (p = 0.5) makes both the update and the apply-only segments replay, and balancing coins forced on steps 11 and
     13 (on both optimizers) run between segments. Between replays the test synchronizes and compares on the
-    device (eager work of its own)."""
+    device (eager work of its own). Host draws and the library's device draws."""
     shapes = [(64, 96), (96, 64), (128, 128), (32,), (64, 96)]
     opts, Ws = [], []
     for graphs in (False, True):
         W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
-        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=11,
+        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws=draws, seed=11,
                          momentum=0.9, precision=prec, preconditioner_update_probability=0.5,
                          update_preconditioner_first=first, graphs=graphs)
         real = opt._draw_update
