@@ -330,10 +330,117 @@ __global__ void __launch_bounds__(256) rform_kernel(const EwArgs a) {
     __syncthreads();  // the next pair rewrites qa, qb, rsq, rmx and red
   }
 }
+// rform_kernel for the layout the optimizer uses: d a multiple of 64, 16-byte aligned rows, R in bf16 only, no
+// trace partials, row statistics for every matrix or for none (STATS). Every iteration issues the same stores on
+// every path, so the wait for the next pair's loads (issued before this pair's stores) leaves the stores in flight:
+// with the branches of the general kernel the compiler cannot count them and waits for them too. The same values;
+// a diagonal pair writes its tile and statistics twice (the same values to the same places), and the pair fetched
+// after a workgroup's last one is clamped to an existing pair and never read.
+template <bool STATS>
+__global__ void __launch_bounds__(256) rform_fast_kernel(const EwArgs a) {
+  constexpr int TP = 65;
+  __shared__ float qa[64 * TP];
+  __shared__ float qb[64 * TP];
+  __shared__ float rsq[2][64], rmx[2][64];
+  const int d = (int)a.m, T = d / 64, np = T * (T + 1) / 2, total = np * a.nb;
+  const long long ld = a.ld;
+  const float sg = (float)a.i0;
+  const int tid = threadIdx.x, c4 = (tid & 15) * 4, r0 = tid >> 4;
+  auto decode = [&](int p, int& b, int& I, int& J) {
+    b = p / np;
+    int t = p % np, i = 0;
+    while (t >= T - i) { t -= T - i; ++i; }
+    I = i;
+    J = i + t;
+  };
+  float pv[2][4][4];
+  auto fetch = [&](int p) {
+    int b, I, J;
+    decode(p, b, I, J);
+    const float* __restrict__ Q = reinterpret_cast<const float*>(a.in[b]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rb = h ? J : I, cb = h ? I : J;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 q = *reinterpret_cast<const float4*>(Q + (long long)(rb * 64 + r0 + 16 * k) * ld + cb * 64 + c4);
+        pv[h][k][0] = q.x; pv[h][k][1] = q.y; pv[h][k][2] = q.z; pv[h][k][3] = q.w;
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) (h ? qb : qa)[(r0 + 16 * k) * TP + c4 + e] = pv[h][k][e];
+  };
+  fetch(blockIdx.x);
+  stage();
+  for (int p = blockIdx.x; p < total; p += gridDim.x) {
+    int b, I, J;
+    decode(p, b, I, J);
+    __syncthreads();  // qa, qb hold pair p
+    const int pn = p + (int)gridDim.x;
+    fetch(pn < total ? pn : total - 1);
+    bf16_t* __restrict__ Rb = reinterpret_cast<bf16_t*>(a.out2[b]);
+    auto emit = [&](const float* src, const float* srct, int rb, int cb, int t) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = r0 + 16 * k;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sg * (srct[(c4 + e) * TP + r] - src[r * TP + c4 + e]);
+        if constexpr (STATS) {
+          float s2 = 0.f, mx = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float q = bf16_to_f32(f32_to_bf16(v[e]));
+            s2 += q * q;
+            mx = fmaxf(mx, fabsf(q));
+          }
+          row16_sum_max(s2, mx);
+          if ((tid & 15) == 0) {
+            rsq[t][r] = s2;
+            rmx[t][r] = mx;
+          }
+        }
+        *reinterpret_cast<uint2*>(Rb + (long long)(rb * 64 + r) * ld + cb * 64 + c4) =
+            make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])), pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
+      }
+    };
+    emit(qa, qb, I, J, 0);
+    emit(qb, qa, J, I, 1);  // a diagonal pair (I = J): the same tile and statistics again
+    __syncthreads();  // rsq, rmx complete; qa, qb no longer read
+    if constexpr (STATS) {
+      float* __restrict__ stt = a.aux[b];
+      const int t = (tid >> 6) & 1, r = tid & 63;  // waves 2, 3 repeat the stores of waves 0, 1
+      const int rb = t ? J : I, cb = t ? I : J, gi = rb * 64 + r;
+      stt[(long long)cb * d + gi] = rsq[t][r];
+      stt[(long long)(T + cb) * d + gi] = rmx[t][r];
+    }
+    stage();  // the next pair (its loads were issued before this pair's stores)
+  }
+}
+
 hipError_t rform_launch(const EwArgs& a, hipStream_t st) {
   const long long T = (a.m + 63) / 64, total = T * (T + 1) / 2 * a.nb;
   if (total > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rform_kernel, dim3((unsigned)(total < RF_GRID ? total : RF_GRID)), dim3(256), 0, st, a);
+  const unsigned grid = (unsigned)(total < RF_GRID ? total : RF_GRID);
+  bool fast = total > 0 && a.m % 64 == 0 && (a.ld & 3) == 0;
+  int stats = -1;
+  for (int b = 0; fast && b < a.nb; ++b) {
+    fast = a.out[b] == nullptr && a.out2[b] != nullptr && a.sc[b] == nullptr &&
+           (reinterpret_cast<uintptr_t>(a.in[b]) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(a.out2[b]) & 7) == 0;
+    const int s_b = a.aux[b] != nullptr;
+    if (stats < 0) stats = s_b;
+    fast = fast && stats == s_b;
+  }
+  if (fast && stats) hipLaunchKernelGGL(rform_fast_kernel<true>, dim3(grid), dim3(256), 0, st, a);
+  else if (fast) hipLaunchKernelGGL(rform_fast_kernel<false>, dim3(grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(rform_kernel, dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
