@@ -462,11 +462,15 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     // register sets; the batch loop is unrolled so that the set index is static). Stores sit behind branches on
     // C / Cb, which the scheduler does not move loads across, so without this each wave would have only one
     // iteration's loads in flight and the epilogue would run at the latency of HBM.
-    auto row_pass_fast = [&]() {
+    // hc, hcb: whether C / Cb are stored, as types when the epilogue loads X1 (then every iteration issues the same
+    // stores on every path, so the compiler counts them and each wait covers the one load it needs; with the
+    // stores behind branches it cannot, and from the middle of the pass on its waits also cover earlier stores)
+    auto row_pass_fast = [&](auto hc, auto hcb) {
       // (two fp32 operands in flight take 4 iterations ahead, within the register budget)
       constexpr int IT = HR * (WC / 4) / 64, U = EPI == EPI_PROC ? 4 : 8, NBT = IT / U;
       static_assert(IT % U == 0, "row pass: whole batches");
       constexpr bool L1 = EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE;
+      constexpr int HC = decltype(hc)::value, HCB = decltype(hcb)::value;  // 1 stored, 0 not, -1 known at run time
       float4 x1[2][U], x2[2][U];
       auto issue = [&](int set, int it0) {
 #pragma unroll
@@ -496,9 +500,9 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
         epi_math(v, q1, q2, ok, row, col);
         if constexpr (EPI == EPI_STRACE) t2 += v[0] * q1[0] + v[1] * q1[1] + v[2] * q1[2] + v[3] * q1[3];
         *reinterpret_cast<float4*>(ep + ei(lr, lc)) = make_float4(v[0], v[1], v[2], v[3]);
-        if (C)
+        if (HC == 1 || (HC < 0 && C))
           *reinterpret_cast<float4*>(C + (long long)row * p.ldc + col) = make_float4(v[0], v[1], v[2], v[3]);
-        if (Cb)
+        if (HCB == 1 || (HCB < 0 && Cb))
           *reinterpret_cast<uint2*>(Cb + (long long)row * p.ldcb + col) =
               make_uint2(pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1])), pack2(f32_to_bf16(v[2]), f32_to_bf16(v[3])));
       };
@@ -671,8 +675,20 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       else tcol_pass(std::false_type{});
       __syncthreads();
     }
-    if (fast) row_pass_fast();
-    else row_pass();
+    if (fast) {
+      using I1 = std::integral_constant<int, 1>;
+      using I0 = std::integral_constant<int, 0>;
+      if constexpr (EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE) {
+        if (C && Cb) row_pass_fast(I1{}, I1{});
+        else if (C) row_pass_fast(I1{}, I0{});
+        else if (Cb) row_pass_fast(I0{}, I1{});
+        else row_pass_fast(I0{}, I0{});
+      } else {
+        row_pass_fast(std::integral_constant<int, -1>{}, std::integral_constant<int, -1>{});
+      }
+    } else {
+      row_pass();
+    }
     __syncthreads();
     if (colpass) {
       if (fast) col_pass(std::true_type{});
