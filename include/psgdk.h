@@ -273,7 +273,8 @@ int psgdk_fill_normal(void* out, int64_t n, int dtype, uint64_t seed, uint64_t s
  * waits for the recorded events and fills one record per launch: the kernel instantiation id
  * (general engine: cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype, cfg 0 = 128 x 128 tiles, 1 = 32 x 128;
  * bf16 engine: 5000 + cfg * 10 + epilogue, cfg 0 = 256 x 256 tiles on 8 waves, 1 = 128 x 128 on 4, 2 = 256 x 256
- * on 4), whether it was a
+ * on 4; its fp32 twin: 6000 + cfg * 10 + epilogue; the small-problem kernels: 7000 / 7001 on 64 x 64 tiles, 7002 / 7003
+ * the tiny-product kernel, bf16 / fp32 operands), whether it was a
  * SYRK (triangular grid), the problems in the launch, its device time, its algorithmic flop count (SYRK n(n+1)k,
  * TRMM n(n+1)p, GEMM 2mnk, per problem) and its algorithmic bytes (operands read once, outputs written once). With out NULL only *n_records is set (records kept). */
 typedef struct psgdk_prof_record {
