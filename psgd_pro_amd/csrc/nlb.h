@@ -18,7 +18,9 @@ struct NlbArgs {
                             // ksplit x 32 x n partial products
   int vmm_cols;             // full path: 1 = one workgroup per 64 output columns over the whole k range (no
                             // partials, ssc = 64); 2 = the same with A staged through LDS in row-contiguous
-                            // runs; 0 = split-K products plus a reduce kernel (ssc = 128)
+                            // runs; 3 = square bf16 matrices read from their upper 64-tiles in
+                            // tournament-paired rounds (ssc = 64); 0 = split-K products plus a reduce kernel
+                            // (ssc = 128)
   int kdim;                 // column kernel: k extent of a rectangular product (0: n)
   int plain;                // column kernel: no row scale and no sums of squares
   long long lda;

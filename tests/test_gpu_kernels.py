@@ -250,14 +250,16 @@ def nlb_full(As, Vs, sign):
                                    (3072, 0)])
 @pytest.mark.parametrize("sign", [1, -1])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("cols,target", [(-1, 1024), (1, 1024), (2, 1024), (0, 1), (0, 1024), (0, 1 << 20)],
-                         ids=["auto", "cols", "rows", "split1", "split1024", "splitmax"])
+@pytest.mark.parametrize("cols,target", [(-1, 1024), (1, 1024), (2, 1024), (3, 1024), (0, 1), (0, 1024),
+                                         (0, 1 << 20)],
+                         ids=["auto", "cols", "rows", "tri", "split1", "split1024", "splitmax"])
 def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, target):
     """Full-storage bound (psgd_pro.py:19-65) of two matrices in one call, against the float64 oracle on the same
     (storage-rounded) matrices. cols = 1: the column-block V A kernel where the layout allows it (n and lda
     multiples of 16 bytes: fp32 n = 100 with a ragged last block, 768, 1000, 3072), else the split-K kernel;
     cols = 2: the same with A staged through LDS (n = 1000: ragged last k chunk and column block; fp32 n = 100:
-    one partial chunk); cols = -1: the library's choice by shape;
+    one partial chunk); cols = 3: the kernel that reads the upper 64-tiles only, in tournament-paired rounds (bf16,
+    n a multiple of 128: 768, 3072; else as cols = 2); cols = -1: the library's choice by shape;
     cols = 0: the split-K kernel, whose workgroup target 1 gives one k slice, 2^20 the most slices, 1024 the
     default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path). fp32:
     rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
@@ -321,12 +323,13 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k, cols):
         assert g <= float(torch.linalg.matrix_norm(A, 2)) * (1 + 2e-2)
 
 
-@pytest.mark.parametrize("cols", [-1, 1, 2, 0], ids=["auto", "cols", "rows", "split"])
-def test_norm_lower_bound_full_sixteen_matrices(hip, cols):
-    """A full group (16 matrices, the most one call takes) of 320 x 320 bf16 SPD matrices of different scales:
-    every matrix's bound against the float64 oracle (rel 2e-2), both V A kernels."""
+@pytest.mark.parametrize("n", [320, 384])
+@pytest.mark.parametrize("cols", [-1, 1, 2, 3, 0], ids=["auto", "cols", "rows", "tri", "split"])
+def test_norm_lower_bound_full_sixteen_matrices(hip, cols, n):
+    """A full group (16 matrices, the most one call takes) of n x n bf16 SPD matrices of different scales: every
+    matrix's bound against the float64 oracle (rel 2e-2), every V A kernel (n = 384: six 64-tiles, the
+    tournament-paired kernel with two matrices per XCD)."""
     from oracle.psgd_oracle import norm_lower_bound
-    n = 320
     mats, Vs = [], []
     for b in range(16):
         X = rnd(n, 40 + 8 * b, seed=100 + b)
