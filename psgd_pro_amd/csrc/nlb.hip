@@ -1070,8 +1070,8 @@ hipError_t gram_launch(const GramArgs& a, int stage, hipStream_t st) {
 // 34.5 us against 74.3 us for their full rows. A round stages the tile in LDS as stored (16-byte writes), then wave w
 // multiplies its k quarter of it with one v_mfma_f32_32x32x16_bf16 per 32-column half (V's 32 rows are one M tile;
 // V fragments straight from global memory): a tile (J, s) is [column][k] and its B fragments are 16-byte reads, a
-// tile (s, J) is [k][column] and its fragments are gathered element by element (the 32 lanes of a half read one LDS
-// row, 64 consecutive bytes), the sign folded in. VT_D rounds' loads are in flight, issued unconditionally (loads
+// tile (s, J) is [k][column] and its fragments come from gfx950's transposing LDS reads (ds_read_b64_tr_b16), the
+// sign folded in. VT_D rounds' loads are in flight, issued unconditionally (loads
 // past the last round re-read it) so that the compiler can count them; one barrier per round (two LDS buffers). The
 // four waves' partial blocks are summed through LDS in the order w = 0..3, 16 rows at a time, as in vmm_rows_kernel.
 // grid: 8 * ceil(nb / 8) * T (workgroups of matrices past nb exit at once).
@@ -1104,6 +1104,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
   // a round's operands in registers: this thread's two 16-byte pieces of the tile (rows v / 8, chunk v % 8 for
   // v = tid, tid + 256) and this lane's V fragment (row c, k = 64 s + 16 w + 8 h .. + 7)
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // not uint4, whose copies go through memory
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x4_v __attribute__((__vector_size__(4 * sizeof(__bf16))));
+  typedef __attribute__((address_space(3))) bf16x4_v lds_bf16x4;  // an LDS address, as the transposing read takes
   struct Rd {
     u32x4 t0, t1, v;
   };
@@ -1132,11 +1135,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
       u32x4 bf;
       if (J <= s) {  // tile (J, s): row 32 j + c, k = 16 w + 8 h .. + 7
         bf = *reinterpret_cast<const u32x4*>(L + (32 * j + c) * VT_LD + 16 * w + 8 * h);
-      } else {  // tile (s, J): column 32 j + c of rows 16 w + 8 h .. + 7, times sign
-        const bf16_t* const col = L + (16 * w + 8 * h) * VT_LD + 32 * j + c;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          bf[e] = ((uint32_t)col[(2 * e) * VT_LD] | ((uint32_t)col[(2 * e + 1) * VT_LD] << 16)) ^ flip;
+      } else {  // tile (s, J): column 32 j + c of rows 16 w + 8 h .. + 7, times sign, by two transposing reads
+        // (each: 16 lanes read a 4 x 16 block, lane i the 4 elements at row i / 4, columns 4 (i % 4) ..; lane i
+        // receives column i of the block, rows 0..3)
+        const int i = lane & 15;
+        const bf16_t* const tb = L + (16 * w + 8 * h + (i >> 2)) * VT_LD + 32 * j + 16 * (c >> 4) + 4 * (i & 3);
+        const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)tb));
+        const u32x2 hi =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tb + 4 * VT_LD)));
+        bf = u32x4{lo[0], lo[1], hi[0], hi[1]} ^ flip;
       }
       acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, x.v), __builtin_bit_cast(bf16x8_t, bf),
                                                        acc[j], 0, 0, 0);
