@@ -106,8 +106,8 @@ int psgdk_norm_lower_bound(int64_t n, int sign, int nb, const float* const* A, i
 
 /* Norm lower bound of the fully stored SPD (sign +1) or skew-symmetric (sign -1) n x n matrix A (row-major, lda;
  * a_dtype PSGDK_F32 or PSGDK_BF16; both triangles stored: the row-norm pass reads both, and with bf16 storage and
- * n a multiple of 128 the products V A read the upper 64 x 64 tiles only, option 4), random start V (32 x n fp32);
- * out[b] (device, one float) receives the bound. With bf16 storage the products V A run in bf16 with fp32
+ * n a multiple of 128 the products V A may read the upper 64 x 64 tiles only, option 4), random start V (32 x n
+ * fp32); out[b] (device, one float) receives the bound. With bf16 storage the products V A run in bf16 with fp32
  * accumulation.
  * Replaces norm_lower_bound_spd / _skh (psgd_pro.py:19-41, :43-65) on full matrices. */
 int psgdk_norm_lower_bound_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda, int a_dtype,
@@ -297,7 +297,7 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * waves; other values are refused); option 2 = workgroups
  * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of the V A
  * kernels (2, 4 or 8; default 4; the column-block kernel takes 2 or 4); option 4 = the V A kernel of full-storage
- * norm bounds (-1 by shape: 3 where it applies, else 2; 0 split-K products plus a reduce kernel, 1 one workgroup
+ * norm bounds (-1 by shape: 3 for bf16 launches of at least 16 matrices and 512 workgroups, else 2; 0 split-K products plus a reduce kernel, 1 one workgroup
  * per 64 output columns over the whole k range, 2 the same with A staged through LDS in row-contiguous runs, 3 bf16
  * matrices of an even number of 64-tiles read from their upper tiles only, in tournament-paired rounds (else as 2);
  * shapes the column kernels cannot read take the split-K kernel); option 5 = how the bf16 update

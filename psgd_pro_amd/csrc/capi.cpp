@@ -225,10 +225,11 @@ thread_local int g_tile_order = 2;  // option 0: 0 problem-major, 1 XCD-contiguo
 thread_local int g_force_cfg = -1;  // option 1: -1 by size, else the bf16 kernel's tile config
 thread_local int g_nlb_target = 1024;  // option 2: workgroups per full-storage V A product (split-K target)
 thread_local int g_vmm_u = 4;          // option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
-thread_local int g_vmm_cols = -1;      // option 4: V A kernel: -1 by shape (3 where it applies, else 2 where the
-                                       // layout holds, else 0), 0 split-K + reduce, 1 column blocks, 2 column
-                                       // blocks with A staged in LDS, 3 upper tiles only in tournament-paired
-                                       // rounds (bf16 full-storage matrices of an even number of 64-tiles; else 2)
+thread_local int g_vmm_cols = -1;      // option 4: V A kernel: -1 by shape (3 for bf16 launches of >= 16
+                                       // matrices and >= 512 workgroups, else 2 where the layout holds, else 0),
+                                       // 0 split-K + reduce, 1 column blocks, 2 column blocks with A staged in LDS,
+                                       // 3 upper tiles only in tournament-paired rounds (bf16 full-storage
+                                       // matrices of an even number of 64-tiles; else 2)
 thread_local int g_t1q_pg = 1;  // option 5: bf16 update forms term1 Q through Pg where cheaper (1) or never (0)
 thread_local int g_upd_streams = 3;  // option 6: side streams of psgdk_kron2d_update_groups (0: the caller's only)
 thread_local int g_rq16 = 1;   // option 7: the bf16 update keeps R Q in bf16 (1) or fp32 (0) for the Q update
@@ -526,8 +527,11 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
   nlb_full_plan(n, nb, w.part_cols, a.ksplit, a.kslice);
   a.vmm_u = g_vmm_u;
   a.vmm_cols = g_vmm_cols != 0 && vmm_cols_ok(n, nb, A, lda, a_bf16 ? 2 : 4, w) ? (g_vmm_cols != 1 ? 2 : 1) : 0;
-  // bf16 matrices of an even number of 64-tiles: the kernel that reads the upper tiles only (option 4 = -1 or 3)
-  if (a.vmm_cols == 2 && a_bf16 && n % 128 == 0 && (g_vmm_cols == -1 || g_vmm_cols == 3)) a.vmm_cols = 3;
+  // bf16 matrices of an even number of 64-tiles: the kernel that reads the upper tiles only. It keeps a matrix on
+  // one XCD, so by shape (option 4 = -1) it takes launches of at least 16 matrices (two per XCD or more) and 512
+  // workgroups; smaller sets ran faster on the row kernel (measured crossovers), and option 4 = 3 forces it.
+  const bool tri_ok = a.vmm_cols == 2 && a_bf16 && n % 128 == 0;
+  if (tri_ok && (g_vmm_cols == 3 || (g_vmm_cols == -1 && nb >= 16 && (int64_t)nb * (n / 64) >= 512))) a.vmm_cols = 3;
   a.ssc = a.vmm_cols ? 64 : 128;
   if (a.vmm_cols && a.vmm_u == 8) a.vmm_u = 4;
   if (stats_in_part) PSGDK_HIP(nlb_full_launch(a, 3, a_bf16, 0, st), "row norms from partials");

@@ -328,7 +328,8 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k, cols):
 def test_norm_lower_bound_full_sixteen_matrices(hip, cols, n):
     """A full group (16 matrices, the most one call takes) of n x n bf16 SPD matrices of different scales: every
     matrix's bound against the float64 oracle (rel 2e-2), every V A kernel (n = 384: six 64-tiles, the
-    tournament-paired kernel with two matrices per XCD)."""
+    tournament-paired kernel with two matrices per XCD when forced, cols = 3; by shape, 96 workgroups take the row
+    kernel)."""
     from oracle.psgd_oracle import norm_lower_bound
     mats, Vs = [], []
     for b in range(16):
