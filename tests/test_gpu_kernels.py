@@ -246,8 +246,8 @@ def nlb_full(As, Vs, sign):
     return [float(o) for o in outs]
 
 
-@pytest.mark.parametrize("n,pad", [(1, 0), (37, 0), (100, 0), (100, 4), (100, 3), (130, 6), (768, 0), (1000, 8),
-                                   (3072, 0)])
+@pytest.mark.parametrize("n,pad", [(1, 0), (37, 0), (100, 0), (100, 4), (100, 3), (130, 6), (768, 0), (768, 8),
+                                   (1000, 8), (3072, 0)])
 @pytest.mark.parametrize("sign", [1, -1])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("cols,target", [(-1, 1024), (1, 1024), (2, 1024), (3, 1024), (0, 1), (0, 1024),
@@ -261,7 +261,8 @@ def test_norm_lower_bound_full_matches_oracle(hip, n, pad, sign, dtype, cols, ta
     one partial chunk); cols = 3: the kernel that reads the upper 64-tiles only, in tournament-paired rounds (bf16,
     n a multiple of 128: 768, 3072; else as cols = 2); cols = -1: the library's choice by shape;
     cols = 0: the split-K kernel, whose workgroup target 1 gives one k slice, 2^20 the most slices, 1024 the
-    default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path). fp32:
+    default plan. pad > 0 gives lda = n + pad (pad 3: rows not 16-byte aligned, the element-load path; n = 768,
+    pad 8: the upper-tile kernel on a row stride wider than n). fp32:
     rel 1e-5. bf16: the products run on bf16 V and A, rel 2e-2."""
     from oracle.psgd_oracle import norm_lower_bound
     S = _nlb_case(n, sign)
@@ -323,13 +324,13 @@ def test_norm_lower_bound_gram_matches_oracle(hip, d, k, cols):
         assert g <= float(torch.linalg.matrix_norm(A, 2)) * (1 + 2e-2)
 
 
-@pytest.mark.parametrize("n", [320, 384])
+@pytest.mark.parametrize("n", [128, 256, 320, 384])
 @pytest.mark.parametrize("cols", [-1, 1, 2, 3, 0], ids=["auto", "cols", "rows", "tri", "split"])
 def test_norm_lower_bound_full_sixteen_matrices(hip, cols, n):
     """A full group (16 matrices, the most one call takes) of n x n bf16 SPD matrices of different scales: every
-    matrix's bound against the float64 oracle (rel 2e-2), every V A kernel (n = 384: six 64-tiles, the
-    tournament-paired kernel with two matrices per XCD when forced, cols = 3; by shape, 96 workgroups take the row
-    kernel)."""
+    matrix's bound against the float64 oracle (rel 2e-2), every V A kernel (n = 128, 256, 384: two, four and six
+    64-tiles, the tournament-paired kernel with two matrices per XCD when forced, cols = 3, its four-round loop
+    ending after two rounds for n = 128 and 384; by shape these launches take the row kernel)."""
     from oracle.psgd_oracle import norm_lower_bound
     mats, Vs = [], []
     for b in range(16):
