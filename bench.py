@@ -630,8 +630,8 @@ def bench_copy(args):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the preconditioner "
-              f"would shard by parameter across GPUs, which is not part of this build.", file=sys.stderr)
+        print(f"bench.py: measures one GPU only (--gpus {args.gpus} requested); the preconditioner would shard by "
+              f"parameter across GPUs, which is not implemented in psgd_pro_amd.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
