@@ -348,6 +348,40 @@ def test_norm_lower_bound_full_sixteen_matrices(hip, cols, n):
         assert g == pytest.approx(ref, rel=2e-2)
 
 
+@pytest.mark.parametrize("sign", [1, -1])
+def test_norm_lower_bound_full_routing_by_shape(hip, sign):
+    """16 bf16 matrices of 2048 (32 tiles each, 512 workgroups): by shape (option 4 = -1) the launch takes the
+    upper-tile kernel, so its bounds equal the forced upper-tile run (option 4 = 3) bit for bit; the row kernel
+    (option 4 = 2) and both of them match the float64 oracle (rel 2e-2)."""
+    from oracle.psgd_oracle import norm_lower_bound
+    n, mats, Vs = 2048, [], []
+    for b in range(16):
+        if sign > 0:
+            X = rnd(n, 24 + 4 * b, seed=300 + b)
+            S = (0.5 + b) * (X @ X.T)
+        else:
+            Y = rnd(n, 16 + 2 * b, seed=400 + b)
+            Z = rnd(n, 16 + 2 * b, seed=500 + b)
+            S = (0.5 + b) * (Y @ Z.T - Z @ Y.T)
+        mats.append(S.to(torch.bfloat16))
+        Vs.append(rnd(32, n, seed=600 + b))
+    dm, dv = [M.to(DEV) for M in mats], [v.to(DEV) for v in Vs]
+    lib = L.lib()
+    got = {}
+    try:
+        for cols in (-1, 3, 2):
+            assert lib.psgdk_set_option(4, cols) == 0
+            got[cols] = nlb_full(dm, dv, sign)
+    finally:
+        lib.psgdk_set_option(4, -1)
+    assert got[-1] == got[3]
+    assert got[3] != got[2]  # the two kernels sum in different orders: the equality above names the kernel taken
+    for b, (M, V) in enumerate(zip(mats, Vs)):
+        ref = float(norm_lower_bound(M.double(), V.double(), skew=sign < 0))
+        assert got[3][b] == pytest.approx(ref, rel=2e-2)
+        assert got[2][b] == pytest.approx(ref, rel=2e-2)
+
+
 @pytest.mark.parametrize("d,tri", [(64, 0), (130, 0), (256, 0), (130, 1)])
 @pytest.mark.parametrize("L0", [0.0, 7.5])
 def test_factor_update_matches_oracle(hip, d, tri, L0):
