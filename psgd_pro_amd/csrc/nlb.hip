@@ -1084,7 +1084,7 @@ __device__ __forceinline__ int vt_partner(int J, int r, int T) {
   return ((2 * r - J) % (T - 1) + (T - 1)) % (T - 1);
 }
 
-// Five waves per SIMD (the accumulators in arch VGPRs, 94 registers in all): 1280 workgroups fit at once, so 24
+// Five waves per SIMD (the accumulators in arch VGPRs, 96 registers in all): 1280 workgroups fit at once, so 24
 // matrices of 3072 columns (1152 workgroups) run in one round; at four per SIMD 128 of them formed a second round.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) vmm_tri_kernel(const NlbArgs p,
                                                                                                int normalize) {
