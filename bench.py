@@ -57,7 +57,8 @@ def parse_args():
     ap.add_argument("--f32kc", type=int, default=1,
                     help="0: fp32 products on the general engine instead of the k-contiguous kernel's fp32 twin (option 8)")
     ap.add_argument("--vmm", type=int, default=-1,
-                    help="V A kernel of the norm bounds (option 4): -1 by shape, 0 split-K, 1 column blocks, 2 LDS rows")
+                    help="V A kernel of the norm bounds (option 4): -1 by shape, 0 split-K, 1 column blocks, 2 LDS rows, "
+                         "3 upper tiles in tournament-paired rounds")
     ap.add_argument("--tile-cfg", type=int, default=-1,
                     help="bf16 GEMM tile configuration for every launch (library option 1; -1: chosen by size)")
     ap.add_argument("--upd-streams", type=int, default=3,
