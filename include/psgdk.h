@@ -291,7 +291,8 @@ int psgdk_profile_start(void);
 int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);
 
 /* Tuning switches, one set per host thread (a thread's settings apply to the calls it makes and never change
- * another thread's results; a new thread starts from the defaults): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
+ * another thread's results; a new thread starts from the defaults, so a switch set on one thread does not reach
+ * calls that other threads make, such as a framework's worker threads): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
  * XCD, 2 = 1 with tile rows grouped by 4 so that the tiles an XCD runs at once share operand panels; default 2);
  * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256 on 8 waves, 1 = 128 x 128, 2 = 256 x 256 on 4
  * waves; other values are refused); option 2 = workgroups

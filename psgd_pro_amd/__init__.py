@@ -7,6 +7,6 @@ HipOps is the drop-in for its arithmetic plugin (kernels/ops.py make_ops). Both 
 `python -m psgd_pro_amd.build`.
 """
 from .kron import KronWhiten
-from .ops import HipOps, make_ops
+from .ops import EagerOps, HipOps, make_ops
 
-__all__ = ["KronWhiten", "HipOps", "make_ops"]
+__all__ = ["KronWhiten", "EagerOps", "HipOps", "make_ops"]

@@ -3,6 +3,13 @@
     python -m psgd_pro_amd.build [--jobs N]
 
 Objects go to psgd_pro_amd/_build/; sources are compiled in parallel and the library is linked with hipcc.
+
+    python -m psgd_pro_amd.build --asan
+
+also builds psgd_pro_amd/_build/libpsgdk_asan.so: the same library with its host code (capi.cpp, the C ABI's
+argument checks, workspace planning and launch set-up) built with AddressSanitizer, for the CPU tests that drive the
+C ABI without a GPU (tests/test_asan_cpu.py loads it with the sanitizer runtime preloaded). Device code is built as
+usual; the sanitizer applies to host code only.
 """
 import argparse
 import concurrent.futures as cf
@@ -34,7 +41,39 @@ def _compile(src):
     return obj, err
 
 
-def build(jobs=None, verbose=False):
+ASAN_LIB = os.path.join(BUILD, "libpsgdk_asan.so")
+# host-only sanitizer flags (each -fsanitize= applies to the host pass through -Xarch_host)
+ASAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def asan_runtime():
+    """Path of the compiler's AddressSanitizer runtime (to preload into a Python that loads ASAN_LIB)."""
+    r = subprocess.run([HIPCC, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = r.stdout.strip()
+    if not os.path.isabs(path) or not os.path.exists(path):
+        lib_dir = subprocess.run([HIPCC, "-print-runtime-dir"], capture_output=True, text=True).stdout.strip()
+        path = os.path.join(lib_dir, "libclang_rt.asan-x86_64.so")
+    return path
+
+
+def build_asan(objects):
+    """capi.cpp with the host sanitizer, linked with the other (regular) objects into ASAN_LIB."""
+    obj = os.path.join(BUILD, "capi_asan.o")
+    cmd = [HIPCC, "-O1", "-g", *[f for f in COMMON if f != "-O3"], *DEVICE_FLAGS, *ASAN_HOST, "-c",
+           os.path.join(CSRC, "capi.cpp"), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stderr}")
+    others = [o for o in objects if os.path.basename(o) != "capi.o"]
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-Xarch_host", "-fsanitize=address", "-shared-libasan",
+           "-o", ASAN_LIB, obj, *others]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
+    return ASAN_LIB
+
+
+def build(jobs=None, verbose=False, asan=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(jobs) as ex:
@@ -48,6 +87,8 @@ def build(jobs=None, verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, LIB)
+    if asan:
+        build_asan([o for o, _ in results])
     return LIB
 
 
@@ -55,5 +96,6 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--asan", action="store_true", help="also build the host-sanitized library for the CPU tests")
     a = ap.parse_args()
-    print(build(a.jobs, a.verbose))
+    print(build(a.jobs, a.verbose, a.asan))

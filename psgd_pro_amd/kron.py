@@ -23,7 +23,7 @@ import ctypes
 import torch
 
 from . import _lib as L
-from .ops import make_ops
+from .ops import EagerOps
 
 _K = L.NLB_K
 
@@ -49,12 +49,28 @@ class _Group:
 
 
 class KronWhiten:
-    """See the module docstring. Arguments as psgd_pro_fast.KronWhiten; keyword-only extras:
-    precision "fp32" | "bf16" (MFMA input precision of the contractions), draws "device" | "host", seed (a private
-    CPU generator for the coins and host draws; None = torch's default generator, as the reference), tri (term1 and P
-    kept as upper triangles), streams (side streams for the groups' update and apply chains; None: 3 for up to four
-    groups, 4 for more, the faster count measured for each case), graphs (replay captured HIP graphs of the step's
-    device work), fuse_groups, r2."""
+    """See the module docstring. Arguments as psgd_pro_fast.KronWhiten (psgd_pro_fast.py:245-264):
+
+    ops: a plugin class from make_ops (EagerOps, the reference's default, is make_ops(())). The engine runs its own
+      fused, grouped kernels rather than calling the plugin's methods one by one, and takes from the plugin what
+      changes its arithmetic: the storage form of term1 and P (flags "tri" or "packed": the upper triangle only;
+      "nan" poisons the lower triangle only in what the plugin's own methods return) and "bf16" (bf16 MFMA inputs).
+      The kernel-selection flags (k1, k2, k2t, k2c, k2b, all) choose among the reference's CUDA/Triton/cuBLAS kernels
+      and their size gates; here one HIP kernel set serves every size. A class that make_ops did not build raises
+      TypeError, and a plugin asking for the Q-symmetrization in place of the Procrustes step (qsym) raises
+      NotImplementedError.
+    batch, cache_p, graph_rng, p2d: the reference's execution strategies for the same arithmetic (vmap over
+      same-shape parameters, cached P, graph-captured draws, P kept as state). The engine always groups same-shape
+      parameters, keeps P as state and can draw on the device (draws="device"), whatever these say; the reference's
+      own checks on them (p2d with batch, cache_p with compile) are kept.
+    compile: must be None (no torch.compile).
+
+    Keyword-only extras: precision "fp32" | "bf16" (MFMA input precision of the contractions), draws "device" |
+    "host", seed (a private CPU generator for the coins and host draws; None = torch's default generator, as the
+    reference), tri (term1 and P kept as upper triangles), streams (side streams for the groups' update and apply
+    chains; None: 3 for up to four groups, 4 for more, the faster count measured for each case), fuse_groups, and
+    graphs, which must stay False: replaying the step from a captured HIP graph is switched off (a capture of the
+    step aborted the process and the cause is not established)."""
 
     def __init__(self, params_with_grad,
                  preconditioner_max_size=float("inf"),
@@ -70,11 +86,11 @@ class KronWhiten:
                  update_preconditioner_first=True,
                  whiten_grad=True,
                  compile=None,
-                 ops=None,
+                 ops=EagerOps,
                  batch=False,
                  cache_p=False,
                  graph_rng=False,
-                 p2d=True,
+                 p2d=False,
                  r2=False,
                  *,
                  precision=None,
@@ -100,17 +116,31 @@ class KronWhiten:
         self._whiten_grad = whiten_grad
         if not whiten_grad:
             assert self.momentum > 0, "Cannot whiten momentum if the momentum setting is invalid."
+        assert not (cache_p and compile is not None), "cache_p relies on tensor version counters: eager only"
+        assert not (p2d and batch), "p2d keeps per-parameter P state; batch stacks parameters"
         if compile is not None:
             raise ValueError("compile: the HIP engine runs without torch.compile (pass compile=None)")
+        if graphs:
+            raise NotImplementedError(
+                "graphs=True: replaying the step from a captured HIP graph is switched off. A capture of the step's "
+                "device work (side streams forked inside torch.cuda.graph) aborted the process, and the cause is not "
+                "established; the step runs its launches eagerly")
         self._r2 = bool(r2)  # procrustes_step_r2 (psgd_pro_fast.py:141-153) instead of procrustes_step2
-        flags = getattr(ops, "flags", frozenset()) if ops is not None else frozenset()
-        self.ops = ops if ops is not None else make_ops(())
+        if ops is None:
+            ops = EagerOps
+        if not getattr(ops, "_psgdk", False):
+            raise TypeError(f"ops: {getattr(ops, '__name__', ops)!r} was not built by psgd_pro_amd.make_ops; the "
+                            "engine runs its own fused kernels and cannot call another plugin's methods")
+        if getattr(ops, "qsym", False):
+            raise NotImplementedError("ops.qsym: the Q-symmetrization in place of the Procrustes step is not built")
+        flags = ops.flags
+        self.ops = ops
         if precision is None:
             precision = "bf16" if "bf16" in flags else "fp32"
         if precision not in ("fp32", "bf16"):
             raise ValueError("precision: 'fp32' or 'bf16'")
         self._prec = L.PREC_BF16 if precision == "bf16" else L.PREC_F32
-        self._tri = (3 if ("tri" in flags) else 0) if tri is None else (3 if tri else 0)
+        self._tri = (3 if flags & {"tri", "packed"} else 0) if tri is None else (3 if tri else 0)
         if draws not in ("device", "host"):
             raise ValueError("draws: 'device' or 'host'")
         self._draws = draws
@@ -123,11 +153,9 @@ class KronWhiten:
         if streams is not None and int(streams) < 0:
             raise ValueError("streams: a count >= 0 or None")
         self._nstreams, self._lanes = (None if streams is None else int(streams)), None
-        self._use_graphs = bool(graphs)
         # one psgdk_kron2d_update_groups call for every bf16-path group: the factor work of all groups is batched
         # by factor side (the same operations as one call per group; larger launches may sum in another order)
         self._fuse = bool(fuse_groups)
-        self._graphs, self._seen = {}, set()
         self._draw_buf = self._draw_buf16 = None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
@@ -457,18 +485,18 @@ class KronWhiten:
         # device work in segments; the balancing coins act between them, as in psgd_pro.py:138-139 (inside the
         # update, so before the apply when the update comes first)
         first = update and self.update_preconditioner_first
-        self._segment("pre", grads, beta, first, not first, noise, V)
+        self._device_work(grads, beta, first, not first, noise, V)
         if first and any(coins):
             self._balance(coins, dev)
         if first:
-            self._segment("apply", grads, None, False, True, None, None)
+            self._device_work(grads, None, False, True, None, None)
         elif update:
-            self._segment("update", grads, None, True, False, noise, V)
+            self._device_work(grads, None, True, False, noise, V)
             if any(coins):
                 self._balance(coins, dev)
 
     def _device_work(self, grads, beta, do_update, do_apply, noise, V):
-        """Momentum (when beta is given), preconditioner update, apply: kernel launches only (capturable)."""
+        """Momentum (when beta is given), preconditioner update, apply: kernel launches only."""
         if beta is not None:  # every parameter's momentum in one launch per 64 tensors
             for c in range(0, len(grads), L.MAX_TENSORS):
                 ch = range(c, min(c + L.MAX_TENSORS, len(grads)))
@@ -483,47 +511,6 @@ class KronWhiten:
             self._apply(self._ms if self.momentum > 0 else grads)
         if do_update and not self.update_preconditioner_first:
             self._update(src, noise, V)
-
-    def _segment(self, kind, grads, beta, do_update, do_apply, noise, V):
-        """Runs one segment of device work eagerly, or (graphs=True) replays a captured HIP graph of it. A
-        graph bakes in its launch arguments, so it is keyed by every host value they take (segment, momentum
-        beta, learning rates, betaL, damping, clip amplitudes); a key is captured the second time it is seen
-        (the first run is eager and sizes the workspaces), and a new value simply captures a new graph."""
-        if not self._use_graphs:
-            self._device_work(grads, beta, do_update, do_apply, noise, V)
-            return
-        key = (kind, beta, do_update, do_apply, self.lr_params, self.lr_preconditioner, self.betaL, self.damping,
-               tuple(self.grad_clip_max_amps), tuple((g.dtype, tuple(g.shape)) for g in grads))
-        rec = self._graphs.get(key)
-        if rec is None and key not in self._seen:
-            self._seen.add(key)
-            self._device_work(grads, beta, do_update, do_apply, noise, V)
-            return
-        if rec is None:
-            rec = self._capture(key, grads, beta, do_update, do_apply, noise, V)
-        for s_g, g in zip(rec["grads"], grads):
-            s_g.copy_(g)
-        rec["graph"].replay()
-
-    def _capture(self, key, grads, beta, do_update, do_apply, noise, V):
-        dev = grads[0].device
-        static = [g.clone() for g in grads]
-        # the graph owns workspaces allocated during its capture (fixed addresses, never freed while it lives)
-        saved = (self._ws_upd, self._ws_app, self._ws_bal, self._lanes)
-        self._ws_upd, self._ws_app, self._ws_bal = L.Workspace(), L.Workspace(), L.Workspace()
-        if self._lanes is not None:
-            self._lanes = [_Lane(ln.stream, L.Workspace(), L.Workspace(), L.Workspace()) for ln in self._lanes]
-        lanes_used = self._lanes
-        torch.cuda.synchronize(dev)
-        g = torch.cuda.CUDAGraph()
-        try:
-            with torch.cuda.graph(g):
-                self._device_work(static, beta, do_update, do_apply, noise, V)
-            rec = {"graph": g, "grads": static, "ws": (self._ws_upd, self._ws_app, self._ws_bal, lanes_used)}
-        finally:
-            self._ws_upd, self._ws_app, self._ws_bal, self._lanes = saved
-        self._graphs[key] = rec
-        return rec
 
     @torch.no_grad()
     def step(self, closure):
@@ -580,7 +567,15 @@ class KronWhiten:
         for k, v in st["hyper"].items():
             setattr(self, k, v)
         self._counter_m = st["counter_m"]
-        self._ms = [m.clone() for m in st["momentum_buffers"]] if st["momentum_buffers"] is not None else None
+        saved = st["momentum_buffers"]
+        if saved is None:
+            self._ms = None
+        elif self._ms is not None and [tuple(m.shape) for m in self._ms] == [tuple(m.shape) for m in saved]:
+            for m, v in zip(self._ms, saved):  # into the existing buffers: their addresses stay valid
+                m.copy_(v)
+        else:
+            dev = self._params_with_grad[0].device
+            self._ms = [v.to(device=dev, dtype=torch.float32, copy=True) for v in saved]
         if st["generator"] is not None:
             if self._gen is None:
                 self._gen = torch.Generator()

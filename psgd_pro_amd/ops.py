@@ -6,11 +6,8 @@ make_ops(flags) in kernels/ops.py:142-215), and the custom ops under it (kernels
 torch.library custom ops in the "psgdk" namespace with fake implementations. Every op runs on the HIP kernels of
 libpsgdk.so; there is no CPU or eager fallback for the 2-D contractions (inputs must be CUDA tensors).
 
-make_ops flags (subset of kernels/ops.py:1-13, re-read for one kernel set that covers every size):
-  tri     term1 and P keep their upper triangle only; every consumer reads the triangle (symm, norm bounds)
-  nan     with tri: the strict lower triangle of term1 / P is filled with NaN (proves no reader touches it)
-  packed  term1 and P are returned as packed upper triangles (n(n+1)/2); consumers unpack
-  bf16    contractions take bfloat16 inputs (fp32 accumulate); default fp32
+make_ops flags: the reference's set (kernels/ops.py:1-13: k1, k2, k2t, k2c, k2b, all, tri, nan, packed) and bf16;
+make_ops's docstring gives what each one selects here.
 """
 import torch
 from torch import Tensor
@@ -223,27 +220,39 @@ def _(Pk, n):
 
 
 def side(S):
-    """n of a symmetric matrix in storage form (square, or packed with n(n+1)/2 values) (kernels/ops.py:119-121)."""
+    """Side n of a symmetric matrix held square (n x n) or as its packed upper triangle: T = n(n+1)/2 values give
+    n = (sqrt(8T + 1) - 1) / 2 (kernels/ops.py:119-121)."""
     return S.shape[0] if S.dim() == 2 else int(((8 * S.shape[0] + 1) ** 0.5 - 1) / 2)
 
 
 def pack_upper(A):
-    """Row-major packed upper triangle of a square matrix (kernels/k1.py:40-43)."""
+    """The packed storage form of square A: its upper triangle, diagonal included, read row by row (element (i, j),
+    j >= i, lands at i n - i(i-1)/2 + j - i) (kernels/k1.py:40-43)."""
     iu = torch.triu_indices(A.shape[0], A.shape[0], device=A.device)
     return A[iu[0], iu[1]].contiguous()
 
 
+# The reference's flag vocabulary (kernels/ops.py:1-13,139-215) and this package's own "bf16".
+REFERENCE_FLAGS = frozenset({"k1", "k2", "k2t", "k2c", "k2b", "all", "tri", "nan", "packed"})
+FLAGS = REFERENCE_FLAGS | {"bf16"}
+
+
 def make_ops(flags=()):
-    """The ops class for psgd_pro_fast-style callers (kernels/ops.py:142-215): every method runs on the HIP kernels.
-    See the module docstring for the flags."""
+    """The ops class for psgd_pro_fast-style callers (kernels/ops.py:142-215); every method runs on the HIP kernels.
+
+    Every flag set the reference accepts is accepted, with its check that tri comes with k1 (AssertionError
+    otherwise). The kernel-selection flags (k1: norm bounds, k2 / k2t / k2c / k2b: the SYRK variants, all: no
+    size gates) choose among the reference's CUDA, Triton and cuBLAS kernels and the sizes from which each takes
+    over from eager torch; here one HIP kernel set covers every method at every size, so they select nothing more.
+    The storage flags keep their meaning: tri (term1 and P as upper triangles, read as triangles by symm / symm_r /
+    the norm bounds), nan (with tri: the strict lower triangle returned as NaN), packed (term1 and P as packed upper
+    triangles; takes precedence over tri for what sym returns). bf16: contractions take bfloat16 inputs (fp32
+    accumulate). Flags outside this vocabulary raise ValueError."""
     flags = frozenset(flags)
-    unknown = flags - {"tri", "nan", "packed", "bf16"}
+    unknown = flags - FLAGS
     if unknown:
-        raise ValueError(f"unknown flags {sorted(unknown)}")
-    if "nan" in flags and "tri" not in flags:
-        raise ValueError("nan needs tri")
-    if "packed" in flags and "tri" in flags:
-        raise ValueError("packed and tri are alternative storage forms")
+        raise ValueError(f"unknown flags {sorted(unknown)}; known: {sorted(FLAGS)}")
+    assert "tri" not in flags or "k1" in flags, "tri needs k1 (term1's only other reader)"
     bf = "bf16" in flags
     tri = "tri" in flags
     packed = "packed" in flags
@@ -269,7 +278,9 @@ def make_ops(flags=()):
     def gram(Pg, i, expr):
         if Pg.dim() != 2:
             return expr(Pg, Pg)  # the caller's own contraction for non-matrix gradients (kernels/ops.py:201-204)
-        return sym_store(Pg, i == 1)
+        if tri:
+            return store(syrk(Pg, i == 1, L.OUT_UPPER, bf))
+        return syrk_full(Pg, i == 1)
 
     def symm_l(S, X):
         if S.dim() == 1:
@@ -301,7 +312,9 @@ def make_ops(flags=()):
     HipOps.sym = staticmethod(sym_store if (tri or packed) else syrk_full)
     HipOps.qsym = False
     HipOps.flags = flags
+    HipOps._psgdk = True  # built here: KronWhiten(ops=...) accepts it
     return HipOps
 
 
-HipOps = make_ops(())
+# The no-flag plugin: the reference's default arithmetic class (psgd_pro_fast.py:106-126), on the HIP kernels.
+HipOps = EagerOps = make_ops(())

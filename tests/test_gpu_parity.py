@@ -322,6 +322,12 @@ def test_fused_groups_bitwise_identical(hip, r2, skew):
                 assert torch.equal(x, y), key
 
 
+GRAPHS_OFF = ("graphs=True is switched off: a capture of the step (side streams forked inside torch.cuda.graph) "
+              "aborted the process (SIGABRT) on the GPU, after an earlier segfault at capture end, and the cause is "
+              "not established; KronWhiten(graphs=True) raises NotImplementedError")
+
+
+@pytest.mark.skip(reason=GRAPHS_OFF)
 @pytest.mark.parametrize("draws", ["host", "device"])
 @pytest.mark.parametrize("first", [True, False])
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
@@ -476,6 +482,7 @@ def test_clip_passes_non_finite_values_through(hip, bad, shape, skew, prec):
         assert torch.equal(Wg[fin], torch.ones_like(Wg[fin]))
 
 
+@pytest.mark.skip(reason=GRAPHS_OFF)
 @pytest.mark.parametrize("prec", ["fp32", "bf16"])
 def test_graph_replay_tracks_oracle(hip, prec):
     """graphs=True (captured HIP graph segments) against the oracle fed the same draws, 14 steps with momentum 0.9:

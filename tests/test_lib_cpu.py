@@ -259,6 +259,6 @@ def test_python_surface_on_cpu():
     with pytest.raises(RuntimeError, match="CUDA"):
         ops.syrk(torch.zeros(4, 4), False)
     with pytest.raises(ValueError):
-        make_ops({"nan"})
+        make_ops({"k3"})
     with pytest.raises(ValueError):
         KronWhiten([W], compile="default")

@@ -493,3 +493,18 @@ def test_rounded_oracle_reduces_to_oracle_and_scales_with_unit_roundoff(skew, r2
     assert 1e-9 < e32 < 1e-6, e32
     assert 1e-4 < e16 < 2e-2, e16
     assert 1e3 < e16 / e32 < 1e6, (e16, e32)  # bf16 / fp32 unit roundoff = 2^16
+
+
+def test_package_flop_count_matches_the_oracle():
+    """The measurement's FLOP count (psgd_pro_amd.flops, used by bench.py) equals the oracle's on every config shape,
+    dense and diagonal sides, step2 and r2."""
+    from psgd_pro_amd import flops as F
+    shapes = [(1024, 1024), (768, 2304), (768, 768), (768, 3072), (3072, 768), (4096, 4096), (4096, 14336), (77, 5)]
+    for m, n in shapes:
+        for d1 in (True, False):
+            for d2 in (True, False):
+                for r2 in (False, True):
+                    assert F.flops_2d(m, n, d1, d2, r2) == O.flops_2d(m, n, d1, d2, r2)
+        for skew in (1.0, math.inf):
+            for d in (m, n):
+                assert F.is_dense(d, m * n, 8192, skew) == O.is_dense(d, m * n, 8192, skew)
