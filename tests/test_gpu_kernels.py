@@ -468,7 +468,7 @@ def test_hip_ops_plugin_methods(hip):
     assert rel_err_norm(ops.symm_r(Z, S), Z.double().cpu() @ S.double().cpu()) < 1e-6
     q = rnd(96, 96, seed=4).to(DEV)
     assert rel_err_norm(ops.gram_q(q), q.double().cpu().T @ q.double().cpu()) < 1e-6
-    tri = K.make_ops({"tri", "nan"})
+    tri = K.make_ops({"k1", "tri", "nan"})
     T = tri.sym(X, False)
     assert bool(torch.isnan(T.tril(-1)[1:, :1]).all())
     assert rel_err_norm(tri.symm(T, Y), S.double().cpu() @ Y.double().cpu()) < 1e-6
