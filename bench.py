@@ -10,6 +10,7 @@ MFMA path (fp32 accumulate). Synthetic data; weights random-initialised.
     python bench.py [--steps K] [--warmup W] [--precision bf16|fp32] [--skew inf|1] [--no-cpu]
     python bench.py --config syrk      # SYRK / TRMM microbenchmark lines (n = k in 512..4096, fp32 and bf16)
     python bench.py --config ceiling   # hipBLASLt against the library's bf16 GEMM on the optimizer's shapes
+    python bench.py --config gemm      # 12 x 3072^3 bf16 GEMM launches (the dominant kernel), for counter runs
 
 `roofline` is measured live: every MFMA-engine launch in the timed steps is bracketed by HIP events on its stream;
 the dominant kernel instantiation (largest total time) is reported with its algorithmic TFLOP/s against the bf16
@@ -44,7 +45,7 @@ def parse_args():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--skew", default="inf")
     ap.add_argument("--blocks", type=int, default=12)
-    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e", "ceiling"], default="vitb")
+    ap.add_argument("--config", choices=["vitb", "syrk", "copy", "llama", "e2e", "ceiling", "gemm"], default="vitb")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--streams", type=int, default=None,
@@ -114,6 +115,76 @@ def mfma_sustained(dev):
     torch.cuda.synchronize(dev)
     sec = ev[0].elapsed_time(ev[1]) * 1e-3 / 3
     return 4 * wgs * iters * 32 * 16384 / sec / 1e12
+
+
+CLOCK_MHZ = 2400.0  # MI355X peak engine clock: the published MFMA and HBM peaks assume it
+
+
+def read_rates(dev):
+    """The read rates this GPU sustains now (psgdk_read_rate, TB/s): HBM (a 2 GiB buffer read once per launch by 2048
+    workgroups) and the L2 (a 2 MiB buffer read 4096 times by 1024 workgroups, odd stride), median of 5 launches."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    out = {}
+    for name, nbytes, wgs, iters, stride in (("hbm", 2 << 30, 2048, (2 << 30) // 4096 // 2048, 1),
+                                             ("l2", 2 << 20, 1024, 4096, 977)):
+        buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+        sink = torch.zeros(wgs, dtype=torch.int32, device=dev)
+        st = L.stream_of(buf)
+        f = lambda: L.check(L.lib().psgdk_read_rate(C.c_void_p(buf.data_ptr()), nbytes, wgs, iters, stride,
+                                                    C.c_void_p(sink.data_ptr()), st))
+        f()
+        times = []
+        for _ in range(5):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            f()
+            ev[1].record()
+            torch.cuda.synchronize(dev)
+            times.append(ev[0].elapsed_time(ev[1]) * 1e-3)
+        out[name] = round(wgs * iters * 4096 / sorted(times)[2] / 1e12, 2)
+        del buf, sink
+    return out
+
+
+class ClockSampler:
+    """The engine clock over a region of work on `stream`: a one-wave sampler on its own stream records (cycle
+    counter, wall counter) pairs about every 4 us (psgdk_clock_sample) while two wall marks on `stream` bracket the
+    region; the clock is the cycle increment over the wall increment between the first and last samples inside it."""
+
+    def __init__(self, dev, stream, est_ms):
+        import torch
+        from psgd_pro_amd import _lib as L
+        self.L, self.stream = L, stream
+        self.n = int(min(1 << 22, max(1024, est_ms * 1e3 / 2.5 * 1.5)))
+        self.buf = torch.zeros(2 * self.n, dtype=torch.int64, device=dev)
+        self.marks = torch.zeros(2, dtype=torch.int64, device=dev)
+        self.side = torch.cuda.Stream(device=dev)
+        khz = C.c_int(0)
+        L.check(L.lib().psgdk_wall_clock_rate(C.byref(khz)))
+        self.khz = khz.value
+
+    def start(self):
+        raw = lambda st: C.c_void_p(st.cuda_stream)
+        self.side.wait_stream(self.stream)
+        self.L.check(self.L.lib().psgdk_clock_sample(self.n, C.c_void_p(self.buf.data_ptr()), raw(self.side)))
+        self.L.check(self.L.lib().psgdk_wall_mark(C.c_void_p(self.marks.data_ptr()), raw(self.stream)))
+
+    def stop(self):
+        self.L.check(self.L.lib().psgdk_wall_mark(C.c_void_p(self.marks.data_ptr() + 8), C.c_void_p(self.stream.cuda_stream)))
+
+    def result(self):
+        import torch
+        torch.cuda.synchronize()
+        s = self.buf.view(-1, 2).cpu()
+        m0, m1 = (int(x) for x in self.marks.cpu())
+        inside = s[(s[:, 1] >= m0) & (s[:, 1] <= m1)]
+        if len(inside) < 2:
+            return {"mhz": None, "samples": int(len(inside)), "coverage": 0.0}
+        dc = float(inside[-1, 0] - inside[0, 0])
+        dw = float(inside[-1, 1] - inside[0, 1])
+        return {"mhz": round(dc / dw * self.khz / 1e3, 1), "samples": int(len(inside)),
+                "coverage": round(dw / max(1.0, float(m1 - m0)), 3)}
 
 
 def roof_ms(fl, by, peak):
@@ -271,15 +342,22 @@ def bench_vitb(args):
     L.check(L.lib().psgdk_set_option(6, 0))  # the grouped update's side streams too
     opt.step_math(grads)
     torch.cuda.synchronize()
+    # the engine clock over this pass: the published peaks assume CLOCK_MHZ, and the GPU lowers its clock under a
+    # sustained MFMA and memory load
+    clock = ClockSampler(dev, stream, est_ms=1.5 * args.steps * ev_ms + 50)
+    clock.start()
     L.profile_start()
     for _ in range(args.steps):
         opt.step_math(grads)
+    clock.stop()
     torch.cuda.synchronize()
     recs = L.profile_stop()
+    clk = clock.result()
     opt._nstreams = args.streams
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
     streams_used = opt.side_streams()
     sustained = mfma_sustained(dev)
+    rates = read_rates(dev)
     peak = PEAK[args.precision]
     agg, syrk = aggregate(recs, peak)
     kid = max(agg, key=lambda k: agg[k][1])
@@ -338,7 +416,13 @@ def bench_vitb(args):
                      "frac": round(achieved / (PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3), 4),
                      "roof_frac": round(roof_tot / ms_tot, 4), "traffic": traffic,
                      "sustained_peak": round(sustained, 1) if mfma_bound and prec_of == "bf16" else None,
-                     "frac_of_sustained": round(achieved / sustained, 4) if mfma_bound and prec_of == "bf16" else None},
+                     "frac_of_sustained": round(achieved / sustained, 4) if mfma_bound and prec_of == "bf16" else None,
+                     "clock_mhz": clk["mhz"],
+                     "frac_at_clock": (round(achieved / ((PEAK[prec_of] if mfma_bound else PEAK_HBM * 1e3)
+                                                         * clk["mhz"] / CLOCK_MHZ), 4)
+                                       if clk["mhz"] and mfma_bound else None)},
+        "clock": dict(clk, published_peak_mhz=CLOCK_MHZ, **{"pass": "the single-stream per-launch pass"}),
+        "read_rate_tbps": dict(rates, hbm_published=PEAK_HBM),
         "launch_classes": launch_classes(recs, args.steps, peak),
         "kernels": {L.kernel_name(k): {"launches_per_step": v[0] / args.steps, "ms_per_step": round(v[1] / args.steps, 3),
                                        "tflops": round(v[2] / (v[1] * 1e-3) / 1e12, 2),
@@ -349,6 +433,41 @@ def bench_vitb(args):
     else:
         out["cpu_baseline"] = None
     return out
+
+
+def bench_gemm(args):
+    """One launch shape of the dominant kernel class, for counter runs: 12 problems of C = A B^T with A, B 3072 x 3072
+    bf16 (k contiguous) and fp32 C, launched `steps` times after `warmup`; the engine clock over the timed launches."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    dev = torch.device("cuda:0")
+    m = n = k = 3072
+    nb = 12
+    gen = torch.Generator(device=dev).manual_seed(0)
+    A = [torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for _ in range(nb)]
+    B = [torch.randn(n, k, device=dev, generator=gen).to(torch.bfloat16) for _ in range(nb)]
+    Cs = [torch.empty(m, n, device=dev) for _ in range(nb)]
+    stream = torch.cuda.current_stream()
+    st = C.c_void_p(stream.cuda_stream)
+    f = lambda: L.check(L.lib().psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(A), k, L.ptrs(B), k, 0.0,
+                                           L.ptrs(Cs), n, st))
+    for _ in range(max(1, args.warmup)):
+        f()
+    torch.cuda.synchronize()
+    clock = ClockSampler(dev, stream, est_ms=args.steps * 1.2 + 20)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    clock.start()
+    ev[0].record(stream)
+    for _ in range(args.steps):
+        f()
+    ev[1].record(stream)
+    clock.stop()
+    clk = clock.result()
+    us = ev[0].elapsed_time(ev[1]) * 1e3 / args.steps
+    tf = 2.0 * m * n * k * nb / (us * 1e-6) / 1e12
+    return {"op": "gemm_bf16", "m": m, "n": n, "k": k, "nb": nb, "launches": args.steps, "us": round(us, 1),
+            "tflops": round(tf, 1), "frac": round(tf / PEAK["bf16"], 4), "clock_mhz": clk["mhz"],
+            "frac_at_clock": round(tf / (PEAK["bf16"] * clk["mhz"] / CLOCK_MHZ), 4) if clk["mhz"] else None}
 
 
 def bench_syrk(args):
@@ -639,6 +758,9 @@ def main():
         return
     if args.config == "llama":
         print(json.dumps(bench_llama(args)), flush=True)
+        return
+    if args.config == "gemm":
+        print(json.dumps(bench_gemm(args)), flush=True)
         return
     if args.config == "syrk":
         for ln in bench_syrk(args):

@@ -325,6 +325,24 @@ int psgdk_get_option(int option, int* value);
  * ceiling a kernel can reach there. */
 int psgdk_mfma_rate(int iters, int wgs, float* out, psgdk_stream_t stream);
 
+/* Measurement (no counterpart in the reference): wgs workgroups of 256 threads, each reading iters blocks of 4 KiB
+ * of buf (device memory of `bytes` bytes, a power of two >= 4096): block (workgroup * iters + i) * stride, wrapped
+ * into the buffer. stride 1 with wgs * iters * 4096 = bytes reads the buffer once (the HBM read rate when it is far
+ * larger than the caches); an odd stride over a small buffer gives the cache read rate. sink: device memory of wgs
+ * uint32 (practically never written). */
+int psgdk_read_rate(const void* buf, int64_t bytes, int wgs, int iters, int64_t stride, uint32_t* sink,
+                    psgdk_stream_t stream);
+
+/* Measurement (no counterpart in the reference): one wave that, `samples` times, sleeps about 8 thousand cycles and
+ * then writes the cycle counter (out[2 i]) and the constant-rate wall counter (out[2 i + 1]; its rate is the
+ * device's hipDeviceAttributeWallClockRate). Launched on a stream of its own next to other work, it gives the engine
+ * clock while that work runs. out: device memory of 2 * samples uint64. */
+int psgdk_clock_sample(int samples, uint64_t* out, psgdk_stream_t stream);
+/* Measurement: the wall counter's rate of the current device in kHz (hipDeviceAttributeWallClockRate; host query). */
+int psgdk_wall_clock_rate(int* khz);
+/* Measurement: out[0] = the wall counter when `stream` reaches this call (marks the ends of a timed region). */
+int psgdk_wall_mark(uint64_t* out, psgdk_stream_t stream);
+
 /* Debug: one MFMA with operands placed by the lane layout the kernels assume (A 16 x K, B K x 16 row-major fp32,
  * K = 32 for bf16, 4 for fp32), C (16 x 16) = A B; prec 2: the 32 x 32 x 16 bf16 shape (A 32 x 16, B 16 x 32,
  * C 32 x 32). Checks the compiler builtins' lane layout. */

@@ -64,6 +64,10 @@ _SIGS = {
     "psgdk_tri_vmm": (_i32, [_i64, _i32, _i32, _vpa, _vpa, _i64, _vpa, _vp, _szp, _vp]),
     "psgdk_norm_lower_bound": (_i32, [_i64, _i32, _i32, _vpa, _i64, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_mfma_rate": (_i32, [_i32, _i32, _vp, _vp]),
+    "psgdk_read_rate": (_i32, [_vp, _i64, _i32, _i32, _i64, _vp, _vp]),
+    "psgdk_clock_sample": (_i32, [_i32, _vp, _vp]),
+    "psgdk_wall_mark": (_i32, [_vp, _vp]),
+    "psgdk_wall_clock_rate": (_i32, [C.POINTER(C.c_int)]),
     "psgdk_fill_normal": (_i32, [_vp, _i64, _i32, C.c_uint64, C.c_uint64, _vp]),
     "psgdk_norm_lower_bound_full": (_i32, [_i64, _i32, _i32, _vpa, _i64, _i32, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_norm_lower_bound_full_noalloc": (_i32, [_i64, _i32, _i32, _vpa, _i64, _i32, _vpa, _vpa, _vp]),

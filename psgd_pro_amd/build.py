@@ -21,7 +21,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpsgdk.so")
-SOURCES = ["gemm.hip", "gemm_bf16.hip", "gemm_small.hip", "nlb.hip", "elem.hip", "capi.cpp", "noalloc.hip"]
+SOURCES = ["gemm.hip", "gemm_bf16.hip", "gemm_small.hip", "nlb.hip", "elem.hip", "capi.cpp", "noalloc.hip",
+           "measure.hip"]
 ARCH = os.environ.get("PSGDK_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

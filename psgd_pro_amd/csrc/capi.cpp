@@ -20,6 +20,10 @@ namespace psgdk {
 hipError_t gemm_launch(GemmArgs& a, int prec, int adt, int bdt, int cfg, hipStream_t st);
 hipError_t debug_mfma_launch(const float* A, const float* B, float* C, int prec, hipStream_t st);
 hipError_t mfma_rate_launch(int iters, int wgs, float* out, hipStream_t st);
+hipError_t read_rate_launch(const void* buf, long long bytes, int wgs, int iters, long long stride, unsigned* sink,
+                            hipStream_t st);
+hipError_t clock_sample_launch(int samples, unsigned long long* out, hipStream_t st);
+hipError_t wall_mark_launch(unsigned long long* out, hipStream_t st);
 int set_error(int code, const char* msg);  // for entry points defined in other source files
 }  // namespace psgdk
 
@@ -2253,6 +2257,36 @@ int psgdk_mfma_rate(int iters, int wgs, float* out, psgdk_stream_t stream) {
   if (iters < 1 || wgs < 1) return fail(PSGDK_EINVAL, "iters = %d, wgs = %d: both must be >= 1", iters, wgs);
   if (!out) return fail(PSGDK_EINVAL, "null pointer");
   return hip_check(mfma_rate_launch(iters, wgs, out, (hipStream_t)stream), "mfma rate");
+}
+
+int psgdk_read_rate(const void* buf, int64_t bytes, int wgs, int iters, int64_t stride, uint32_t* sink,
+                    psgdk_stream_t stream) {
+  if (!buf || !sink) return fail(PSGDK_EINVAL, "null pointer");
+  if (bytes < 4096 || (bytes & (bytes - 1)) != 0)
+    return fail(PSGDK_EINVAL, "bytes = %lld: must be a power of two >= 4096", (long long)bytes);
+  if (wgs < 1 || iters < 1 || stride < 1)
+    return fail(PSGDK_EINVAL, "wgs = %d, iters = %d, stride = %lld: each must be >= 1", wgs, iters, (long long)stride);
+  return hip_check(read_rate_launch(buf, bytes, wgs, iters, stride, sink, (hipStream_t)stream), "read rate");
+}
+
+int psgdk_clock_sample(int samples, uint64_t* out, psgdk_stream_t stream) {
+  if (!out) return fail(PSGDK_EINVAL, "null pointer");
+  if (samples < 1 || samples > (1 << 24)) return fail(PSGDK_EINVAL, "samples = %d: must be in 1 .. 2^24", samples);
+  return hip_check(clock_sample_launch(samples, reinterpret_cast<unsigned long long*>(out), (hipStream_t)stream),
+                   "clock sample");
+}
+
+int psgdk_wall_clock_rate(int* khz) {
+  if (!khz) return fail(PSGDK_EINVAL, "null pointer");
+  int dev = 0;
+  PSGDK_HIP(hipGetDevice(&dev), "hipGetDevice");
+  PSGDK_HIP(hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev), "wall clock rate");
+  return PSGDK_OK;
+}
+
+int psgdk_wall_mark(uint64_t* out, psgdk_stream_t stream) {
+  if (!out) return fail(PSGDK_EINVAL, "null pointer");
+  return hip_check(wall_mark_launch(reinterpret_cast<unsigned long long*>(out), (hipStream_t)stream), "wall mark");
 }
 
 int psgdk_debug_mfma(int prec, const float* A, const float* B, float* C, psgdk_stream_t stream) {

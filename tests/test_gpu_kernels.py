@@ -724,3 +724,33 @@ def test_fill_normal_matches_philox_reference(hip):
     assert abs(float(a.double().mean())) < 5 / math.sqrt(n)
     assert abs(float(a.double().var()) - 1) < 5 * math.sqrt(2 / n)
     assert hip.psgdk_fill_normal(C_ptr(a[1:]), 8, L.F32, 7, 0, st) == L.EINVAL  # misaligned
+
+
+def test_measurement_kernels(hip):
+    """psgdk_read_rate reads a buffer once (stride 1) and many times (odd stride) without writing its sink;
+    psgdk_clock_sample's counters advance and give an engine clock between 0.3 and 3 GHz; the two psgdk_wall_mark
+    marks bracket every sample of a sampler launched between them on the same stream."""
+    import ctypes as C
+    buf = torch.ones(1 << 20, dtype=torch.uint8, device=DEV)
+    sink = torch.zeros(64, dtype=torch.int32, device=DEV)
+    st = L.stream_of(buf)
+    L.check(hip.psgdk_read_rate(C_ptr(buf), 1 << 20, 64, 4, 1, C_ptr(sink), st))
+    L.check(hip.psgdk_read_rate(C_ptr(buf), 1 << 20, 64, 64, 977, C_ptr(sink), st))
+    samples = torch.zeros(2 * 16, dtype=torch.int64, device=DEV)
+    marks = torch.zeros(2, dtype=torch.int64, device=DEV)
+    L.check(hip.psgdk_wall_mark(C_ptr(marks), st))
+    L.check(hip.psgdk_clock_sample(16, C_ptr(samples), st))
+    L.check(hip.psgdk_wall_mark(C.c_void_p(marks.data_ptr() + 8), st))
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    s = samples.cpu().view(16, 2)
+    cyc, wall = s[:, 0], s[:, 1]
+    assert bool((cyc[1:] > cyc[:-1]).all()) and bool((wall[1:] > wall[:-1]).all())
+    khz = C.c_int(0)
+    L.check(hip.psgdk_wall_clock_rate(C.byref(khz)))
+    assert khz.value > 0
+    mhz = float(cyc[-1] - cyc[0]) / float(wall[-1] - wall[0]) * khz.value / 1e3
+    print(f"engine clock {mhz:.0f} MHz (wall counter {khz.value} kHz)", flush=True)
+    assert 300 < mhz < 3000
+    m = marks.cpu()
+    assert int(m[0]) <= int(wall[0]) and int(wall[-1]) <= int(m[1])

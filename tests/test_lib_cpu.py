@@ -262,3 +262,21 @@ def test_python_surface_on_cpu():
         make_ops({"k3"})
     with pytest.raises(ValueError):
         KronWhiten([W], compile="default")
+
+
+def test_measurement_entry_points_validate_without_device_work():
+    """psgdk_read_rate / psgdk_clock_sample / psgdk_wall_mark refuse bad arguments before any launch."""
+    lib = L.lib()
+    sink = C.c_void_p(0x1000)
+    assert lib.psgdk_read_rate(None, 4096, 1, 1, 1, sink, None) == L.EINVAL
+    assert lib.psgdk_read_rate(C.c_void_p(0x1000), 4096, 1, 1, 1, None, None) == L.EINVAL
+    for nbytes in (0, 2048, 4097, 3 << 20):
+        assert lib.psgdk_read_rate(C.c_void_p(0x1000), nbytes, 1, 1, 1, sink, None) == L.EINVAL, nbytes
+        assert "power of two" in _err()
+    for wgs, iters, stride in ((0, 1, 1), (1, 0, 1), (1, 1, 0)):
+        assert lib.psgdk_read_rate(C.c_void_p(0x1000), 4096, wgs, iters, stride, sink, None) == L.EINVAL
+    assert lib.psgdk_clock_sample(0, C.c_void_p(0x1000), None) == L.EINVAL
+    assert lib.psgdk_clock_sample((1 << 24) + 1, C.c_void_p(0x1000), None) == L.EINVAL
+    assert lib.psgdk_clock_sample(4, None, None) == L.EINVAL
+    assert lib.psgdk_wall_mark(None, None) == L.EINVAL
+    assert lib.psgdk_wall_clock_rate(None) == L.EINVAL
