@@ -152,17 +152,28 @@ class ClockSampler:
     counter, wall counter) pairs about every 4 us (psgdk_clock_sample) while two wall marks on `stream` bracket the
     region; the clock is the cycle increment over the wall increment between the first and last samples inside it."""
 
-    def __init__(self, dev, stream, est_ms):
+    def __init__(self, dev):
+        """Create it before any other stream of the process: the runtime spreads streams over a few hardware queues,
+        and a sampler whose queue is shared with the timed stream runs before that stream's work instead of beside
+        it (then no sample falls inside the region and the result says so)."""
         import torch
         from psgd_pro_amd import _lib as L
-        self.L, self.stream = L, stream
-        self.n = int(min(1 << 22, max(1024, est_ms * 1e3 / 2.5 * 1.5)))
-        self.buf = torch.zeros(2 * self.n, dtype=torch.int64, device=dev)
-        self.marks = torch.zeros(2, dtype=torch.int64, device=dev)
+        self.L, self.dev = L, dev
         self.side = torch.cuda.Stream(device=dev)
         khz = C.c_int(0)
         L.check(L.lib().psgdk_wall_clock_rate(C.byref(khz)))
         self.khz = khz.value
+        probe = torch.zeros(1, dtype=torch.int64, device=dev)  # first use of the stream (queues may bind on use)
+        L.check(L.lib().psgdk_wall_mark(C.c_void_p(probe.data_ptr()), C.c_void_p(self.side.cuda_stream)))
+        torch.cuda.synchronize(dev)
+
+    def arm(self, stream, est_ms):
+        import torch
+        self.stream = stream
+        self.n = int(min(1 << 22, max(1024, est_ms * 1e3 / 2.5 * 1.5)))
+        self.buf = torch.zeros(2 * self.n, dtype=torch.int64, device=self.dev)
+        self.marks = torch.zeros(2, dtype=torch.int64, device=self.dev)
+        return self
 
     def start(self):
         raw = lambda st: C.c_void_p(st.cuda_stream)
@@ -303,6 +314,7 @@ def bench_vitb(args):
     from psgd_pro_amd import _lib as L
 
     dev = torch.device("cuda:0")
+    clock = ClockSampler(dev)  # first stream of the process (see ClockSampler)
     L.check(L.lib().psgdk_set_option(5, args.t1q_pg))
     L.check(L.lib().psgdk_set_option(6, args.upd_streams))
     L.check(L.lib().psgdk_set_option(1, args.tile_cfg))
@@ -344,7 +356,7 @@ def bench_vitb(args):
     torch.cuda.synchronize()
     # the engine clock over this pass: the published peaks assume CLOCK_MHZ, and the GPU lowers its clock under a
     # sustained MFMA and memory load
-    clock = ClockSampler(dev, stream, est_ms=1.5 * args.steps * ev_ms + 50)
+    clock.arm(stream, est_ms=1.5 * args.steps * ev_ms + 50)
     clock.start()
     L.profile_start()
     for _ in range(args.steps):
@@ -441,6 +453,7 @@ def bench_gemm(args):
     import torch
     from psgd_pro_amd import _lib as L
     dev = torch.device("cuda:0")
+    clock = ClockSampler(dev)
     m = n = k = 3072
     nb = 12
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -454,7 +467,7 @@ def bench_gemm(args):
     for _ in range(max(1, args.warmup)):
         f()
     torch.cuda.synchronize()
-    clock = ClockSampler(dev, stream, est_ms=args.steps * 1.2 + 20)
+    clock.arm(stream, est_ms=args.steps * 1.2 + 20)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     clock.start()
     ev[0].record(stream)
