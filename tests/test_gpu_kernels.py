@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from psgd_pro_amd import _lib as L
+from psgd_pro_amd import KronWhiten
 from psgd_pro_amd import ops as K
 from tests.metrics import rel_err_norm
 
@@ -754,3 +755,64 @@ def test_measurement_kernels(hip):
     assert 300 < mhz < 3000
     m = marks.cpu()
     assert int(m[0]) <= int(wall[0]) and int(wall[-1]) <= int(m[1])
+
+
+@pytest.mark.parametrize("flags", [("k1", "k2"), ("k1", "k2t", "all"), ("k2c",), ("k2b", "nan"), ("k1", "k2", "tri"),
+                                   ("k1", "tri", "nan", "packed")])
+def test_reference_flag_sets_compute_the_eager_methods(hip, flags):
+    """Plugins built from the reference's own flag sets (kernels/ops.py:142-215) return the values of the eager
+    definitions (psgd_pro_fast.py:106-126) for every method: syrk / gram_q full, sym / gram in the storage form the
+    flags ask for (full, upper triangle with an optional NaN lower part, or packed), symm / symm_r from that form, the
+    norm bounds equal to the full-matrix ones on the same start."""
+    ops = K.make_ops(set(flags))
+    X = rnd(96, 160, seed=1).to(DEV)
+    X64 = X.double().cpu()
+    S64 = X64 @ X64.T
+    Y = rnd(96, 40, seed=2).to(DEV)
+    Z = rnd(40, 96, seed=3).to(DEV)
+    assert rel_err_norm(ops.syrk(X, False), S64) < 1e-6
+    assert rel_err_norm(ops.gram_q(X), X64.T @ X64) < 1e-6
+    S = ops.sym(X, False)
+    tri, packed = "tri" in flags, "packed" in flags
+    if packed:
+        assert S.dim() == 1 and S.numel() == 96 * 97 // 2
+        assert rel_err_norm(K.unpack(S, 96), S64) < 1e-6
+    elif tri:
+        assert S.shape == (96, 96) and rel_err_norm(S.triu(), S64.triu()) < 1e-6
+        if "nan" in flags:
+            assert bool(torch.isnan(S.tril(-1)).sum() == 96 * 95 // 2)
+    else:
+        assert rel_err_norm(S, S64) < 1e-6
+    G = ops.gram(X, 0, None)
+    assert rel_err_norm(G.triu() if tri else G, S64.triu() if tri else S64) < 1e-6
+    assert rel_err_norm(ops.symm(S, Y), S64 @ Y.double().cpu()) < 1e-6
+    assert rel_err_norm(ops.symm_r(Z, S), Z.double().cpu() @ S64) < 1e-6
+    Sf = ops.syrk(X, False)
+    V = rnd(32, 96, seed=5).to(DEV)
+    ref = float(K.norm_lower_bound(Sf, V, 1))
+    assert abs(float(ops.norm_lower_bound_spd(S, V)) - ref) <= 1e-5 * ref
+    A = rnd(96, 96, seed=6).to(DEV)
+    R = A - A.T  # skew, a non-contiguous expression as Q^T - Q is in the reference
+    ref_k = float(K.norm_lower_bound(R.contiguous(), V, -1))
+    assert ref_k > 0 and float(ops.norm_lower_bound_skh(R, V)) == ref_k
+
+
+def test_optimizer_takes_storage_from_the_plugin(hip):
+    """KronWhiten(ops=make_ops({"k1", "tri"})) keeps term1 and P as upper triangles: bitwise the same run as
+    KronWhiten(tri=True), and EagerOps (the default) bitwise the same as tri=False."""
+    shapes = [(96, 64), (64, 96)]
+    gen = torch.Generator().manual_seed(7)
+    grads = [[(0.01 * torch.randn(s, generator=gen)).to(DEV) for s in shapes] for _ in range(3)]
+    out = {}
+    for name, kw in (("ops_tri", dict(ops=K.make_ops({"k1", "tri"}))), ("tri", dict(tri=True)),
+                     ("eager", dict(ops=K.EagerOps)), ("full", dict(tri=False))):
+        W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
+        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=3,
+                           **kw)
+        for gs in grads:
+            opt.step_math(gs)
+        torch.cuda.synchronize()
+        out[name] = ([w.detach().clone() for w in W], [q.clone() for i in range(len(shapes)) for q in opt.factors(i)[0]])
+    for a, b in (("ops_tri", "tri"), ("eager", "full")):
+        for x, y in zip(out[a][0] + out[a][1], out[b][0] + out[b][1]):
+            assert torch.equal(x, y), (a, b)
