@@ -25,6 +25,7 @@ extern "C" {
 #endif
 
 typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
+typedef struct ihipEvent_t* psgdk_event_t;   /* hipEvent_t */
 
 #define PSGDK_VERSION 3
 #define PSGDK_MAXB 16 /* problems per grouped call */
@@ -206,6 +207,15 @@ int psgdk_kron2d_update(const psgdk_kron2d_t* g, const psgdk_update_opts_t* o, c
 int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
                                const psgdk_update_opts_t* const* opts, const void* const* const* noise,
                                const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream);
+/* psgdk_kron2d_update_groups that also records, for each group g with group_done[g] non-NULL, the caller's event
+ * group_done[g] once that group's factors, L, P and bf16 shadows are final (the batches holding its factors done),
+ * so that work on one group (its balance and apply) can start while other groups' batches still run. The call still
+ * joins all its work back to `stream`. Events are created by the caller (hipEventCreate) and re-recorded by every
+ * call. No counterpart in the reference (its per-parameter loop runs in order, psgd_pro_fast.py:351-368). */
+int psgdk_kron2d_update_groups_ev(int ngroups, const psgdk_kron2d_t* const* groups,
+                                  const psgdk_update_opts_t* const* opts, const void* const* const* noise,
+                                  const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream,
+                                  psgdk_event_t const* group_done);
 
 /* Precondition, clip and update: pre = P1 G P2 (apply_2d, psgd_pro_fast.py:156-161 = precond_grad_kron,
  * psgd_pro.py:107-112), clip to RMS <= max_avg_amp and |.| <= max_element_amp, param -= lr_params * clipped

@@ -76,6 +76,8 @@ _SIGS = {
     "psgdk_kron2d_update": (_i32, [C.POINTER(Kron2d), C.POINTER(UpdateOpts), _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_kron2d_update_groups": (_i32, [_i32, C.POINTER(C.POINTER(Kron2d)), C.POINTER(C.POINTER(UpdateOpts)),
                                           C.POINTER(_vpa), C.POINTER(_vpa), _vp, _szp, _vp]),
+    "psgdk_kron2d_update_groups_ev": (_i32, [_i32, C.POINTER(C.POINTER(Kron2d)), C.POINTER(C.POINTER(UpdateOpts)),
+                                             C.POINTER(_vpa), C.POINTER(_vpa), _vp, _szp, _vp, _vpa]),
     "psgdk_kron2d_apply": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_apply2d": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_factor_update": (_i32, [_i32, _i64, _i32, _vpa, _i32, _vpa, _vpa, _vpa, _vpa, C.c_float, C.c_float,

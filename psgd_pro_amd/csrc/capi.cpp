@@ -253,6 +253,7 @@ thread_local int g_tiny = 64;         // option 11: of those, launches with fewe
 struct SideStreams {
   std::vector<hipStream_t> s;
   std::vector<hipEvent_t> ev;  // 1 fork + per side stream 2 (phase join, final join)
+  std::vector<hipEvent_t> bev;  // the end of each batch of a grouped update (per-group completion events)
 };
 std::mutex& side_stream_mutex() {
   static std::mutex m;
@@ -276,6 +277,15 @@ int side_streams(int n, SideStreams** out) {
     ss.ev.push_back(e);
   }
   *out = &ss;
+  return PSGDK_OK;
+}
+// Caller holds side_stream_mutex(): at least n batch events in ss.
+int batch_events(SideStreams* ss, size_t n) {
+  while (ss->bev.size() < n) {
+    hipEvent_t e;
+    PSGDK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "batch event");
+    ss->bev.push_back(e);
+  }
   return PSGDK_OK;
 }
 
@@ -831,6 +841,7 @@ int refresh_p_diag(const psgdk_kron2d_t* g, int f, const int* sel, int nsel, hip
 // The items are independent after Pg, and every kernel computes each problem of a launch on its own, so the
 // results do not depend on how the items are batched.
 struct B16Item {
+  int gi = 0;  // the item's group in the call
   int64_t d = 0, other = 0;
   float term2 = 0.f;
   const bf16_t* pcol = nullptr;  // d x other rows (k = other): term1 = pcol pcol^T
@@ -1046,9 +1057,11 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
 
 // The update of ng bf16-path groups: per-group noise, Y and Pg, then the items of every dense factor in batches of
 // one side d (largest first), the items of a batch ordered by their other side.
+// group_done (optional): per group an event recorded once that group's factors, L and shadows are final (its
+// items' batches done), so that a caller can start work on one group before the whole call has finished.
 int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_update_opts_t* const* os,
                       const void* const* const* noise, const float* const* const* V, void* ws, size_t* ws_bytes,
-                      hipStream_t st) {
+                      hipStream_t st, const hipEvent_t* group_done = nullptr) {
   Ws w(ws);
   std::vector<std::vector<bf16_t*>> Xb(ng), YTb(ng), Pgb(ng), PgTb(ng);
   std::vector<std::vector<float*>> dterm(ng);  // a diagonal factor's term1
@@ -1068,6 +1081,7 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
       for (int f = 0; f < 2; ++f) {
         if (g->kind[f] != PSGDK_FACTOR_DENSE) continue;  // a diagonal factor is updated in the per-group phase
         B16Item x;
+        x.gi = gi;
         x.d = f == 0 ? g->m : g->n;
         x.other = f == 0 ? g->n : g->m;
         x.term2 = (float)mn / (float)x.d;
@@ -1214,7 +1228,36 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
       for (int j = 0; j < S; ++j)
         if (i != j) PSGDK_HIP(hipStreamWaitEvent(ss->s[i], ss->ev[1 + j], 0), "phase join wait");
   }
-  for (size_t k = 0; k < batches.size(); ++k) PSGDK_TRY(b16_items(batches[k], os[0], nws[k], lane((int)k)));
+  if (group_done && S > 1) PSGDK_TRY(batch_events(ss, batches.size()));
+  for (size_t k = 0; k < batches.size(); ++k) {
+    PSGDK_TRY(b16_items(batches[k], os[0], nws[k], lane((int)k)));
+    if (group_done && S > 1) PSGDK_HIP(hipEventRecord(ss->bev[k], lane((int)k)), "batch end");
+  }
+  if (group_done) {
+    // group gi is final once every batch holding one of its items is: its event is recorded on the lane of its last
+    // such batch after that lane waits for the others' end events (every group has an item: b16_group needs a
+    // dense factor; its diagonal factors were updated before the phase join)
+    for (int gi = 0; gi < ng; ++gi) {
+      if (!group_done[gi]) continue;
+      if (S == 1) {
+        PSGDK_HIP(hipEventRecord(group_done[gi], st), "group done");
+        continue;
+      }
+      int last = -1;
+      for (size_t k = 0; k < batches.size(); ++k)
+        for (const B16Item* x : batches[k])
+          if (x->gi == gi) last = (int)k;
+      if (last < 0) return fail(PSGDK_EINVAL, "group %d has no dense factor", gi);
+      hipStream_t L = lane(last);
+      for (size_t k = 0; k < batches.size(); ++k) {
+        if ((int)k == last || lane((int)k) == L) continue;
+        bool has = false;
+        for (const B16Item* x : batches[k]) has = has || x->gi == gi;
+        if (has) PSGDK_HIP(hipStreamWaitEvent(L, ss->bev[k], 0), "group done wait");
+      }
+      PSGDK_HIP(hipEventRecord(group_done[gi], L), "group done");
+    }
+  }
   if (S > 1) {
     joiner.ss = nullptr;
     for (int i = 0; i < S; ++i) {
@@ -1944,6 +1987,21 @@ int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
   }
   if (ws && (!noise || !V)) return fail(PSGDK_EINVAL, "null noise or V");
   return b16_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int psgdk_kron2d_update_groups_ev(int ngroups, const psgdk_kron2d_t* const* groups,
+                                  const psgdk_update_opts_t* const* opts, const void* const* const* noise,
+                                  const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream,
+                                  psgdk_event_t const* group_done) {
+  if (!group_done) return fail(PSGDK_EINVAL, "null group_done array");
+  if (!ws) return psgdk_kron2d_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, stream);
+  // the checks of psgdk_kron2d_update_groups, then the call with the completion events
+  size_t need = 0;
+  PSGDK_TRY(psgdk_kron2d_update_groups(ngroups, groups, opts, noise, V, nullptr, &need, stream));
+  if (*ws_bytes < need) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, need);
+  if (!noise || !V) return fail(PSGDK_EINVAL, "null noise or V");
+  return b16_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, (hipStream_t)stream,
+                           reinterpret_cast<const hipEvent_t*>(group_done));
 }
 
 int psgdk_kron2d_apply(const psgdk_kron2d_t* g, const psgdk_apply_opts_t* o, void* const* params,

@@ -156,6 +156,8 @@ class KronWhiten:
         # one psgdk_kron2d_update_groups call for every bf16-path group: the factor work of all groups is batched
         # by factor side (the same operations as one call per group; larger launches may sum in another order)
         self._fuse = bool(fuse_groups)
+        self._gev = {}  # per group: the event its update records when its factors are final
+        self._overlap = True  # False: the whole update, then every balance, then every apply (each a fork / join)
         self._draw_buf = self._draw_buf16 = None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
@@ -386,71 +388,159 @@ class KronWhiten:
                 return False
         return grp.m * grp.n * 2 < 2 ** 31
 
+    def _update_opts(self):
+        return L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))
+
+    def _apply_opts(self):
+        max_avg, max_el = self.grad_clip_max_amps
+        return L.ApplyOpts(self.lr_params, max_avg, max_el, self._tri)
+
+    def _split_groups(self):
+        """(the bf16-path groups one grouped update call takes, the groups updated one call each)"""
+        fused = [g for g in self._groups if self._fuse and self._b16(g)][:L.MAX_GROUPS]
+        return fused, [g for g in self._groups if not any(g is f for f in fused)]
+
+    def _update_fused(self, fused, srcs, noise, V, ln, dev, events=None):
+        """One grouped update of the bf16-path groups on the current stream (psgdk_kron2d_update_groups; with
+        events, psgdk_kron2d_update_groups_ev, which records each group's event once its factors are final)."""
+        o = self._update_opts()
+        opts, nzs, vvs = [], [], []
+        for grp in fused:
+            og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
+            og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
+            opts.append(og)
+            nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
+            vvs.append(L.ptrs([V[p.index] for p in grp.members]))
+        ng = len(fused)
+        garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
+        oarr = (ctypes.POINTER(L.UpdateOpts) * ng)(*[ctypes.pointer(x) for x in opts])
+        narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
+        varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
+        st = L.stream_of(srcs[0])
+        if events is None:
+            L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
+                      stream=st)
+            return
+        earr = L.ptrs([ev.cuda_event for ev in events])
+        fn = L.lib().psgdk_kron2d_update_groups_ev
+        sz = ctypes.c_size_t(0)
+        L.check(fn(ng, garr, oarr, narr, varr, None, ctypes.byref(sz), st, earr))
+        buf = ln.ws_upd.get(sz.value, dev)
+        sz2 = ctypes.c_size_t(buf.numel())
+        L.check(fn(ng, garr, oarr, narr, varr, ctypes.c_void_p(buf.data_ptr()), ctypes.byref(sz2), st, earr))
+
+    def _update_group(self, grp, srcs, noise, V, ln, dev):
+        """One group's update on the current stream (psgdk_kron2d_update)."""
+        o = self._update_opts()
+        o.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
+        nz = L.ptrs([noise[p.index] for p in grp.members])
+        vv = L.ptrs([V[p.index] for p in grp.members])
+        L.call_ws(L.lib().psgdk_kron2d_update, grp.struct, o, nz, vv, ws=ln.ws_upd, device=dev,
+                  stream=L.stream_of(srcs[0]))
+
+    def _balance_group(self, grp, coins, ln, dev):
+        """psgd_pro.py:138-139 for the group's parameters whose coin came up, on the current stream."""
+        flags = [int(coins[p.index]) for p in grp.members]
+        if any(flags):
+            fl = (ctypes.c_int32 * len(flags))(*flags)
+            L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=ln.ws_bal, device=dev,
+                      stream=torch.cuda.current_stream(dev).cuda_stream)
+
+    def _apply_group(self, grp, srcs, pre, ln, dev):
+        """Precondition, clip and update the group's parameters on the current stream (psgdk_kron2d_apply)."""
+        self._bind_sources(grp, srcs)
+        prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
+        po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
+        L.call_ws(L.lib().psgdk_kron2d_apply, grp.struct, self._apply_opts(), prm, po, None, ws=ln.ws_app, device=dev,
+                  stream=L.stream_of(srcs[0]))
+
+    def _pre_buffers(self, dev):
+        """The preconditioned gradients' outputs when `capture` is set (else None)."""
+        if not self.capture:
+            return None
+        return [torch.empty(p.m, p.n, device=dev, dtype=torch.float32) for p in self._params]
+
+    def _keep_pre(self, pre):
+        if pre is not None:
+            self.pre = [t.view(p.shape) for t, p in zip(pre, self._params)]
+
+    @staticmethod
+    def _on(ln, cur):
+        return torch.cuda.stream(ln.stream if ln.stream is not None else cur)
+
     def _update(self, srcs, noise, V):
-        o = L.UpdateOpts(self.lr_preconditioner, self.betaL, self.damping, 0.0, self._tri, int(self._r2))
         dev = srcs[0].device
         with self._forked(dev) as (cur, lanes):
-            fused = [g for g in self._groups if self._fuse and self._b16(g)][:L.MAX_GROUPS]
-            rest = [g for g in self._groups if not any(g is f for f in fused)]
+            fused, rest = self._split_groups()
             if fused:
-                ln = lanes[0]
-                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                    opts, nzs, vvs = [], [], []
-                    for grp in fused:
-                        og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
-                        og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
-                        opts.append(og)
-                        nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
-                        vvs.append(L.ptrs([V[p.index] for p in grp.members]))
-                    ng = len(fused)
-                    garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
-                    oarr = (ctypes.POINTER(L.UpdateOpts) * ng)(*[ctypes.pointer(x) for x in opts])
-                    narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
-                    varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
-                    L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
-                              stream=L.stream_of(srcs[0]))
+                with self._on(lanes[0], cur):
+                    self._update_fused(fused, srcs, noise, V, lanes[0], dev)
             for gi, grp in enumerate(rest):
                 ln = lanes[(gi + (1 if fused else 0)) % len(lanes)]
-                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                    s = grp.struct
-                    gdt = self._bind_sources(grp, srcs)
-                    o.grad_eps = torch.finfo(gdt).eps
-                    nz = L.ptrs([noise[p.index] for p in grp.members])
-                    vv = L.ptrs([V[p.index] for p in grp.members])
-                    L.call_ws(L.lib().psgdk_kron2d_update, s, o, nz, vv, ws=ln.ws_upd, device=dev,
-                              stream=L.stream_of(srcs[0]))
+                with self._on(ln, cur):
+                    self._update_group(grp, srcs, noise, V, ln, dev)
 
     def _balance(self, coins, dev):
         """psgd_pro.py:138-139: balance the factors of every parameter whose coin came up (eager, rare)."""
         with self._forked(dev) as (cur, lanes):
             for gi, grp in enumerate(self._groups):
-                flags = [int(coins[p.index]) for p in grp.members]
-                if not any(flags):
-                    continue
                 ln = lanes[gi % len(lanes)]
-                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                    fl = (ctypes.c_int32 * len(flags))(*flags)
-                    L.call_ws(L.lib().psgdk_kron2d_balance, grp.struct, fl, self._tri, ws=ln.ws_bal, device=dev,
-                              stream=torch.cuda.current_stream(dev).cuda_stream)
+                with self._on(ln, cur):
+                    self._balance_group(grp, coins, ln, dev)
 
     def _apply(self, srcs):
-        max_avg, max_el = self.grad_clip_max_amps
-        o = L.ApplyOpts(self.lr_params, max_avg, max_el, self._tri)
         dev = srcs[0].device
-        pre = [torch.empty(p.m, p.n, device=dev, dtype=torch.float32) for p in self._params] \
-            if self.capture else None
+        pre = self._pre_buffers(dev)
         with self._forked(dev) as (cur, lanes):
             for gi, grp in enumerate(self._groups):
                 ln = lanes[gi % len(lanes)]
-                with torch.cuda.stream(ln.stream if ln.stream is not None else cur):
-                    s = grp.struct
-                    self._bind_sources(grp, srcs)
-                    prm = L.ptrs([self._params_with_grad[p.index] for p in grp.members])
-                    po = L.ptrs([pre[p.index] for p in grp.members]) if pre is not None else None
-                    L.call_ws(L.lib().psgdk_kron2d_apply, s, o, prm, po, None, ws=ln.ws_app, device=dev,
-                              stream=L.stream_of(srcs[0]))
-        if pre is not None:
-            self.pre = [t.view(p.shape) for t, p in zip(pre, self._params)]
+                with self._on(ln, cur):
+                    self._apply_group(grp, srcs, pre, ln, dev)
+        self._keep_pre(pre)
+
+    def _group_event(self, grp):
+        """A persistent event per group, created (recorded once) so that its handle exists for the library."""
+        ev = self._gev.get(id(grp))
+        if ev is None:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream())
+            self._gev[id(grp)] = ev
+        return ev
+
+    def _update_then_apply(self, srcs, noise, V, coins, asrcs):
+        """The update, then per group its balance (when one of its coins came up) and its apply, each group's after
+        that group's own update only: the grouped update records a completion event per group
+        (psgdk_kron2d_update_groups_ev), the groups updated one call each record theirs, and the balance and apply
+        chains run on the side streams other than the grouped update's, smaller factor sides first (their batches
+        end first). Each group goes through the same operations in the same order as with the whole update, then
+        every balance, then every apply (bitwise the same results)."""
+        dev = srcs[0].device
+        pre = self._pre_buffers(dev)
+        with self._forked(dev) as (cur, lanes):
+            fused, rest = self._split_groups()
+            done = {}
+            if fused:
+                evs = [self._group_event(g) for g in fused]
+                with self._on(lanes[0], cur):
+                    self._update_fused(fused, srcs, noise, V, lanes[0], dev, events=evs)
+                done.update((id(g), ev) for g, ev in zip(fused, evs))
+            for gi, grp in enumerate(rest):
+                ln = lanes[(gi + (1 if fused else 0)) % len(lanes)]
+                with self._on(ln, cur):
+                    self._update_group(grp, srcs, noise, V, ln, dev)
+                    ev = self._group_event(grp)
+                    ev.record(ln.stream)
+                    done[id(grp)] = ev
+            # the grouped call joins all of its work into lanes[0]: the chains run on the other lanes
+            alanes = lanes[1:] if fused else lanes
+            side = lambda g: max(g.m if g.kind[0] == L.FACTOR_DENSE else 0, g.n if g.kind[1] == L.FACTOR_DENSE else 0)
+            for i, grp in enumerate(sorted(self._groups, key=side)):
+                ln = alanes[i % len(alanes)]
+                with self._on(ln, cur):
+                    ln.stream.wait_event(done[id(grp)])
+                    self._balance_group(grp, coins, ln, dev)
+                    self._apply_group(grp, asrcs, pre, ln, dev)
+        self._keep_pre(pre)
 
     # ----------------------------------------------------------------------------------------------------------
     @torch.no_grad()
@@ -485,6 +575,12 @@ class KronWhiten:
         # device work in segments; the balancing coins act between them, as in psgd_pro.py:138-139 (inside the
         # update, so before the apply when the update comes first)
         first = update and self.update_preconditioner_first
+        if first and self._overlap and self.side_streams() >= 2:
+            # each group's balance and apply start as soon as that group's own factors are final
+            self._momentum_step(grads, beta)
+            self._update_then_apply(grads if self._whiten_grad else self._ms, noise, V, coins,
+                                    self._ms if self.momentum > 0 else grads)
+            return
         self._device_work(grads, beta, first, not first, noise, V)
         if first and any(coins):
             self._balance(coins, dev)
@@ -495,15 +591,21 @@ class KronWhiten:
             if any(coins):
                 self._balance(coins, dev)
 
+    def _momentum_step(self, grads, beta):
+        """psgd_pro.py:340-341 on the caller's stream when beta is given: every parameter's momentum in one launch
+        per 64 tensors."""
+        if beta is None:
+            return
+        for c in range(0, len(grads), L.MAX_TENSORS):
+            ch = range(c, min(c + L.MAX_TENSORS, len(grads)))
+            numel = (ctypes.c_int64 * len(ch))(*[grads[i].numel() for i in ch])
+            dts = (ctypes.c_int32 * len(ch))(*[L.dtype_code(grads[i].dtype) for i in ch])
+            L.check(L.lib().psgdk_momentum_multi(len(ch), numel, beta, dts, L.ptrs([self._ms[i] for i in ch]),
+                                                 L.ptrs([grads[i] for i in ch]), L.stream_of(grads[0])))
+
     def _device_work(self, grads, beta, do_update, do_apply, noise, V):
         """Momentum (when beta is given), preconditioner update, apply: kernel launches only."""
-        if beta is not None:  # every parameter's momentum in one launch per 64 tensors
-            for c in range(0, len(grads), L.MAX_TENSORS):
-                ch = range(c, min(c + L.MAX_TENSORS, len(grads)))
-                numel = (ctypes.c_int64 * len(ch))(*[grads[i].numel() for i in ch])
-                dts = (ctypes.c_int32 * len(ch))(*[L.dtype_code(grads[i].dtype) for i in ch])
-                L.check(L.lib().psgdk_momentum_multi(len(ch), numel, beta, dts, L.ptrs([self._ms[i] for i in ch]),
-                                                     L.ptrs([grads[i] for i in ch]), L.stream_of(grads[0])))
+        self._momentum_step(grads, beta)
         src = grads if self._whiten_grad else self._ms
         if do_update and self.update_preconditioner_first:
             self._update(src, noise, V)

@@ -283,6 +283,37 @@ def test_side_streams_bitwise_identical(hip, prec):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_per_group_apply_scheduling_bitwise(hip, prec):
+    """With the update first, each group's balance and apply wait only for that group's own update (a completion
+    event per group from psgdk_kron2d_update_groups_ev, or from its own update call). Against the whole update, then
+    every balance, then every apply: bitwise the same factors and parameters over 5 steps with momentum, balancing
+    coins forced for some parameters on steps 1 and 3, and update-skipping steps (probability 0.6)."""
+    shapes = [(64, 96), (96, 64), (128, 128), (32,), (64, 96), (256, 64)]
+    runs = []
+    for overlap in (False, True):
+        W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
+        opt = KronWhiten(W, preconditioner_max_skew=math.inf, preconditioner_init_scale=1.0, draws="host", seed=9,
+                         momentum=0.9, precision=prec, streams=3, preconditioner_update_probability=0.6)
+        opt._overlap = overlap
+        real = opt._draw_update
+
+        def forced(srcs, real=real, opt=opt):
+            noise, V, coins = real(srcs)
+            if opt._t in (1, 3):
+                coins = [c or i in (0, 2, 5) for i, c in enumerate(coins)]
+            return noise, V, coins
+        opt._draw_update = forced
+        for t in range(5):
+            opt._t = t
+            opt.step_math([g.to(DEV) for g in grads_for(shapes, t)])
+        torch.cuda.synchronize()
+        qs = [q.detach().clone() for i in range(len(shapes)) for q in opt.factors(i)[0]]
+        runs.append(([w.detach().clone() for w in W], qs))
+    for a, b in zip(runs[0][0] + runs[0][1], runs[1][0] + runs[1][1]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("skew", [math.inf, 2.0], ids=["dense", "mixed"])
 @pytest.mark.parametrize("r2", [False, True], ids=["step2", "r2"])
 def test_fused_groups_bitwise_identical(hip, r2, skew):
