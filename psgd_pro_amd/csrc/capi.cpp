@@ -227,6 +227,7 @@ struct B16Out {
 // thread's results.
 thread_local int g_tile_order = 2;  // option 0: 0 problem-major, 1 XCD-contiguous runs, 2 runs + grouped rows
 thread_local int g_force_cfg = -1;  // option 1: -1 by size, else the bf16 kernel's tile config
+thread_local int g_ws = 1;          // option 12: the main loop of the 256 x 256 tiles chosen by size (0 cfg 0, 1 cfg 3)
 thread_local int g_nlb_target = 1024;  // option 2: workgroups per full-storage V A product (split-K target)
 thread_local int g_vmm_u = 4;          // option 3: MFMA steps per load batch of the V A kernel (2, 4 or 8)
 thread_local int g_vmm_cols = -1;      // option 4: V A kernel: -1 by shape (3 for bf16 launches of >= 16
@@ -291,10 +292,15 @@ int batch_events(SideStreams* ss, size_t n) {
 
 // The 256-tile configuration needs most of the 256 CUs busy; with K >= 4096 its faster main loop pays for a
 // half-empty chip down to 128 tiles (one 4096 x 4096 SYRK, 136 tiles: 117 us against 133 us on 528 128-tiles).
-int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb) {
+// Its warp-specialized main loop (cfg 3, option 12) gives the same sums; it is taken except for the two epilogues
+// that read two more operands per element (EPI_FACTOR, EPI_PROCB): with three waves per SIMD those spill registers
+// and run at half the epilogue's load depth, and lose more than the main loop gains (measured on the ViT-B step:
+// the d = 3072 SYRKs 907 -> 840 us, the PROCB products 1676 -> 1759 us).
+int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   if (g_force_cfg >= 0) return g_force_cfg;
   const int64_t t0 = gemm_bf16_tiles(M, N, tri, 0) * nb;
-  return t0 >= 160 || (t0 >= 128 && K >= 4096) ? 0 : 1;
+  if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return 1;
+  return g_ws && epi != EPI_FACTOR && epi != EPI_PROCB ? 3 : 0;
 }
 
 // Operand contract of the k-contiguous kernel (gemm_bf16, esz 2; its fp32 twin, esz 4): 16-byte aligned bases,
@@ -337,7 +343,7 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
     a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b]; a.CT[b] = o.CT[b];
     a.X1[b] = e.X1[b]; a.X2[b] = e.X2[b]; a.s[b] = e.s[b]; a.part[b] = e.part[b];
   }
-  int cfg = b16_cfg(M, N, K, tri, nb);
+  int cfg = b16_cfg(M, N, K, tri, nb, e.epi);
   if (esz == 4) cfg = 1;  // the fp32 kernel: the 128-tile configuration
   // a plain store whose 128-tiles would leave most of the chip idle: the small-problem kernel (64-tiles, k in
   // 512-byte chunks, two in flight). Measured crossovers against the pipelined kernels (launch of nb problems, in
@@ -2215,7 +2221,7 @@ int psgdk_set_option(int option, int value) {
     return PSGDK_OK;
   }
   if (option == 1) {
-    if (value < -1 || value > 2) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 2");
+    if (value < -1 || value > 3) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 3");
     g_force_cfg = value;
     return PSGDK_OK;
   }
@@ -2264,6 +2270,11 @@ int psgdk_set_option(int option, int value) {
     g_tiny = value;
     return PSGDK_OK;
   }
+  if (option == 12) {
+    if (value != 0 && value != 1) return fail(PSGDK_EINVAL, "option 12 (warp-specialized main loop) must be 0 or 1");
+    g_ws = value;
+    return PSGDK_OK;
+  }
   if (option == 6) {
     if (value < 0 || value > 8) return fail(PSGDK_EINVAL, "option 6 (grouped update side streams) must be 0 .. 8");
     g_upd_streams = value;
@@ -2276,7 +2287,7 @@ int psgdk_get_option(int option, int* value) {
   if (!value) return fail(PSGDK_EINVAL, "value is null");
   const int* opts[] = {&g_tile_order, &g_force_cfg,   &g_nlb_target, &g_vmm_u, &g_vmm_cols,
                        &g_t1q_pg,     &g_upd_streams, &g_rq16,       &g_f32kc, &g_big_batch, &g_small,
-                       &g_tiny};
+                       &g_tiny,       &g_ws};
   if (option < 0 || option >= (int)(sizeof opts / sizeof opts[0])) return fail(PSGDK_EINVAL, "unknown option %d", option);
   *value = *opts[option];
   return PSGDK_OK;

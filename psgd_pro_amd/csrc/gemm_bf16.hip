@@ -42,6 +42,9 @@ __device__ __forceinline__ int remap_xcd(int w, int G) {
 // the LDS serves without conflicts (measured: 4 cycles per ds_read_b128, against 8 with rows padded to 144
 // bytes); the 8 lanes that write one row still cover its 8 slots.
 __device__ __forceinline__ int swz(int row, int c) { return c ^ (row & 7); }
+// The 32 x 32 x 16 MFMA's fragment read: 16 lanes read one chunk of 16 consecutive rows. XORing with row bits 1-3
+// spreads them over 16 distinct bank groups (with row bits 0-2, rows r and r + 8 met: 2-way conflicts).
+__device__ __forceinline__ int swz32(int row, int c) { return c ^ ((row >> 1) & 7); }
 
 // Global -> register -> LDS staging of one ROWS x (8 chunks) tile with buffer loads. Lane `tid` owns the 16-byte
 // k chunk tid % 8 of rows tid / 8 + 32 i (i < NV): the lane part of the byte offset is the VGPR offset, the row
@@ -49,7 +52,7 @@ __device__ __forceinline__ int swz(int row, int c) { return c ^ (row & 7); }
 // past K (K is a multiple of a chunk) gets an offset beyond the buffer extent: it reads zero (or, where the scalar
 // part wraps the 32-bit sum, some element of the same buffer), and either way only feeds outputs that are not
 // stored.
-template <typename T, int ROWS, int NT>
+template <typename T, int ROWS, int NT, bool SW32 = false>
 struct Ld {
   static constexpr int CE = Kc<T>::CE, KP = 8 * CE;
   static constexpr int NV = ROWS * 8 / NT;  // 16-byte vectors per thread
@@ -69,11 +72,21 @@ struct Ld {
     }
   }
 
+  // load() for the producer waves of the warp-specialized loop: the same loads, with the lane's offset passed
+  // through an empty asm statement so that the compiler cannot hoist the eight per-row selects out of the k loop
+  // (kept across it they take eight more registers per operand, which the producer's two register sets leave no
+  // room for)
+  __device__ __forceinline__ void load_pinned(__amdgpu_buffer_rsrc_t rs, int voff, long long ld, int mn0, int rows,
+                                              int k0, int K, int t) {
+    asm volatile("" : "+v"(voff));
+    load(rs, voff, ld, mn0, rows, k0, K, t);
+  }
+
   __device__ __forceinline__ void store(T* lds, int t) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int v = t + NT * i, row = v >> 3, kv = v & 7;
-      *reinterpret_cast<uint4*>(lds + row * KP + swz(row, kv) * CE) = r[i];
+      *reinterpret_cast<uint4*>(lds + row * KP + (SW32 ? swz32(row, kv) : swz(row, kv)) * CE) = r[i];
     }
   }
 
@@ -113,13 +126,18 @@ struct Ld {
 // (the bf16 kernel) or float (its fp32 twin for k-contiguous fp32 operands: the same tiles, LDS layout, schedule
 // and epilogues, four fp32 MFMAs per fragment pair).
 // LAY (fp32 only): bit 0 set = A stored m-contiguous, bit 1 = B stored n-contiguous (the buffer's rows are k).
-template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0>
+// PW > 0 (bf16, 256 x 256 tiles on 2 x 4 waves): PW further waves only stage the operands (warp-specialized main
+// loop; see below); the WGM x WGN waves multiply on 32 x 32 x 16 MFMAs and run the epilogue.
+template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0, int PW = 0>
 __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   constexpr int CE = Kc<T>::CE, BK = 8 * CE, KP = BK, MPF = Kc<T>::MPF;
   using F = typename Kc<T>::F;
-  constexpr int NT = 64 * WGM * WGN;
+  constexpr int NT = 64 * WGM * WGN;  // the multiplying waves' threads
   constexpr int TM = BM / WGM, TN = BN / WGN;
-  constexpr bool PP = WGM == 2 && WGN == 4;  // ping-pong main loop (8 waves, two groups of 4)
+  constexpr bool WS = PW > 0;                       // warp-specialized: producer and MFMA waves
+  constexpr bool PP = !WS && WGM == 2 && WGN == 4;  // ping-pong main loop (8 waves, two groups of 4)
+  static_assert(!WS || (std::is_same_v<T, bf16_t> && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && PW == 4),
+                "warp-specialized main loop: bf16, 256 x 256 tiles, 8 MFMA waves, 4 producer waves");
   constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 tiles per wave along m, n
   extern __shared__ __align__(16) unsigned char smem[];
   T* const As0 = reinterpret_cast<T*>(smem);
@@ -150,6 +168,8 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   const T* __restrict__ Ap = reinterpret_cast<const T*>(p.A[b]);
   const T* __restrict__ Bp = reinterpret_cast<const T*>(p.tri ? p.A[b] : p.B[b]);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // a producer wave (WS): the test is on a scalar copy of the wave index, so both roles are scalar branches
+  const bool producer = WS && __builtin_amdgcn_readfirstlane(wave) >= WGM * WGN;
   const int wm = wave / WGN, wn = wave % WGN;
   const int r = lane & 15, g = lane >> 4;
 
@@ -166,6 +186,16 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto& dst = BLK ? part : acc;  // the MFMA accumulators of the main loop
+  // WS: 4 x 2 tiles of 32 x 32 per wave (element m of lane l at row 8 (m / 4) + 4 (l / 32) + m % 4, column l % 32)
+  f32x16_t acc32[WS ? 4 : 1][WS ? 2 : 1];
+  if constexpr (WS) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int m = 0; m < 16; ++m) acc32[i][j][m] = 0.f;
+  }
 
   // k tiles of this output tile: all of K, or (kbeg: A upper-triangular, zero left of the tile's first row) from the
   // k tile holding m0; kb is the k origin of the first one
@@ -248,7 +278,78 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       __builtin_amdgcn_sched_group_barrier(0x008, FN * MPF, 0);
     }
   };
-  if constexpr (!PP) {
+  if constexpr (WS) {
+    // Warp-specialized: the PW = 4 producer waves (one per SIMD) move every operand tile from HBM into LDS and
+    // multiply nothing; the 8 MFMA waves (two per SIMD, each 128 x 64 of the output as 4 x 2 tiles of 32 x 32)
+    // multiply from LDS and load nothing. One barrier per k tile: in the phase of tile kt the MFMA waves read LDS
+    // stage kt & 1 while the producers write tile kt + 1 into stage (kt + 1) & 1 and then request tile kt + 3. The
+    // producers hold two tiles in registers (two sets of 16 x 16 bytes per thread), so a tile's loads have two phases
+    // to arrive; the roles live in separate loops, so no wave holds both the accumulators and the staging registers.
+    // LDS rows are swizzled for the 32-row fragment reads (swz32). Loads past the last tile read zeros and their
+    // stage is never read.
+    if (producer) {
+      constexpr int NTP = 64 * PW;
+      const int t = tid - NT;
+      const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * CE) * (long long)sizeof(T));
+      const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * CE) * (long long)sizeof(T));
+      Ld<T, BM, NTP, true> la0, la1;
+      Ld<T, BN, NTP, true> lb0, lb1;
+      la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb, p.K, t);
+      lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb, p.K, t);
+      la1.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + BK, p.K, t);
+      lb1.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + BK, p.K, t);
+      la0.store(As0, t);
+      lb0.store(Bs0, t);
+      la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + 2 * BK, p.K, t);
+      lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + 2 * BK, p.K, t);
+      __syncthreads();
+      // Two phases per trip, so that the register set of each is static: the first stores set 1 (tile kt + 1),
+      // the second set 0. Both are unconditional inside the loop and an odd last phase is peeled after it: with a
+      // conditional second phase the compiler's wait counts at the loop head merge a path on which set 1 holds the
+      // newest loads, and the first phase then waits for every load in flight (vmcnt(0)), not for its own set only.
+      int kt = 0;
+      for (; kt + 1 < nk; kt += 2) {
+        la1.store(As0 + BM * KP, t);
+        lb1.store(Bs0 + BN * KP, t);
+        la1.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + (kt + 3) * BK, p.K, t);
+        lb1.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 3) * BK, p.K, t);
+        __syncthreads();
+        la0.store(As0, t);
+        lb0.store(Bs0, t);
+        la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + (kt + 4) * BK, p.K, t);
+        lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 4) * BK, p.K, t);
+        __syncthreads();
+      }
+      if (kt < nk) {
+        la1.store(As0 + BM * KP, t);
+        lb1.store(Bs0 + BN * KP, t);
+        __syncthreads();
+      }
+    } else {
+      // four k steps of 16 per tile; lane (c, hh) reads chunk 2 ks + hh of fragment rows c (row offsets are
+      // multiples of 32, so the swizzle is that of c)
+      const int c = lane & 31, hh = lane >> 5;
+      __syncthreads();
+      for (int kt = 0; kt < nk; ++kt) {
+        const T* As = As0 + (kt & 1) * BM * KP;
+        const T* Bs = Bs0 + (kt & 1) * BN * KP;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int ko = swz32(c, 2 * ks + hh) * CE;
+          F bq[2], aq[4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bq[j] = *reinterpret_cast<const F*>(Bs + (wn * TN + 32 * j + c) * KP + ko);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) aq[i] = *reinterpret_cast<const F*>(As + (wm * TM + 32 * i + c) * KP + ko);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc32[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[i], bq[j], acc32[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+      }
+    }
+  } else if constexpr (!PP) {
     const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * CE) * (long long)sizeof(T));
     const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * CE) * (long long)sizeof(T));
     Ld<T, BM, NT> la;
@@ -376,12 +477,25 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   auto half = [&](auto h_c) {
     constexpr int h = decltype(h_c)::value;
     // (1) park accumulators: tile (i, j) of this half at local row (i - h FM/2) * 16 + 4g + e, column 16 j + r
+    // (WS: 32 x 32 tile (i, j), i = 2h, 2h + 1, element m at local row (i - 2h) * 32 + 8 (m / 4) + 4 hh + m % 4,
+    // column 32 j + c)
+    if constexpr (WS) {
+      const int c = lane & 31, hh = lane >> 5;
 #pragma unroll
-    for (int ii = 0; ii < FM / 2; ++ii)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ep[ei(ii * 16 + g * 4 + e, j * 16 + r)] = acc[h * (FM / 2) + ii][j][e];
+          for (int m = 0; m < 16; ++m)
+            ep[ei(ii * 32 + 8 * (m >> 2) + 4 * hh + (m & 3), j * 32 + c)] = acc32[2 * h + ii][j][m];
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ep[ei(ii * 16 + g * 4 + e, j * 16 + r)] = acc[h * (FM / 2) + ii][j][e];
+    }
     __syncthreads();
     const int grow0 = m0 + wm * TM + h * HR;  // global row of local row 0
     const int gcol0 = n0 + wn * TN;
@@ -467,7 +581,8 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     // stores behind branches it cannot, and from the middle of the pass on its waits also cover earlier stores)
     auto row_pass_fast = [&](auto hc, auto hcb) {
       // (two fp32 operands in flight take 4 iterations ahead, within the register budget)
-      constexpr int IT = HR * (WC / 4) / 64, U = EPI == EPI_PROC ? 4 : 8, NBT = IT / U;
+      // (the warp-specialized kernel's three waves per SIMD leave fewer registers: half the depth)
+      constexpr int IT = HR * (WC / 4) / 64, U = (EPI == EPI_PROC ? 4 : 8) / (WS ? 2 : 1), NBT = IT / U;
       static_assert(IT % U == 0, "row pass: whole batches");
       constexpr bool L1 = EPI == EPI_FACTOR || EPI == EPI_PROC || EPI == EPI_PROCB || EPI == EPI_STRACE;
       constexpr int HC = decltype(hc)::value, HCB = decltype(hcb)::value;  // 1 stored, 0 not, -1 known at run time
@@ -525,7 +640,7 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     // into the parked values before the row pass adds Qn. Interior tiles issue the loads 8 iterations ahead.
     auto tcol_pass = [&](auto fast_c) {
       constexpr bool FAST = decltype(fast_c)::value;
-      constexpr int IT = WC * (HR / 4) / 64, U = 8, NBT = IT / U;
+      constexpr int IT = WC * (HR / 4) / 64, U = WS ? 4 : 8, NBT = IT / U;
       static_assert(IT % U == 0, "transposed column pass: whole batches");
       const float c2 = 0.5f * s0 * s0 * s1;
       const bf16_t* __restrict__ X2b = reinterpret_cast<const bf16_t*>(X2);
@@ -696,8 +811,14 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       __syncthreads();
     }
   };
-  half(std::integral_constant<int, 0>{});
-  half(std::integral_constant<int, 1>{});
+  if (!producer) {
+    half(std::integral_constant<int, 0>{});
+    half(std::integral_constant<int, 1>{});
+  } else {  // producer waves (WS): the epilogue's barriers, nothing else (each half: parking, row pass, and the
+            // transposed and column passes where the epilogue has them)
+    const int nbar = 2 * (2 + (EPI == EPI_PROCB ? 1 : 0) + (colpass ? 1 : 0));
+    for (int i = 0; i < nbar; ++i) __syncthreads();
+  }
   if constexpr (EPI == EPI_RQ || EPI == EPI_SUMSQ || EPI == EPI_STRACE) {
     __shared__ float red[16];
     t1 = block_sum(t1, red);
@@ -709,9 +830,9 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_kernel(const GB16Args p) {
-  gemm_kc_body<bf16_t, BM, BN, WGM, WGN, EPI>(p);
+template <int BM, int BN, int WGM, int WGN, int EPI, int PW = 0>
+__global__ void __launch_bounds__(64 * (WGM * WGN + PW)) gemm_bf16_kernel(const GB16Args p) {
+  gemm_kc_body<bf16_t, BM, BN, WGM, WGN, EPI, 0, PW>(p);
 }
 
 // two workgroups per CU (two waves per SIMD): the register budget of every layout
@@ -726,14 +847,14 @@ int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
   return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0>
+template <typename T, int BM, int BN, int WGM, int WGN, int EPI, int LAY = 0, int PW = 0>
 static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   constexpr int NW = WGM * WGN;
   constexpr int smem_main = 2 * (BM + BN) * 128,
                 smem_epi = NW * (BM / WGM / 2) * epi_pitch(BM / WGM / 2, BN / WGN) * 4;
   constexpr int smem = smem_main > smem_epi ? smem_main : smem_epi;
   void (*fn)(GB16Args) = nullptr;
-  if constexpr (std::is_same_v<T, bf16_t>) fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI>;
+  if constexpr (std::is_same_v<T, bf16_t>) fn = gemm_bf16_kernel<BM, BN, WGM, WGN, EPI, PW>;
   else fn = gemm_f32kc_kernel<BM, BN, WGM, WGN, EPI, LAY>;
   // once per instantiation (a function-local static is initialised once, also under concurrent first calls)
   static const hipError_t attr =
@@ -742,34 +863,36 @@ static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;
-  hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(64 * NW), smem, st, a);
+  hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(64 * (NW + PW)), smem, st, a);
   return hipGetLastError();
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int LAY = 0>
+template <typename T, int BM, int BN, int WGM, int WGN, int LAY = 0, int PW = 0>
 static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
   constexpr bool B16 = std::is_same_v<T, bf16_t>;
   switch (a.epi) {
-    case EPI_FACTOR: return launch_b16<T, BM, BN, WGM, WGN, EPI_FACTOR, LAY>(a, st);
-    case EPI_PROC: return launch_b16<T, BM, BN, WGM, WGN, EPI_PROC, LAY>(a, st);
-    case EPI_SCALE: return launch_b16<T, BM, BN, WGM, WGN, EPI_SCALE, LAY>(a, st);
-    case EPI_SUMSQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_SUMSQ, LAY>(a, st);
-    case EPI_STRACE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STRACE, LAY>(a, st);
-    case EPI_STORE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STORE, LAY>(a, st);
-    case EPI_RQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_RQ, LAY>(a, st);  // R read as T
+    case EPI_FACTOR: return launch_b16<T, BM, BN, WGM, WGN, EPI_FACTOR, LAY, PW>(a, st);
+    case EPI_PROC: return launch_b16<T, BM, BN, WGM, WGN, EPI_PROC, LAY, PW>(a, st);
+    case EPI_SCALE: return launch_b16<T, BM, BN, WGM, WGN, EPI_SCALE, LAY, PW>(a, st);
+    case EPI_SUMSQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_SUMSQ, LAY, PW>(a, st);
+    case EPI_STRACE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STRACE, LAY, PW>(a, st);
+    case EPI_STORE: return launch_b16<T, BM, BN, WGM, WGN, EPI_STORE, LAY, PW>(a, st);
+    case EPI_RQ: return launch_b16<T, BM, BN, WGM, WGN, EPI_RQ, LAY, PW>(a, st);  // R read as T
     default: break;
   }
   if constexpr (B16) {  // reads a bf16 X operand
-    if (a.epi == EPI_PROCB) return launch_b16<T, BM, BN, WGM, WGN, EPI_PROCB, LAY>(a, st);
+    if (a.epi == EPI_PROCB) return launch_b16<T, BM, BN, WGM, WGN, EPI_PROCB, LAY, PW>(a, st);
   }
   return hipErrorInvalidValue;
 }
 
 // cfg 0: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64; cfg 1: 128 x 128 tiles, 4 waves of 64 x 64;
-// cfg 2: 256 x 256 tiles, 4 waves of 128 x 128 (one wave per SIMD)
+// cfg 2: 256 x 256 tiles, 4 waves of 128 x 128 (one wave per SIMD); cfg 3: 256 x 256 tiles, 8 MFMA waves of
+// 128 x 64 on 32 x 32 x 16 MFMAs plus 4 producer waves (warp-specialized main loop)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st) {
   if (cfg == 1) return launch_epi<bf16_t, 128, 128, 2, 2>(a, st);
   if (cfg == 2) return launch_epi<bf16_t, 256, 256, 2, 2>(a, st);
+  if (cfg == 3) return launch_epi<bf16_t, 256, 256, 2, 4, 0, 4>(a, st);
   return launch_epi<bf16_t, 256, 256, 2, 4>(a, st);
 }
 

@@ -64,7 +64,7 @@ def test_argument_validation():
     assert lib.psgdk_symm(0, 0, 3, 8, 8, 0, 1, one, 8, one, 8, one, 8, None) == L.EINVAL
 
 
-DEFAULTS = {0: 2, 1: -1, 2: 1024, 3: 4, 4: -1, 5: 1, 6: 3, 7: 1, 8: 1, 9: 64, 10: 128, 11: 64}
+DEFAULTS = {0: 2, 1: -1, 2: 1024, 3: 4, 4: -1, 5: 1, 6: 3, 7: 1, 8: 1, 9: 64, 10: 128, 11: 64, 12: 1}
 
 
 def _get(opt):
@@ -77,10 +77,10 @@ def test_option_ranges():
     """psgdk_set_option accepts each option's documented values and refuses the rest (host state only)."""
     lib = L.lib()
     try:
-        for opt, good, bad in [(0, [0, 1, 2], [3, -1]), (1, [-1, 0, 1, 2], [3, -2]), (2, [1, 4096], [0, -5]),
+        for opt, good, bad in [(0, [0, 1, 2], [3, -1]), (1, [-1, 0, 1, 2, 3], [4, -2]), (2, [1, 4096], [0, -5]),
                                (3, [2, 4, 8], [1, 16]), (4, [-1, 0, 1, 2, 3], [4, -2]), (5, [0, 1], [2]),
                                (6, [0, 3, 8], [9, -1]), (7, [0, 1], [2]), (8, [0, 1], [2]), (9, [1, 12, 64], [0, 65]),
-                               (10, [0, 64, 1000], [-1]), (11, [0, 16, 1000], [-1])]:
+                               (10, [0, 64, 1000], [-1]), (11, [0, 16, 1000], [-1]), (12, [0, 1], [2, -1])]:
             for v in bad:
                 assert lib.psgdk_set_option(opt, v) == L.EINVAL, (opt, v)
             for v in good:
