@@ -217,6 +217,25 @@ int psgdk_kron2d_update_groups_ev(int ngroups, const psgdk_kron2d_t* const* grou
                                   const float* const* const* V, void* ws, size_t* ws_bytes, psgdk_stream_t stream,
                                   psgdk_event_t const* group_done);
 
+/* A group's noise drawn inside the update instead of read from a buffer: problem b's m x n noise (row-major) is
+ * the normals offset[b] .. offset[b] + m n - 1 of the sequence psgdk_fill_normal(.., seed, stream_id, ..) writes,
+ * rounded to the group's g_dtype as that call rounds them, so the update equals, bit for bit, the one that reads a
+ * buffer filled by psgdk_fill_normal at those offsets. offset[b] >= 0, a multiple of 4. */
+typedef struct psgdk_draws {
+  uint64_t seed;
+  uint64_t stream_id;
+  int64_t offset[PSGDK_MAXB];
+} psgdk_draws_t;
+
+/* psgdk_kron2d_update_groups_ev where each group takes its noise either from noise[g] (device pointers, as there)
+ * or, with noise NULL or noise[g] NULL, from draws[g]: the normals are generated by the kernel that forms the
+ * noisy gradient, so the step writes and reads no noise buffer. group_done may be NULL (no events). Replaces
+ * psgd_pro.py:123 / psgd_pro_fast.py:200-206 (torch.randn_like(G) into memory, then G + (damping + eps |G|) V). */
+int psgdk_kron2d_update_groups_drawn(int ngroups, const psgdk_kron2d_t* const* groups,
+                                     const psgdk_update_opts_t* const* opts, const void* const* const* noise,
+                                     const psgdk_draws_t* const* draws, const float* const* const* V, void* ws,
+                                     size_t* ws_bytes, psgdk_stream_t stream, psgdk_event_t const* group_done);
+
 /* Precondition, clip and update: pre = P1 G P2 (apply_2d, psgd_pro_fast.py:156-161 = precond_grad_kron,
  * psgd_pro.py:107-112), clip to RMS <= max_avg_amp and |.| <= max_element_amp, param -= lr_params * clipped
  * (psgd_pro.py:371-381). pre_out[b] / clipped_out[b] (m x n fp32, optional: NULL array or NULL entries) receive

@@ -46,6 +46,12 @@ class ApplyOpts(C.Structure):
                 ("tri", C.c_int32)]
 
 
+class Draws(C.Structure):
+    """psgdk_draws_t: a group's noise generated inside the update (normals offset[b] .. of the
+    psgdk_fill_normal(seed, stream_id) sequence)."""
+    _fields_ = [("seed", C.c_uint64), ("stream_id", C.c_uint64), ("offset", C.c_int64 * MAXB)]
+
+
 class ProfRecord(C.Structure):
     _fields_ = [("kernel_id", C.c_int32), ("tri", C.c_int32), ("nb", C.c_int32), ("ms", C.c_float),
                 ("flops", C.c_double), ("bytes", C.c_double)]
@@ -78,6 +84,9 @@ _SIGS = {
                                           C.POINTER(_vpa), C.POINTER(_vpa), _vp, _szp, _vp]),
     "psgdk_kron2d_update_groups_ev": (_i32, [_i32, C.POINTER(C.POINTER(Kron2d)), C.POINTER(C.POINTER(UpdateOpts)),
                                              C.POINTER(_vpa), C.POINTER(_vpa), _vp, _szp, _vp, _vpa]),
+    "psgdk_kron2d_update_groups_drawn": (_i32, [_i32, C.POINTER(C.POINTER(Kron2d)),
+                                                C.POINTER(C.POINTER(UpdateOpts)), C.POINTER(_vpa),
+                                                C.POINTER(C.POINTER(Draws)), C.POINTER(_vpa), _vp, _szp, _vp, _vpa]),
     "psgdk_kron2d_apply": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_apply2d": (_i32, [C.POINTER(Kron2d), C.POINTER(ApplyOpts), _vpa, _vpa, _vpa, _vp, _szp, _vp]),
     "psgdk_factor_update": (_i32, [_i32, _i64, _i32, _vpa, _i32, _vpa, _vpa, _vpa, _vpa, C.c_float, C.c_float,

@@ -1065,9 +1065,11 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
 // one side d (largest first), the items of a batch ordered by their other side.
 // group_done (optional): per group an event recorded once that group's factors, L and shadows are final (its
 // items' batches done), so that a caller can start work on one group before the whole call has finished.
+// draws (optional): group gi with no noise pointers (noise or noise[gi] null) generates its noise from draws[gi].
 int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_update_opts_t* const* os,
                       const void* const* const* noise, const float* const* const* V, void* ws, size_t* ws_bytes,
-                      hipStream_t st, const hipEvent_t* group_done = nullptr) {
+                      hipStream_t st, const hipEvent_t* group_done = nullptr,
+                      const psgdk_draws_t* const* draws = nullptr) {
   Ws w(ws);
   std::vector<std::vector<bf16_t*>> Xb(ng), YTb(ng), Pgb(ng), PgTb(ng);
   std::vector<std::vector<float*>> dterm(ng);  // a diagonal factor's term1
@@ -1125,10 +1127,33 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
   for (size_t k = 0; k < batches.size(); ++k) nlb_take(w, batches[k][0]->d, (int)batches[k].size(), nws[k]);
   if (!ws) { *ws_bytes = w.off; return PSGDK_OK; }
   if (*ws_bytes < w.off) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, w.off);
+  // group gi's noise: noise[gi] when given, else draws[gi]
+  auto drawn = [&](int gi) { return (!noise || !noise[gi]) ? draws[gi] : nullptr; };
   for (int gi = 0; gi < ng; ++gi) {
-    PSGDK_TRY(check_ptrs(noise[gi], gs[gi]->nb, "noise"));
+    if (!noise || !noise[gi]) {
+      if (!draws || !draws[gi]) return fail(PSGDK_EINVAL, "group %d: neither noise pointers nor draws", gi);
+      for (int b = 0; b < gs[gi]->nb; ++b)
+        if (draws[gi]->offset[b] < 0 || draws[gi]->offset[b] % 4 || draws[gi]->offset[b] > ((int64_t)1 << 60))
+          return fail(PSGDK_EINVAL, "group %d: draw offset[%d] = %lld (a multiple of 4 in 0 .. 2^60)", gi, b,
+                      (long long)draws[gi]->offset[b]);
+    } else {
+      PSGDK_TRY(check_ptrs(noise[gi], gs[gi]->nb, "noise"));
+    }
     PSGDK_TRY(check_ptrs(V[gi], gs[gi]->nb, "V"));
   }
+  // the noise of group gi into a noise kernel's arguments
+  auto set_noise = [&](EwArgs& a, int gi) {
+    const psgdk_draws_t* d = drawn(gi);
+    if (d) {
+      a.draw = 1;
+      a.dk0 = (unsigned)d->seed; a.dk1 = (unsigned)(d->seed >> 32);
+      a.ds0 = (unsigned)d->stream_id; a.ds1 = (unsigned)(d->stream_id >> 32);
+    }
+    for (int b = 0; b < gs[gi]->nb; ++b) {
+      if (d) a.doff[b] = d->offset[b];
+      else a.in2[b] = reinterpret_cast<const float*>(noise[gi][b]);
+    }
+  };
   // streams: the per-group phase of group gi and batch k run on side stream gi % S and k % S; every batch starts
   // after every group's Pg exists. Under HIP graph capture everything stays on the caller's stream: a capture that
   // forked onto these side streams ended in a host-side crash inside the end of the capture, so that combination
@@ -1170,9 +1195,10 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
       std::memset(&a, 0, sizeof a);
       a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
       for (int b = 0; b < nb; ++b) {
-        a.in[b] = g->G[b]; a.in2[b] = reinterpret_cast<const float*>(noise[gi][b]); a.in3[b] = g->P[1][b];
+        a.in[b] = g->G[b]; a.in3[b] = g->P[1][b];
         a.out2[b] = Xb[gi][b];
       }
+      set_noise(a, gi);
       PSGDK_HIP(noise_t_launch(a, st), "noise (transposed, column-scaled)");
       B16Out out;
       out.ldcb = n; out.ldct = m;
@@ -1185,9 +1211,10 @@ int b16_update_groups(int ng, const psgdk_kron2d_t* const* gs, const psgdk_updat
         std::memset(&a, 0, sizeof a);
         a.nb = nb; a.m = m; a.n = n; a.dt = g->g_dtype; a.f0 = os[gi]->damping; a.f1 = os[gi]->grad_eps;
         for (int b = 0; b < nb; ++b) {
-          a.in[b] = g->G[b]; a.in2[b] = reinterpret_cast<const float*>(noise[gi][b]); a.out2[b] = Xb[gi][b];
+          a.in[b] = g->G[b]; a.out2[b] = Xb[gi][b];
           a.in3[b] = d0 ? nullptr : g->P[0][b];
         }
+        set_noise(a, gi);
         PSGDK_HIP(noise_launch(a, st), "noise");
       }
       if (d0) {
@@ -1993,6 +2020,21 @@ int psgdk_kron2d_update_groups(int ngroups, const psgdk_kron2d_t* const* groups,
   }
   if (ws && (!noise || !V)) return fail(PSGDK_EINVAL, "null noise or V");
   return b16_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int psgdk_kron2d_update_groups_drawn(int ngroups, const psgdk_kron2d_t* const* groups,
+                                     const psgdk_update_opts_t* const* opts, const void* const* const* noise,
+                                     const psgdk_draws_t* const* draws, const float* const* const* V, void* ws,
+                                     size_t* ws_bytes, psgdk_stream_t stream, psgdk_event_t const* group_done) {
+  // the checks of psgdk_kron2d_update_groups (its size query takes no noise), then the call
+  size_t need = 0;
+  PSGDK_TRY(psgdk_kron2d_update_groups(ngroups, groups, opts, nullptr, nullptr, nullptr, &need, stream));
+  if (!ws) { *ws_bytes = need; return PSGDK_OK; }
+  if (*ws_bytes < need) return fail(PSGDK_EWORKSPACE, "workspace %zu < %zu bytes", *ws_bytes, need);
+  if (!V) return fail(PSGDK_EINVAL, "null V");
+  if (!noise && !draws) return fail(PSGDK_EINVAL, "null noise and draws");
+  return b16_update_groups(ngroups, groups, opts, noise, V, ws, ws_bytes, (hipStream_t)stream,
+                           reinterpret_cast<const hipEvent_t*>(group_done), draws);
 }
 
 int psgdk_kron2d_update_groups_ev(int ngroups, const psgdk_kron2d_t* const* groups,

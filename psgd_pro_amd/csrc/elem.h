@@ -19,6 +19,11 @@ struct EwArgs {
   void* out2[MAXB];
   float* sc[MAXB];         // device scalars
   float* aux[MAXB];        // kernel-specific extra output
+  // noise kernels: draw = 1 generates the noise N instead of reading in2: problem b's element i is normal
+  // doff[b] + i of the Philox4x32-10 sequence keyed (dk0, dk1) on counter words (ds0, ds1) (normal_fill_launch's)
+  int draw;
+  unsigned dk0, dk1, ds0, ds1;
+  long long doff[MAXB];
 };
 
 // X = G + (damping + eps |G|) * N  (fp32 into out and / or bf16 into out2; N in G's dtype dt; N null: X = G)

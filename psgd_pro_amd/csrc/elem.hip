@@ -80,6 +80,57 @@ __device__ __forceinline__ void ew_range8(long long total, int blocks_per, long 
   ew_range(total >> 3, blocks_per, beg, end);
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Standard normals from a counter-based generator: Philox4x32 with 10 rounds (Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011), key = the 64-bit seed, counter = (block b of four
+// outputs, as two 32-bit words; the 64-bit stream id as two words). A round multiplies words 0 and 2 by the
+// published constants 0xD2511F53 and 0xCD9E8D57, keeps the low halves and XORs the high halves with words 1, 3 and
+// the key; the key is bumped by the Weyl increments 0x9E3779B9 and 0xBB67AE85 between rounds. Each word x gives
+// the uniform u = (floor(x / 256) + 1/2) 2^-24 in (0, 1), exact in fp32 (so ln u keeps its precision next to 1),
+// and each pair (u0, u1) two normals by the Box-Muller transform,
+// sqrt(-2 ln u0) (cos 2 pi u1, sin 2 pi u1). Output b covers elements 4 b .. 4 b + 3 (fp32, or bf16 rounded from
+// the fp32 value).
+__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
+    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
+    c[0] = hi1 ^ c[1] ^ k0;
+    c[1] = lo1;
+    c[2] = hi0 ^ c[3] ^ k1;
+    c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// The four normals of output block blk (elements 4 blk .. 4 blk + 3) as normal_fill_kernel computes them, before
+// the storage rounding.
+__device__ __forceinline__ void philox_normals4(unsigned long long blk, uint32_t k0, uint32_t k1, uint32_t s0,
+                                                uint32_t s1, float (&z)[4]) {
+  uint32_t c[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), s0, s1};
+  philox4x32_10(c, k0, k1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float u0 = ((float)(c[2 * h] >> 8) + 0.5f) * 5.9604644775390625e-8f;  // 2^-24
+    const float u1 = ((float)(c[2 * h + 1] >> 8) + 0.5f) * 5.9604644775390625e-8f;
+    // the hardware transcendentals: v_log_f32 (log2), v_sqrt_f32, and v_sin_f32 / v_cos_f32, which take their
+    // argument in revolutions (sin 2 pi u1 directly); -2 ln u0 = -2 ln 2 log2 u0
+    const float r = __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(u0));
+    z[2 * h] = r * __builtin_amdgcn_cosf(u1);
+    z[2 * h + 1] = r * __builtin_amdgcn_sinf(u1);
+  }
+}
+// a normal as stored in dtype dt (0 fp32, 1 bf16) and read back as float, as the noise kernels read a filled buffer
+__device__ __forceinline__ float stored_normal(float z, int dt) { return dt ? bf16_to_f32(f32_to_bf16(z)) : z; }
+// element j of the drawn sequence, as stored in dtype dt (the block's four normals computed for one of them)
+__device__ __forceinline__ float drawn_normal(const EwArgs& a, unsigned long long j, int dt) {
+  float z[4];
+  philox_normals4(j >> 2, a.dk0, a.dk1, a.ds0, a.ds1, z);
+  const int e = (int)(j & 3);
+  return stored_normal(e == 0 ? z[0] : e == 1 ? z[1] : e == 2 ? z[2] : z[3], dt);
+}
+
 __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int blocks_per) {
   const int b = blockIdx.x / blocks_per;
   long long beg, end;
@@ -89,13 +140,25 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   bf16_t* Xb = reinterpret_cast<bf16_t*>(a.out2[b]);
   const float* rsc = a.in3[b];  // optional row scale (a diagonal P1 folded into the input of P1 X P2)
   const long long total = a.m * a.n;
+  const bool drawn = a.draw != 0;
+  const unsigned long long doff = drawn ? (unsigned long long)a.doff[b] : 0ull;
   if ((total & 7) == 0 && (a.n & 7) == 0 && al16(G) && (!N || al16(N)) && (!X || al16(X)) && (!Xb || al16(Xb))) {
     ew_range8(total, blocks_per, beg, end);
     for (long long v = beg + threadIdx.x; v < end; v += EW_THREADS) {
       float g[8], nz[8];
       ew_load8_dt(G, a.dt, 8 * v, g);
-      if (N) {
+      if (drawn) {  // elements doff + 8 v .. + 7: two whole blocks (doff is a multiple of 4)
+        float z[4];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          philox_normals4((doff >> 2) + 2ull * (unsigned long long)v + q, a.dk0, a.dk1, a.ds0, a.ds1, z);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) nz[4 * q + e] = stored_normal(z[e], a.dt);
+        }
+      } else if (N) {
         ew_load8_dt(N, a.dt, 8 * v, nz);
+      }
+      if (drawn || N) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) g[e] = g[e] + (a.f0 + a.f1 * fabsf(g[e])) * nz[e];
       }
@@ -112,7 +175,9 @@ __global__ void __launch_bounds__(EW_THREADS) noise_kernel(const EwArgs a, int b
   ew_range(total, blocks_per, beg, end);
   for (long long i = beg + threadIdx.x; i < end; i += EW_THREADS) {
     const float g = ldv(G, a.dt, i);
-    float x = N ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, i) : g;
+    float x = drawn ? g + (a.f0 + a.f1 * fabsf(g)) * drawn_normal(a, doff + (unsigned long long)i, a.dt)
+              : N   ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, i)
+                    : g;
     if (rsc) x *= rsc[i / a.n];
     if (X) X[i] = x;
     if (Xb) Xb[i] = f32_to_bf16(x);
@@ -147,7 +212,9 @@ __global__ void __launch_bounds__(256) noise_t_kernel(const EwArgs a) {
     if (gi < m && gj < n) {
       const long long o = gi * n + gj;
       const float g = ldv(G, a.dt, o);
-      x = N ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, o) : g;
+      x = a.draw ? g + (a.f0 + a.f1 * fabsf(g)) * drawn_normal(a, (unsigned long long)a.doff[b] + o, a.dt)
+          : N    ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, o)
+                 : g;
       if (csc) x *= csc[gj];
     }
     t[r][c] = x;
@@ -834,48 +901,13 @@ hipError_t momentum_multi_launch(const MomList& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// Standard normals from a counter-based generator: Philox4x32 with 10 rounds (Salmon, Moraes, Dror and Shaw,
-// "Parallel random numbers: as easy as 1, 2, 3", SC 2011), key = the 64-bit seed, counter = (block b of four
-// outputs, as two 32-bit words; the 64-bit stream id as two words). A round multiplies words 0 and 2 by the
-// published constants 0xD2511F53 and 0xCD9E8D57, keeps the low halves and XORs the high halves with words 1, 3 and
-// the key; the key is bumped by the Weyl increments 0x9E3779B9 and 0xBB67AE85 between rounds. Each word x gives
-// the uniform u = (floor(x / 256) + 1/2) 2^-24 in (0, 1), exact in fp32 (so ln u keeps its precision next to 1),
-// and each pair (u0, u1) two normals by the Box-Muller transform,
-// sqrt(-2 ln u0) (cos 2 pi u1, sin 2 pi u1). Output b covers elements 4 b .. 4 b + 3 (fp32, or bf16 rounded from
-// the fp32 value).
-__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
-    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
-    c[0] = hi1 ^ c[1] ^ k0;
-    c[1] = lo1;
-    c[2] = hi0 ^ c[3] ^ k1;
-    c[3] = lo0;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-}
-
 __global__ void __launch_bounds__(EW_THREADS) normal_fill_kernel(void* out, long long n, int dt, uint32_t k0,
                                                                    uint32_t k1, uint32_t s0, uint32_t s1) {
   const long long nblk = (n + 3) / 4;
   for (long long blk = (long long)blockIdx.x * EW_THREADS + threadIdx.x; blk < nblk;
        blk += (long long)gridDim.x * EW_THREADS) {
-    uint32_t c[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), s0, s1};
-    philox4x32_10(c, k0, k1);
     float z[4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float u0 = ((float)(c[2 * h] >> 8) + 0.5f) * 5.9604644775390625e-8f;  // 2^-24
-      const float u1 = ((float)(c[2 * h + 1] >> 8) + 0.5f) * 5.9604644775390625e-8f;
-      // the hardware transcendentals: v_log_f32 (log2), v_sqrt_f32, and v_sin_f32 / v_cos_f32, which take their
-      // argument in revolutions (sin 2 pi u1 directly); -2 ln u0 = -2 ln 2 log2 u0
-      const float r = __builtin_amdgcn_sqrtf(-1.3862943611198906f * __builtin_amdgcn_logf(u0));
-      z[2 * h] = r * __builtin_amdgcn_cosf(u1);
-      z[2 * h + 1] = r * __builtin_amdgcn_sinf(u1);
-    }
+    philox_normals4((unsigned long long)blk, k0, k1, s0, s1, z);
     const long long i0 = 4 * blk;
     if (dt == 1) {  // bf16 storage (dtype codes: 0 fp32, 1 bf16)
       bf16_t* o = reinterpret_cast<bf16_t*>(out) + i0;

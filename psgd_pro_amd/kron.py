@@ -14,9 +14,12 @@ factor). Tensors of order 3 or more are rejected (NotImplementedError).
 Random draws (psgd_pro.py:123,35,59,138,345): draws="host" reproduces psgd_pro.py's stream on a CPU generator
 (update coin, then per parameter the damping noise, two 32 x d starts per dense factor, the balancing coin) and
 uploads the normals; draws="device" draws the coins on the CPU (update coin, then one balancing coin per parameter,
-as psgd_pro_fast.py:482-483), then a 62-bit seed, and the library fills the step's normals on the GPU from it
-(Philox4x32-10 and Box-Muller, psgdk_fill_normal: one launch per dtype buffer).
+as psgd_pro_fast.py:482-483), then a 62-bit seed, and the library draws the step's normals on the GPU from it
+(Philox4x32-10 and Box-Muller): psgdk_fill_normal fills the float32 buffer (the norm bounds' starts, float32 noise),
+and bf16 noise is generated inside the grouped update's noise kernel (psgdk_kron2d_update_groups_drawn), the same
+values as a filled bf16 buffer would hold.
 """
+import collections
 import contextlib
 import ctypes
 
@@ -26,6 +29,8 @@ from . import _lib as L
 from .ops import EagerOps
 
 _K = L.NLB_K
+# a parameter's noise generated inside the update: normals offset .. of the Philox sequence (seed, stream_id)
+_Drawn = collections.namedtuple("_Drawn", "seed stream_id offset")
 
 
 def _is_dense(size, numel, max_size, max_skew):
@@ -158,6 +163,7 @@ class KronWhiten:
         self._fuse = bool(fuse_groups)
         self._gev = {}  # per group: the event its update records when its factors are final
         self._overlap = True  # False: the whole update, then every balance, then every apply (each a fork / join)
+        self._draw_in_update = True  # device draws: bf16 noise generated inside grouped updates (no noise buffer)
         self._draw_buf = self._draw_buf16 = None
         self._init_scale = preconditioner_init_scale
         if preconditioner_init_scale is not None:
@@ -280,8 +286,9 @@ class KronWhiten:
         returns (per-parameter noise views, per-parameter V views, balance coins). The noise is drawn in the dtype
         of the tensor the update reads (the gradient, or the float32 momentum buffer when whiten_grad is off), as
         randn_like(G) does (psgd_pro_fast.py:200-206), the starts in float32 (the factors' dtype). Two persistent
-        device buffers (fixed addresses: captured graphs read them), one per dtype, each view at a multiple of 8
-        elements."""
+        device buffers, one per dtype, each view at a multiple of 8 elements. With device draws, bf16 noise that only
+        grouped updates read is not written to its buffer: its entries are _Drawn records (seed, stream id, offset
+        in that buffer's layout), from which the update's noise kernel generates the same values."""
         ndt = [g.dtype if self._whiten_grad else torch.float32 for g in grads]
         r8 = lambda x: (x + 7) // 8 * 8
         lay, tot = [], {torch.float32: 0, torch.bfloat16: 0}  # per parameter: (noise offset, V offset, sizes)
@@ -293,8 +300,15 @@ class KronWhiten:
             tot[torch.float32] += r8(b)
             lay.append((no, vo, a, b))
         dev = grads[0].device
+        # device draws whose bf16 noise only grouped bf16-path updates read: that noise is generated inside the
+        # update (psgdk_kron2d_update_groups_drawn, the same values) and the bf16 buffer is neither filled nor read
+        fused_idx = {p.index for g in self._split_groups()[0] for p in g.members}
+        drawn16 = self._draw_in_update and self._draws == "device" and tot[torch.bfloat16] > 0 and all(
+            i in fused_idx for i, dt in enumerate(ndt) if dt == torch.bfloat16)
         bufs = {}
         for dt, attr in ((torch.float32, "_draw_buf"), (torch.bfloat16, "_draw_buf16")):
+            if dt == torch.bfloat16 and drawn16:
+                continue
             cur = getattr(self, attr, None)
             if cur is None or cur.numel() < max(1, tot[dt]):
                 cur = torch.empty(max(1, tot[dt]), device=dev, dtype=dt)
@@ -322,12 +336,13 @@ class KronWhiten:
             seed = int(torch.randint(0, 2 ** 62, (1,), generator=self._gen))
             st = L.stream_of(bufs[torch.float32])
             for sid, dt in enumerate((torch.float32, torch.bfloat16)):
-                if tot[dt]:
+                if tot[dt] and dt in bufs:
                     L.check(L.lib().psgdk_fill_normal(ctypes.c_void_p(bufs[dt].data_ptr()), tot[dt], L.dtype_code(dt),
                                                       seed, sid, st))
         noise, V = [], []
         for dt, (no, vo, a, b) in zip(ndt, lay):
-            noise.append(bufs[dt][no:no + a])
+            # stream id 1: the bf16 sequence (psgdk_fill_normal's stream_id of the bf16 buffer)
+            noise.append(_Drawn(seed, 1, no) if dt not in bufs else bufs[dt][no:no + a])
             V.append(bufs[torch.float32][vo:vo + b] if b else None)
         return noise, V, coins
 
@@ -404,12 +419,21 @@ class KronWhiten:
         """One grouped update of the bf16-path groups on the current stream (psgdk_kron2d_update_groups; with
         events, psgdk_kron2d_update_groups_ev, which records each group's event once its factors are final)."""
         o = self._update_opts()
-        opts, nzs, vvs = [], [], []
+        opts, nzs, vvs, drs = [], [], [], []
         for grp in fused:
             og = L.UpdateOpts(o.lr, o.betaL, o.damping, 0.0, o.tri, o.r2)
             og.grad_eps = torch.finfo(self._bind_sources(grp, srcs)).eps
             opts.append(og)
-            nzs.append(L.ptrs([noise[p.index] for p in grp.members]))
+            nz = [noise[p.index] for p in grp.members]
+            if isinstance(nz[0], _Drawn):  # a group's members share the gradient dtype, so all or none are drawn
+                d = L.Draws(nz[0].seed, nz[0].stream_id)
+                for b, x in enumerate(nz):
+                    d.offset[b] = x.offset
+                drs.append(ctypes.pointer(d))
+                nzs.append(None)
+            else:
+                drs.append(None)
+                nzs.append(L.ptrs(nz))
             vvs.append(L.ptrs([V[p.index] for p in grp.members]))
         ng = len(fused)
         garr = (ctypes.POINTER(L.Kron2d) * ng)(*[ctypes.pointer(g.struct) for g in fused])
@@ -417,6 +441,16 @@ class KronWhiten:
         narr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*nzs)
         varr = (ctypes.POINTER(ctypes.c_void_p) * ng)(*vvs)
         st = L.stream_of(srcs[0])
+        if any(d is not None for d in drs):
+            darr = (ctypes.POINTER(L.Draws) * ng)(*drs)
+            earr = L.ptrs([ev.cuda_event for ev in events]) if events is not None else None
+            fn = L.lib().psgdk_kron2d_update_groups_drawn
+            sz = ctypes.c_size_t(0)
+            L.check(fn(ng, garr, oarr, narr, darr, varr, None, ctypes.byref(sz), st, earr))
+            buf = ln.ws_upd.get(sz.value, dev)
+            sz2 = ctypes.c_size_t(buf.numel())
+            L.check(fn(ng, garr, oarr, narr, darr, varr, ctypes.c_void_p(buf.data_ptr()), ctypes.byref(sz2), st, earr))
+            return
         if events is None:
             L.call_ws(L.lib().psgdk_kron2d_update_groups, ng, garr, oarr, narr, varr, ws=ln.ws_upd, device=dev,
                       stream=st)

@@ -353,6 +353,49 @@ def test_fused_groups_bitwise_identical(hip, r2, skew):
                 assert torch.equal(x, y), key
 
 
+@pytest.mark.parametrize("skew", [math.inf, 2.0], ids=["dense", "mixed"])
+def test_noise_drawn_in_update_bitwise(hip, skew):
+    """draws="device": the bf16 noise generated inside the grouped update (psgdk_kron2d_update_groups_drawn, no
+    noise buffer) against the same normals filled into a buffer by psgdk_fill_normal and read back: bitwise equal
+    Q, L, P and parameters after 3 steps with momentum. The set mixes bf16 and fp32 gradients (the fp32 noise stays
+    in its buffer), dense-diagonal groups at skew 2 (the transposed noise kernel) and a gradient 8 bytes past a
+    16-byte boundary (the noise kernel's per-element path)."""
+    shapes = [(128, 384), (128, 384), (256, 128), (64, 40), (32, 512), (512, 48), (96,)]
+    gen = torch.Generator().manual_seed(11)
+    steps = []
+    for _ in range(3):
+        gs = []
+        for i, s in enumerate(shapes):
+            dt = torch.bfloat16 if len(s) == 2 and s != (64, 40) else torch.float32
+            g = (0.01 * torch.randn(s, generator=gen)).to(dt).to(DEV)
+            if i == 2:
+                buf = torch.zeros(g.numel() + 8, dtype=dt, device=DEV)
+                v = buf[4:4 + g.numel()].view(s)
+                v.copy_(g)
+                assert v.data_ptr() % 16 == 8
+                g = v
+            gs.append(g)
+        steps.append(gs)
+    res = []
+    for inside in (True, False):
+        W = [torch.zeros(s, device=DEV, requires_grad=True) for s in shapes]
+        opt = KronWhiten(W, precision="bf16", draws="device", seed=5, preconditioner_max_skew=skew,
+                         preconditioner_init_scale=1.0, momentum=0.9)
+        opt._draw_in_update = inside
+        for gs in steps:
+            opt.step_math(gs)
+        torch.cuda.synchronize()
+        assert (opt._draw_buf16 is None) == inside
+        res.append(([w.detach().clone() for w in W], opt.state_dict()))
+    (Wa, sa), (Wb, sb) = res
+    for a, b in zip(Wa, Wb):
+        assert torch.equal(a, b)
+    for pa, pb in zip(sa["params"], sb["params"]):
+        for key in ("Q", "L", "P"):
+            for x, y in zip(pa[key], pb[key]):
+                assert torch.equal(x, y), key
+
+
 GRAPHS_OFF = ("graphs=True is switched off: a capture of the step (side streams forked inside torch.cuda.graph) "
               "aborted the process (SIGABRT) on the GPU, after an earlier segfault at capture end, and the cause is "
               "not established; KronWhiten(graphs=True) raises NotImplementedError")

@@ -248,6 +248,34 @@ def test_update_groups_validation():
     assert call([group(), group(shadows=False)], [o, o]) == L.EINVAL and "bf16" in _err()
     assert call([group(prec=L.PREC_F32)], [o]) == L.EINVAL
 
+    # the drawn-noise form: the same size query without noise; with a workspace, a group needs noise pointers or
+    # draws, and draw offsets must be multiples of 4 (refused before any device work)
+    ga = (C.POINTER(L.Kron2d) * 2)(*[C.pointer(group()), C.pointer(group())])
+    oa = (C.POINTER(L.UpdateOpts) * 2)(C.pointer(o), C.pointer(o))
+    sz2 = C.c_size_t(0)
+    assert lib.psgdk_kron2d_update_groups_drawn(2, ga, oa, None, None, None, None, C.byref(sz2), None, None) == L.OK
+    assert sz2.value == sz.value
+    V = (C.POINTER(C.c_void_p) * 2)(L.ptrs([0x1000]), L.ptrs([0x1000]))
+    ws = C.c_void_p(0x100000)
+
+    def drawn(offsets):
+        ds = []
+        for off in offsets:
+            if off is None:
+                ds.append(None)
+                continue
+            d = L.Draws(7, 1)
+            d.offset[0] = off
+            ds.append(C.pointer(d))
+        da = (C.POINTER(L.Draws) * 2)(*ds)
+        n = (C.POINTER(C.c_void_p) * 2)(None, None)
+        return lib.psgdk_kron2d_update_groups_drawn(2, ga, oa, n, da, V, ws, C.byref(sz2), None, None)
+
+    assert drawn([0, None]) == L.EINVAL and "neither" in _err()
+    assert drawn([0, 6]) == L.EINVAL and "multiple of 4" in _err()
+    assert drawn([-4, 8]) == L.EINVAL
+    assert lib.psgdk_kron2d_update_groups_drawn(2, ga, oa, None, None, V, ws, C.byref(sz2), None, None) == L.EINVAL
+
 
 def test_python_surface_on_cpu():
     """The optimizer and the ops refuse CPU tensors with a clear error (no silent CPU path)."""
