@@ -1154,7 +1154,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
   load(1, x1);
   load(2, x2);
   load(3, x3);
-  if (tid < NLB_K) rsl[tid] = vmm_row_scale(p, b, tid, T, normalize);  // read after the first round's barrier
   for (int r0 = 0; r0 < T; r0 += 4) {
     do_round(r0, x0);
     load(r0 + 4, x0);
@@ -1167,6 +1166,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
     load(r0 + 6, x2);
     load(r0 + 7, x3);
   }
+  // The row scales, read after the epilogue's first barrier. Computed here, where the rounds' operand registers are
+  // free, the helper's loads go out together; before the rounds (x0..x3 in flight) the compiler issued them one at a
+  // time, each waited for, and the first round's barrier waited out that chain of T dependent loads.
+  if (tid < NLB_K) rsl[tid] = vmm_row_scale(p, b, tid, T, normalize);
   // Epilogue: lane (c, h) holds rows 8 (i / 4) + 4 h + i % 4 of column 32 j + c; rows 0-15 are i < 8
   float (*red)[16][VMC] = reinterpret_cast<float (*)[16][VMC]>(sm);
   const int lr = tid >> 4, cl = (tid & 15) * 4, col = J * VMC + cl;
