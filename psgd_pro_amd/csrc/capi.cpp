@@ -300,6 +300,10 @@ int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   if (g_force_cfg >= 0) return g_force_cfg;
   const int64_t t0 = gemm_bf16_tiles(M, N, tri, 0) * nb;
   if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return 1;
+  // a SYRK of at most three 256-tile rows: half or more of its 256-tiles straddle the diagonal and compute a whole
+  // block for half of one; its 128-tiles waste a third as much (ViT-B: the d = 768 SYRKs 1.53 -> 1.50 ms of SYRK
+  // time per step)
+  if (tri && M <= 768) return 1;
   return g_ws && epi != EPI_FACTOR && epi != EPI_PROCB ? 3 : 0;
 }
 
@@ -324,11 +328,22 @@ bool b16_operands_ok(int nb, int64_t M, int64_t N, int64_t K, P const* A, int64_
 
 // The k-contiguous kernel on bf16 (esz 2) or fp32 (esz 4) operands.
 // kbeg: A is upper-triangular with its zeros stored; each tile starts its k loop at its first row (TRMM).
+// kper (optional, bf16 k-contiguous operands): problem b has its own K = kper[b] with lda = ldb = kper[b]; K is then
+// the largest of them (the size rule's K).
 int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64_t lda, const void* const* B,
             int64_t ldb, const B16Out& o, const EpiSpec& e, int tri, int out_mode, int* ntiles, hipStream_t st,
-            int esz = 2, bool amc = false, bool bmc = false, int kbeg = 0) {
-  if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb, esz, amc, tri ? amc : bmc))
+            int esz = 2, bool amc = false, bool bmc = false, int kbeg = 0, const int* kper = nullptr) {
+  if (kper) {
+    if (esz != 2 || amc || bmc || kbeg) return fail(PSGDK_EINVAL, "per-problem K: bf16 k-contiguous operands only");
+    for (int b = 0; b < nb; ++b) {
+      const void* Ab[1] = {A[b]};
+      const void* Bb[1] = {tri ? A[b] : B[b]};
+      if (kper[b] < 1 || kper[b] > K || !b16_operands_ok(1, M, tri ? M : N, kper[b], Ab, kper[b], Bb, kper[b]))
+        return fail(PSGDK_EINVAL, "k-contiguous kernel operand contract violated (problem %d, K = %d)", b, kper[b]);
+    }
+  } else if (!b16_operands_ok(nb, M, tri ? M : N, K, A, lda, tri ? A : B, ldb, esz, amc, tri ? amc : bmc)) {
     return fail(PSGDK_EINVAL, "k-contiguous kernel operand contract violated (K, leading dimensions, alignment or size)");
+  }
   GB16Args a;
   std::memset(&a, 0, sizeof a);
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
@@ -337,7 +352,9 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   a.vec = g_tile_order;
   a.amc = amc; a.bmc = tri ? amc : bmc;
   a.kbeg = kbeg;
+  a.kper = kper ? 1 : 0;
   for (int b = 0; b < nb; ++b) {
+    a.kp[b] = kper ? kper[b] : (int)K;
     a.A[b] = reinterpret_cast<const bf16_t*>(A[b]);
     a.B[b] = reinterpret_cast<const bf16_t*>(B[b]);
     a.C[b] = o.C[b]; a.Cb[b] = o.Cb[b]; a.CTb[b] = o.CTb[b]; a.CT[b] = o.CT[b];
@@ -351,7 +368,8 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   // products about 400 (the fp32 twin's main loop is the slower one there).
   const int64_t t128 = (int64_t)gemm_bf16_tiles(M, N, tri, 1) * nb;
   const int64_t small_max = esz == 4 ? 3 * (int64_t)g_small : tri ? 3 * (int64_t)g_small / 2 : g_small;
-  const bool small = e.epi == EPI_STORE && !kbeg && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 && t128 < small_max;
+  const bool small = e.epi == EPI_STORE && !kbeg && !kper && !amc && !(tri ? amc : bmc) && g_force_cfg < 0 &&
+                     t128 < small_max;
   // ... and one whose 64-tiles would still fill only a fraction of the CUs: the tiny-product kernel
   const bool tiny = small && (int64_t)gemm_small_tiles(M, N, tri) * nb < g_tiny;
   if (ntiles)
@@ -366,11 +384,17 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   r.kernel_id = small ? 7000 + (tiny ? 2 : 0) + (esz == 4 ? 1 : 0) : (esz == 4 ? 6000 : 5000) + cfg * 10 + a.epi;
   r.tri = tri;
   r.nb = nb;
-  r.flops = tri ? (double)M * (M + 1) * K * nb : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * K * nb;
+  double ksum = (double)K * nb;  // the problems' k extents summed
+  if (kper) {
+    ksum = 0;
+    for (int b = 0; b < nb; ++b) ksum += kper[b];
+  }
+  const double kavg = ksum / nb;
+  r.flops = tri ? (double)M * (M + 1) * ksum : kbeg ? (double)M * (M + 1) * N * nb : 2.0 * M * N * ksum;
   {  // operands once (kbeg: A's upper triangle), each output written once, each epilogue operand read once
     const double out = tri ? (out_mode == PSGDK_OUT_MIRROR ? (double)M * M : (double)M * (M + 1) / 2) : (double)M * N;
-    const double a_el = kbeg ? (double)M * (M + 1) / 2 : (double)M * K;
-    double by = a_el * esz + (tri ? 0.0 : (double)N * K * esz);
+    const double a_el = kbeg ? (double)M * (M + 1) / 2 : (double)M * kavg;
+    double by = a_el * esz + (tri ? 0.0 : (double)N * kavg * esz);
     if (o.C[0]) by += 4 * out;
     if (o.Cb[0]) by += 2 * out;
     if (o.CTb[0]) by += 2 * out;
@@ -871,8 +895,37 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
   // The SPD bound of term1 = pcol pcol^T. Items whose other side is under half of d (the Pg route: term1 Q goes
   // through pcol) bound term1 from pcol without forming it (run_nlb_gram, one launch sequence per other side, H in
   // the T1b buffer and pcol H in the Rb buffer, both free until later phases); the others form term1 by SYRK (one
-  // launch per other side) and share one full-storage bound.
+  // launch for all of them) and share one full-storage bound.
   std::vector<int> full;
+  {  // term1 = pcol pcol^T, full symmetric bf16 (its only consumers read bf16), for every item that forms it: one
+     // launch whatever the other sides (K = other per problem). The problems go longest K first, dealt in snake
+     // order over 8 runs, one per XCD (the kernel gives each XCD a contiguous run of tiles), so that every XCD
+     // gets a like share of long and short problems.
+    std::vector<int> sy;
+    for (int i = 0; i < nb; ++i)
+      if (!(g_t1q_pg && 2 * it[i]->other < d)) { sy.push_back(i); full.push_back(i); }
+    if (!sy.empty()) {
+      std::stable_sort(sy.begin(), sy.end(), [&](int x, int y) { return it[x]->other > it[y]->other; });
+      std::vector<int> run[8];
+      for (size_t j = 0; j < sy.size(); ++j) {
+        const size_t r = j % 16;
+        run[r < 8 ? r : 15 - r].push_back(sy[j]);
+      }
+      int k = 0, kp[MAXB];
+      int64_t kmax = 0;
+      B16Out out;
+      out.ldcb = d;
+      for (auto& rn : run)
+        for (int i : rn) {
+          A[k] = it[i]->pcol; out.Cb[k] = it[i]->T1b; kp[k] = (int)it[i]->other;
+          kmax = std::max<int64_t>(kmax, it[i]->other);
+          ++k;
+        }
+      EpiSpec e;
+      PSGDK_TRY(run_b16(k, d, d, kmax, A, kmax, A, kmax, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st, 2, false, false,
+                        0, kp));
+    }
+  }
   for (int i0 = 0; i0 < nb;) {
     int k = 0;
     int idx[MAXB];
@@ -893,13 +946,7 @@ int b16_items(const std::vector<B16Item*>& it, const psgdk_update_opts_t* o, con
         Pc[j] = x->pcol; Pr[j] = x->prow; Hb[j] = x->T1b; Wb[j] = x->Rb; Vs[j] = x->Vs;
       }
       PSGDK_TRY(run_nlb_gram(d, other, k, Pc, Pr, Hb, Wb, Vs, fin, nw, st));
-      continue;
     }
-    B16Out out;  // term1 = pcol pcol^T, full symmetric bf16 (its only consumers read bf16)
-    out.ldcb = d;
-    for (int j = 0; j < k; ++j) { A[j] = it[idx[j]]->pcol; out.Cb[j] = it[idx[j]]->T1b; full.push_back(idx[j]); }
-    EpiSpec e;
-    PSGDK_TRY(run_b16(k, d, d, other, A, other, A, other, out, e, 1, PSGDK_OUT_MIRROR, nullptr, st));
   }
   if (!full.empty()) {
     NlbFinal fin;

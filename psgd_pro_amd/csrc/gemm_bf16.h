@@ -20,6 +20,8 @@ struct GB16Args {
   int amc, bmc;       // fp32 kernel: A / B stored m- / n-contiguous (rows of the buffer are k; M / N a multiple of 4)
   int kbeg;           // 1: A is upper-triangular (A[i][k] = 0 for k < i, zeros stored): a tile of rows m0.. starts its
                       // k loop at the k tile holding m0 (TRMM)
+  int kper;           // 1: problem b has its own K = kp[b], with lda = ldb = kp[b] (k-contiguous rows of exactly K)
+  int kp[MAXB];
   const bf16_t* A[MAXB];
   const bf16_t* B[MAXB];
   float* C[MAXB];
@@ -32,7 +34,8 @@ struct GB16Args {
   float* part[MAXB];
 };
 
-// cfg 0: 256 x 256 tiles (8 waves), cfg 1: 128 x 128 tiles (4 waves), cfg 2: 256 x 256 tiles (4 waves)
+// cfg 0: 256 x 256 tiles (8 waves), cfg 1: 128 x 128 tiles (4 waves), cfg 2: 256 x 256 tiles (4 waves), cfg 3:
+// 256 x 256 tiles (8 MFMA waves on 32 x 32 x 16 and 4 load-only waves)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
 // The same kernel for k-contiguous fp32 operands (A, B reinterpreted as float; K, leading dimensions multiples of 4;
 // always the 128-tile configuration, with k summed in blocks of 128; operands k-contiguous or, with amc / bmc,

@@ -146,6 +146,9 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   const int G = p.ntiles * p.nb;
   const int logical = p.vec ? remap_xcd(blockIdx.x, G) : (int)blockIdx.x;
   const int b = logical / p.ntiles, tile = logical % p.ntiles;
+  // this problem's k extent and leading dimensions (kper: its own K, rows of exactly K)
+  const int K = p.kper ? p.kp[b] : p.K;
+  const long long lda = p.kper ? (long long)K : p.lda, ldb = p.kper ? (long long)K : p.ldb;
   int ti, tj;
   if (p.tri) {
     ti = 0;
@@ -200,14 +203,14 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   // k tiles of this output tile: all of K, or (kbeg: A upper-triangular, zero left of the tile's first row) from the
   // k tile holding m0; kb is the k origin of the first one
   const int kfirst = p.kbeg ? m0 / BK : 0, kb = kfirst * BK;
-  const int nk = (p.K + BK - 1) / BK - kfirst;
+  const int nk = (K + BK - 1) / BK - kfirst;
   // fp32 operands may be stored m- / n-contiguous (amc, bmc: the buffer's rows are k)
   constexpr bool amc = (LAY & 1) != 0, bmc = (LAY & 2) != 0;  // a SYRK (B = A) has both bits or neither
   static_assert(LAY == 0 || std::is_same_v<T, float>, "m/n-contiguous operands: fp32 only");
   const __amdgpu_buffer_rsrc_t rsA =
-      make_rsrc(Ap, (long long)(amc ? p.K : p.M) * p.lda * (long long)sizeof(T));
+      make_rsrc(Ap, (long long)(amc ? K : p.M) * lda * (long long)sizeof(T));
   const __amdgpu_buffer_rsrc_t rsB =
-      make_rsrc(Bp, (long long)(bmc ? p.K : (p.tri ? p.M : p.N)) * p.ldb * (long long)sizeof(T));
+      make_rsrc(Bp, (long long)(bmc ? K : (p.tri ? p.M : p.N)) * ldb * (long long)sizeof(T));
   // acc += a b over one pair of 16-byte fragments (32 k of bf16, or 16 k of fp32 in four steps)
   auto mma = [](f32x4_t& c, const F& a, const F& bb) {
     if constexpr (MPF == 1) {
@@ -290,18 +293,18 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     if (producer) {
       constexpr int NTP = 64 * PW;
       const int t = tid - NT;
-      const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * CE) * (long long)sizeof(T));
-      const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * CE) * (long long)sizeof(T));
+      const int voffA = (int)(((long long)(t >> 3) * lda + (t & 7) * CE) * (long long)sizeof(T));
+      const int voffB = (int)(((long long)(t >> 3) * ldb + (t & 7) * CE) * (long long)sizeof(T));
       Ld<T, BM, NTP, true> la0, la1;
       Ld<T, BN, NTP, true> lb0, lb1;
-      la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb, p.K, t);
-      lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb, p.K, t);
-      la1.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + BK, p.K, t);
-      lb1.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + BK, p.K, t);
+      la0.load_pinned(rsA, voffA, lda, m0, p.M, kb, K, t);
+      lb0.load_pinned(rsB, voffB, ldb, n0, rowsB, kb, K, t);
+      la1.load_pinned(rsA, voffA, lda, m0, p.M, kb + BK, K, t);
+      lb1.load_pinned(rsB, voffB, ldb, n0, rowsB, kb + BK, K, t);
       la0.store(As0, t);
       lb0.store(Bs0, t);
-      la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + 2 * BK, p.K, t);
-      lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + 2 * BK, p.K, t);
+      la0.load_pinned(rsA, voffA, lda, m0, p.M, kb + 2 * BK, K, t);
+      lb0.load_pinned(rsB, voffB, ldb, n0, rowsB, kb + 2 * BK, K, t);
       __syncthreads();
       // Two phases per trip, so that the register set of each is static: the first stores set 1 (tile kt + 1),
       // the second set 0. Both are unconditional inside the loop and an odd last phase is peeled after it: with a
@@ -311,13 +314,13 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       for (; kt + 1 < nk; kt += 2) {
         la1.store(As0 + BM * KP, t);
         lb1.store(Bs0 + BN * KP, t);
-        la1.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + (kt + 3) * BK, p.K, t);
-        lb1.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 3) * BK, p.K, t);
+        la1.load_pinned(rsA, voffA, lda, m0, p.M, kb + (kt + 3) * BK, K, t);
+        lb1.load_pinned(rsB, voffB, ldb, n0, rowsB, kb + (kt + 3) * BK, K, t);
         __syncthreads();
         la0.store(As0, t);
         lb0.store(Bs0, t);
-        la0.load_pinned(rsA, voffA, p.lda, m0, p.M, kb + (kt + 4) * BK, p.K, t);
-        lb0.load_pinned(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 4) * BK, p.K, t);
+        la0.load_pinned(rsA, voffA, lda, m0, p.M, kb + (kt + 4) * BK, K, t);
+        lb0.load_pinned(rsB, voffB, ldb, n0, rowsB, kb + (kt + 4) * BK, K, t);
         __syncthreads();
       }
       if (kt < nk) {
@@ -350,15 +353,15 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
       }
     }
   } else if constexpr (!PP) {
-    const int voffA = (int)(((long long)(tid >> 3) * p.lda + (tid & 7) * CE) * (long long)sizeof(T));
-    const int voffB = (int)(((long long)(tid >> 3) * p.ldb + (tid & 7) * CE) * (long long)sizeof(T));
+    const int voffA = (int)(((long long)(tid >> 3) * lda + (tid & 7) * CE) * (long long)sizeof(T));
+    const int voffB = (int)(((long long)(tid >> 3) * ldb + (tid & 7) * CE) * (long long)sizeof(T));
     Ld<T, BM, NT> la;
     Ld<T, BN, NT> lb;
     auto load = [&](int k0) {
-      if constexpr (amc) la.load_mc(rsA, p.lda, m0, p.M, k0, p.K, tid);
-      else la.load(rsA, voffA, p.lda, m0, p.M, k0, p.K, tid);
-      if constexpr (bmc) lb.load_mc(rsB, p.ldb, n0, rowsB, k0, p.K, tid);
-      else lb.load(rsB, voffB, p.ldb, n0, rowsB, k0, p.K, tid);
+      if constexpr (amc) la.load_mc(rsA, lda, m0, p.M, k0, K, tid);
+      else la.load(rsA, voffA, lda, m0, p.M, k0, K, tid);
+      if constexpr (bmc) lb.load_mc(rsB, ldb, n0, rowsB, k0, K, tid);
+      else lb.load(rsB, voffB, ldb, n0, rowsB, k0, K, tid);
     };
     auto store = [&](T* as, T* bs) {
       if constexpr (amc) la.store_mc(as, tid);
@@ -401,23 +404,23 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
     // h is uniform per wave but not provably so, and a scalar offset derived from it would be waterfalled.
     const int h = wave >> 2, t = (tid & 255) + h * (NT / 2) * 4;  // rows h * 128 + (tid & 255) / 8 (+ 32 i)
     static_assert(BM == BN && (NT / 2) * 4 == (BM / 2) * 8, "ping-pong loader: one group loads half the rows");
-    const int voffA = (int)(((long long)(t >> 3) * p.lda + (t & 7) * CE) * (long long)sizeof(T));
-    const int voffB = (int)(((long long)(t >> 3) * p.ldb + (t & 7) * CE) * (long long)sizeof(T));
+    const int voffA = (int)(((long long)(t >> 3) * lda + (t & 7) * CE) * (long long)sizeof(T));
+    const int voffB = (int)(((long long)(t >> 3) * ldb + (t & 7) * CE) * (long long)sizeof(T));
     Ld<T, BM / 2, NT / 2> la;
     Ld<T, BN / 2, NT / 2> lb;
-    la.load(rsA, voffA, p.lda, m0, p.M, kb, p.K, t);
-    lb.load(rsB, voffB, p.ldb, n0, rowsB, kb, p.K, t);
+    la.load(rsA, voffA, lda, m0, p.M, kb, K, t);
+    lb.load(rsB, voffB, ldb, n0, rowsB, kb, K, t);
     la.store(As0, t);
     lb.store(Bs0, t);
-    la.load(rsA, voffA, p.lda, m0, p.M, kb + BK, p.K, t);
-    lb.load(rsB, voffB, p.ldb, n0, rowsB, kb + BK, p.K, t);
+    la.load(rsA, voffA, lda, m0, p.M, kb + BK, K, t);
+    lb.load(rsB, voffB, ldb, n0, rowsB, kb + BK, K, t);
     __syncthreads();
     auto memory = [&](int kt) {
       const int nxt = (kt + 1) & 1;
       la.store(As0 + nxt * BM * KP, t);
       lb.store(Bs0 + nxt * BN * KP, t);
-      la.load(rsA, voffA, p.lda, m0, p.M, kb + (kt + 2) * BK, p.K, t);
-      lb.load(rsB, voffB, p.ldb, n0, rowsB, kb + (kt + 2) * BK, p.K, t);
+      la.load(rsA, voffA, lda, m0, p.M, kb + (kt + 2) * BK, K, t);
+      lb.load(rsB, voffB, ldb, n0, rowsB, kb + (kt + 2) * BK, K, t);
     };
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;

@@ -562,15 +562,16 @@ def test_syrk_bf16_microbench_shape(hip):
 @pytest.mark.parametrize("kind,nb,m,n,k", [("gemm", 2, 768, 768, 2304), ("gemm", 1, 300, 520, 264),
                                             ("syrk", 3, 1000, 1000, 512), ("syrk", 1, 2304, 2304, 3072)])
 def test_load_only_waves_give_the_same_sums(hip, kind, nb, m, n, k):
-    """The 256-tile configuration with load-only waves and 32 x 32 x 16 MFMAs (option 1 = 3) returns bit for bit
-    what the ping-pong configuration on 16 x 16 x 32 MFMAs (option 1 = 0) returns, edge tiles included; the size rule
-    relies on this when it swaps one for the other."""
+    """The 256-tile configuration with load-only waves and 32 x 32 x 16 MFMAs (option 1 = 3) and the 128-tile
+    configuration (option 1 = 1) return bit for bit what the ping-pong configuration on 16 x 16 x 32 MFMAs (option 1 =
+    0) returns, edge tiles included: every configuration sums k in the same order, so the size rule's choice (which
+    looks at the whole launch) does not change a problem's result."""
     A = [rnd(m, k, seed=10 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     B = [rnd(n, k, seed=20 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
-    out = {c: [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)] for c in (0, 3)}
+    out = {c: [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)] for c in (0, 1, 3)}
     st = L.stream_of(A[0])
     try:
-        for c in (0, 3):
+        for c in (0, 1, 3):
             L.check(hip.psgdk_set_option(1, c))
             if kind == "gemm":
                 L.check(hip.psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(A), k, L.ptrs(B), k, 0.0,
@@ -581,6 +582,7 @@ def test_load_only_waves_give_the_same_sums(hip, kind, nb, m, n, k):
         L.check(hip.psgdk_set_option(1, -1))
     for b in range(nb):
         assert torch.equal(out[0][b], out[3][b]), (kind, b)
+        assert torch.equal(out[0][b], out[1][b]), (kind, b, "128-tile configuration")
     X = A[0].double().cpu()
     Y = X if kind == "syrk" else B[0].double().cpu()
     check_gemm_bound(out[3][0].cpu(), X, Y.T)
