@@ -205,17 +205,37 @@ __global__ void __launch_bounds__(256) noise_t_kernel(const EwArgs a) {
   bf16_t* __restrict__ Y = reinterpret_cast<bf16_t*>(a.out2[b]);
   const int tid = threadIdx.x, c = tid & 63, r0 = tid >> 6;
   const long long gj = (long long)J * 64 + c;
-#pragma unroll 4
-  for (int r = r0; r < 64; r += 4) {
+  // this thread's 16 rows r0 + 4 q: their G (and a read noise's) values are loaded together, an element outside
+  // the matrix reading element 0 and being discarded (loads behind the bounds branch waited for each in turn)
+  const bool rd = !a.draw && N;
+  float gv[16], nv[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const long long gi = (long long)I * 64 + r0 + 4 * q;
+    const long long o = gi < m && gj < n ? gi * n + gj : 0;
+    gv[q] = ldv(G, a.dt, o);
+    nv[q] = 0.f;
+  }
+  if (rd) {  // uniform over the launch
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const long long gi = (long long)I * 64 + r0 + 4 * q;
+      nv[q] = ldv(N, a.dt, gi < m && gj < n ? gi * n + gj : 0);
+    }
+  }
+  const float cs = csc && gj < n ? csc[gj] : 1.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int r = r0 + 4 * q;
     const long long gi = (long long)I * 64 + r;
     float x = 0.f;
     if (gi < m && gj < n) {
       const long long o = gi * n + gj;
-      const float g = ldv(G, a.dt, o);
+      const float g = gv[q];
       x = a.draw ? g + (a.f0 + a.f1 * fabsf(g)) * drawn_normal(a, (unsigned long long)a.doff[b] + o, a.dt)
-          : N    ? g + (a.f0 + a.f1 * fabsf(g)) * ldv(N, a.dt, o)
+          : N    ? g + (a.f0 + a.f1 * fabsf(g)) * nv[q]
                  : g;
-      if (csc) x *= csc[gj];
+      if (csc) x *= cs;
     }
     t[r][c] = x;
   }

@@ -34,11 +34,20 @@ __global__ void __launch_bounds__(256) tri_rownorm_kernel(const NlbArgs p) {
   const int lr = tid >> 2, lc0 = (tid & 3) * 16;
   const int gi = I * RT + lr;
   float rs = 0.f, am = 0.f, dm = -INFINITY;
+  // the 16 loads go out together: each reads a valid address (element 0 in place of one outside the stored
+  // triangle) and the value is selected afterwards (a load behind a per-element branch waited for each in turn)
+  float a16[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     const int gj = J * RT + lc0 + c;
-    float v = 0.f;
-    if (gi < n && gj < n && gi <= gj) v = A[(long long)gi * ld + gj];
+    const bool ok = gi < n && gj < n && gi <= gj;
+    a16[c] = A[ok ? (long long)gi * ld + gj : 0];
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int gj = J * RT + lc0 + c;
+    const float v0 = a16[c];
+    float v = gi < n && gj < n && gi <= gj ? v0 : 0.f;
     if (gi == gj && gi < n) {
       dm = fmaxf(dm, v);
       if (p.sign < 0) v = 0.f;  // skew: the diagonal is zero by definition
