@@ -174,8 +174,9 @@ def kernel_name(kernel_id):
     if kernel_id >= 5000:  # 5000 (bf16) or 6000 (fp32 k-contiguous) + 10 cfg + epilogue
         base = 6000 if kernel_id >= 6000 else 5000
         cfg, epi = divmod(kernel_id - base, 10)
-        tile = {0: "256, 256, 2, 4", 1: "128, 128, 2, 2", 2: "256, 256, 2, 2", 3: "256, 256, 2, 4"}[cfg]
-        ws = ", 4" if cfg == 3 else ""  # the warp-specialized kernel's 4 producer waves
+        tile = {0: "256, 256, 2, 4", 1: "128, 128, 2, 2", 2: "256, 256, 2, 2", 3: "256, 256, 2, 4",
+                4: "128, 128, 2, 2"}[cfg]
+        ws = ", 4" if cfg in (3, 4) else ""  # the warp-specialized kernels' 4 producer waves
         return f"gemm_{'f32kc' if base == 6000 else 'bf16'}_kernel<{tile}, {epi}{ws}>"
     cfg, rest = divmod(kernel_id, 1000)
     prec, rest = divmod(rest, 100)

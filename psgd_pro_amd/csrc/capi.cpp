@@ -295,16 +295,18 @@ int batch_events(SideStreams* ss, size_t n) {
 // Its warp-specialized main loop (cfg 3, option 12) gives the same sums; it is taken except for the two epilogues
 // that read two more operands per element (EPI_FACTOR, EPI_PROCB): with three waves per SIMD those spill registers
 // and run at half the epilogue's load depth, and lose more than the main loop gains (measured on the ViT-B step:
-// the d = 3072 SYRKs 907 -> 840 us, the PROCB products 1676 -> 1759 us).
+// the d = 3072 SYRKs 907 -> 840 us, the PROCB products 1676 -> 1759 us). The 128-tile launches take the same loop
+// on 128 x 128 tiles (cfg 4) under the same rule (16 SYRKs of 768 x 3072: 67.9 -> 58.5 us).
 int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   if (g_force_cfg >= 0) return g_force_cfg;
+  const bool ws = g_ws && epi != EPI_FACTOR && epi != EPI_PROCB;  // the load-only-wave configurations 3 and 4
   const int64_t t0 = gemm_bf16_tiles(M, N, tri, 0) * nb;
-  if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return 1;
+  if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return ws ? 4 : 1;
   // a SYRK of at most three 256-tile rows: half or more of its 256-tiles straddle the diagonal and compute a whole
   // block for half of one; its 128-tiles waste a third as much (ViT-B: the d = 768 SYRKs 1.53 -> 1.50 ms of SYRK
   // time per step)
-  if (tri && M <= 768) return 1;
-  return g_ws && epi != EPI_FACTOR && epi != EPI_PROCB ? 3 : 0;
+  if (tri && M <= 768) return ws ? 4 : 1;
+  return ws ? 3 : 0;
 }
 
 // Operand contract of the k-contiguous kernel (gemm_bf16, esz 2; its fp32 twin, esz 4): 16-byte aligned bases,
@@ -2320,7 +2322,7 @@ int psgdk_set_option(int option, int value) {
     return PSGDK_OK;
   }
   if (option == 1) {
-    if (value < -1 || value > 3) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 3");
+    if (value < -1 || value > 4) return fail(PSGDK_EINVAL, "option 1 (bf16 tile config) must be -1 .. 4");
     g_force_cfg = value;
     return PSGDK_OK;
   }

@@ -35,7 +35,8 @@ struct GB16Args {
 };
 
 // cfg 0: 256 x 256 tiles (8 waves), cfg 1: 128 x 128 tiles (4 waves), cfg 2: 256 x 256 tiles (4 waves), cfg 3:
-// 256 x 256 tiles (8 MFMA waves on 32 x 32 x 16 and 4 load-only waves)
+// 256 x 256 tiles (8 MFMA waves on 32 x 32 x 16 and 4 load-only waves), cfg 4: 128 x 128 tiles (4 MFMA waves on
+// 32 x 32 x 16 and 4 load-only waves)
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st);
 // The same kernel for k-contiguous fp32 operands (A, B reinterpreted as float; K, leading dimensions multiples of 4;
 // always the 128-tile configuration, with k summed in blocks of 128; operands k-contiguous or, with amc / bmc,

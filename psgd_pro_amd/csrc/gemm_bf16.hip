@@ -136,8 +136,9 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr bool WS = PW > 0;                       // warp-specialized: producer and MFMA waves
   constexpr bool PP = !WS && WGM == 2 && WGN == 4;  // ping-pong main loop (8 waves, two groups of 4)
-  static_assert(!WS || (std::is_same_v<T, bf16_t> && BM == 256 && BN == 256 && WGM == 2 && WGN == 4 && PW == 4),
-                "warp-specialized main loop: bf16, 256 x 256 tiles, 8 MFMA waves, 4 producer waves");
+  static_assert(!WS || (std::is_same_v<T, bf16_t> && PW == 4 &&
+                        ((BM == 256 && BN == 256 && WGM == 2 && WGN == 4) || (BM == 128 && BN == 128 && WGM == 2 && WGN == 2))),
+                "warp-specialized main loop: bf16, 256 x 256 tiles on 8 MFMA waves or 128 x 128 on 4, 4 producer waves");
   constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 tiles per wave along m, n
   extern __shared__ __align__(16) unsigned char smem[];
   T* const As0 = reinterpret_cast<T*>(smem);
@@ -189,13 +190,15 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto& dst = BLK ? part : acc;  // the MFMA accumulators of the main loop
-  // WS: 4 x 2 tiles of 32 x 32 per wave (element m of lane l at row 8 (m / 4) + 4 (l / 32) + m % 4, column l % 32)
-  f32x16_t acc32[WS ? 4 : 1][WS ? 2 : 1];
+  // WS: FM32 x FN32 tiles of 32 x 32 per wave (element m of lane l at row 8 (m / 4) + 4 (l / 32) + m % 4, column
+  // l % 32)
+  constexpr int FM32 = WS ? TM / 32 : 1, FN32 = WS ? TN / 32 : 1;
+  f32x16_t acc32[FM32][FN32];
   if constexpr (WS) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM32; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < FN32; ++j)
 #pragma unroll
         for (int m = 0; m < 16; ++m) acc32[i][j][m] = 0.f;
   }
@@ -339,15 +342,16 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const int ko = swz32(c, 2 * ks + hh) * CE;
-          F bq[2], aq[4];
+          F bq[FN32], aq[FM32];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) bq[j] = *reinterpret_cast<const F*>(Bs + (wn * TN + 32 * j + c) * KP + ko);
+          for (int j = 0; j < FN32; ++j) bq[j] = *reinterpret_cast<const F*>(Bs + (wn * TN + 32 * j + c) * KP + ko);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) aq[i] = *reinterpret_cast<const F*>(As + (wm * TM + 32 * i + c) * KP + ko);
+          for (int i = 0; i < FM32; ++i) aq[i] = *reinterpret_cast<const F*>(As + (wm * TM + 32 * i + c) * KP + ko);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < FM32; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc32[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[i], bq[j], acc32[i][j], 0, 0, 0);
+            for (int j = 0; j < FN32; ++j)
+              acc32[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[i], bq[j], acc32[i][j], 0, 0, 0);
         }
         __syncthreads();
       }
@@ -480,17 +484,17 @@ __device__ __forceinline__ void gemm_kc_body(const GB16Args& p) {
   auto half = [&](auto h_c) {
     constexpr int h = decltype(h_c)::value;
     // (1) park accumulators: tile (i, j) of this half at local row (i - h FM/2) * 16 + 4g + e, column 16 j + r
-    // (WS: 32 x 32 tile (i, j), i = 2h, 2h + 1, element m at local row (i - 2h) * 32 + 8 (m / 4) + 4 hh + m % 4,
-    // column 32 j + c)
+    // (WS: 32 x 32 tile (i, j) of this half, i = h FM32/2 + ii, element m at local row ii * 32 + 8 (m / 4) + 4 hh +
+    // m % 4, column 32 j + c)
     if constexpr (WS) {
       const int c = lane & 31, hh = lane >> 5;
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
+      for (int ii = 0; ii < FM32 / 2; ++ii)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN32; ++j)
 #pragma unroll
           for (int m = 0; m < 16; ++m)
-            ep[ei(ii * 32 + 8 * (m >> 2) + 4 * hh + (m & 3), j * 32 + c)] = acc32[2 * h + ii][j][m];
+            ep[ei(ii * 32 + 8 * (m >> 2) + 4 * hh + (m & 3), j * 32 + c)] = acc32[h * (FM32 / 2) + ii][j][m];
     } else {
 #pragma unroll
       for (int ii = 0; ii < FM / 2; ++ii)
@@ -845,7 +849,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 2) gemm_f32kc_kernel(const GB1
 }
 
 int gemm_bf16_tiles(long long M, long long N, int tri, int cfg) {
-  const int T = cfg == 1 ? 128 : 256;
+  const int T = cfg == 1 || cfg == 4 ? 128 : 256;
   const long long tm = (M + T - 1) / T, tn = (N + T - 1) / T;
   return (int)(tri ? tm * (tm + 1) / 2 : tm * tn);
 }
@@ -891,9 +895,11 @@ static hipError_t launch_epi(GB16Args& a, hipStream_t st) {
 
 // cfg 0: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64; cfg 1: 128 x 128 tiles, 4 waves of 64 x 64;
 // cfg 2: 256 x 256 tiles, 4 waves of 128 x 128 (one wave per SIMD); cfg 3: 256 x 256 tiles, 8 MFMA waves of
-// 128 x 64 on 32 x 32 x 16 MFMAs plus 4 producer waves (warp-specialized main loop)
+// 128 x 64 on 32 x 32 x 16 MFMAs plus 4 producer waves (warp-specialized main loop); cfg 4: the same on 128 x 128
+// tiles, 4 MFMA waves of 64 x 64
 hipError_t gemm_bf16_launch(GB16Args& a, int cfg, hipStream_t st) {
   if (cfg == 1) return launch_epi<bf16_t, 128, 128, 2, 2>(a, st);
+  if (cfg == 4) return launch_epi<bf16_t, 128, 128, 2, 2, 0, 4>(a, st);
   if (cfg == 2) return launch_epi<bf16_t, 256, 256, 2, 2>(a, st);
   if (cfg == 3) return launch_epi<bf16_t, 256, 256, 2, 4, 0, 4>(a, st);
   return launch_epi<bf16_t, 256, 256, 2, 4>(a, st);

@@ -21,11 +21,13 @@ def hip():
     return _lib.lib()
 
 
-@pytest.fixture(params=[-1, 0, 1, 2, 3], ids=["cfg_auto", "cfg256x8", "cfg128x4", "cfg256x4", "cfg256ws"])
+@pytest.fixture(params=[-1, 0, 1, 2, 3, 4], ids=["cfg_auto", "cfg256x8", "cfg128x4", "cfg256x4", "cfg256ws",
+                                                   "cfg128ws"])
 def b16cfg(request, hip):
     """Forces the bf16 kernel's tile configuration (-1: chosen by size; 0: 256 x 256 tiles on 8 waves, the
     ping-pong main loop; 1: 128 x 128 on 4 waves; 2: 256 x 256 on 4 waves; 3: 256 x 256 on 8 MFMA waves and 4
-    producer waves, the warp-specialized main loop) for one test, then restores it."""
+    producer waves, the warp-specialized main loop; 4: 128 x 128 on 4 MFMA waves and 4 producer waves) for one
+    test, then restores it."""
     assert hip.psgdk_set_option(1, request.param) == 0
     yield request.param
     hip.psgdk_set_option(1, -1)

@@ -568,10 +568,10 @@ def test_load_only_waves_give_the_same_sums(hip, kind, nb, m, n, k):
     looks at the whole launch) does not change a problem's result."""
     A = [rnd(m, k, seed=10 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
     B = [rnd(n, k, seed=20 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
-    out = {c: [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)] for c in (0, 1, 3)}
+    out = {c: [torch.full((m, n), float("nan"), device=DEV) for _ in range(nb)] for c in (0, 1, 3, 4)}
     st = L.stream_of(A[0])
     try:
-        for c in (0, 1, 3):
+        for c in (0, 1, 3, 4):
             L.check(hip.psgdk_set_option(1, c))
             if kind == "gemm":
                 L.check(hip.psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(A), k, L.ptrs(B), k, 0.0,
@@ -583,6 +583,7 @@ def test_load_only_waves_give_the_same_sums(hip, kind, nb, m, n, k):
     for b in range(nb):
         assert torch.equal(out[0][b], out[3][b]), (kind, b)
         assert torch.equal(out[0][b], out[1][b]), (kind, b, "128-tile configuration")
+        assert torch.equal(out[0][b], out[4][b]), (kind, b, "128-tile configuration with load-only waves")
     X = A[0].double().cpu()
     Y = X if kind == "syrk" else B[0].double().cpu()
     check_gemm_bound(out[3][0].cpu(), X, Y.T)

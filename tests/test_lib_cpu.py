@@ -77,7 +77,7 @@ def test_option_ranges():
     """psgdk_set_option accepts each option's documented values and refuses the rest (host state only)."""
     lib = L.lib()
     try:
-        for opt, good, bad in [(0, [0, 1, 2], [3, -1]), (1, [-1, 0, 1, 2, 3], [4, -2]), (2, [1, 4096], [0, -5]),
+        for opt, good, bad in [(0, [0, 1, 2], [3, -1]), (1, [-1, 0, 1, 2, 3, 4], [5, -2]), (2, [1, 4096], [0, -5]),
                                (3, [2, 4, 8], [1, 16]), (4, [-1, 0, 1, 2, 3], [4, -2]), (5, [0, 1], [2]),
                                (6, [0, 3, 8], [9, -1]), (7, [0, 1], [2]), (8, [0, 1], [2]), (9, [1, 12, 64], [0, 65]),
                                (10, [0, 64, 1000], [-1]), (11, [0, 16, 1000], [-1]), (12, [0, 1], [2, -1])]:
