@@ -302,10 +302,10 @@ int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   const bool ws = g_ws && epi != EPI_FACTOR && epi != EPI_PROCB;  // the load-only-wave configurations 3 and 4
   const int64_t t0 = gemm_bf16_tiles(M, N, tri, 0) * nb;
   if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return ws ? 4 : 1;
-  // a SYRK of at most three 256-tile rows: half or more of its 256-tiles straddle the diagonal and compute a whole
-  // block for half of one; its 128-tiles waste a third as much (ViT-B: the d = 768 SYRKs 1.53 -> 1.50 ms of SYRK
-  // time per step)
-  if (tri && M <= 768) return ws ? 4 : 1;
+  // a SYRK of at most nine 256-tile rows: a fifth or more of its 256-tiles straddle the diagonal and compute a whole
+  // block for half of one; its 128-tiles waste half as much, which outweighs their slower main loop (12 SYRKs of
+  // 2304 x 2304: 227.5 -> 210.1 us on cfg 4; 16 of 3072, twelve rows: 530 -> 611 us, so not there)
+  if (tri && M <= 2304) return ws ? 4 : 1;
   return ws ? 3 : 0;
 }
 
