@@ -324,7 +324,8 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * calls that other threads make, such as a framework's worker threads): option 0 = tile order of the bf16 kernel (0 problem-major, 1 contiguous runs per
  * XCD, 2 = 1 with tile rows grouped by 4 so that the tiles an XCD runs at once share operand panels; default 2);
  * option 1 = its tile configuration (-1 chosen by size, 0 = 256 x 256 on 8 waves, 1 = 128 x 128, 2 = 256 x 256 on 4
- * waves, 3 = 256 x 256 on 8 MFMA waves fed by 4 load-only waves; other values are refused); option 2 = workgroups
+ * waves, 3 = 256 x 256 on 8 MFMA waves fed by 4 load-only waves, 4 = 128 x 128 on 4 MFMA waves fed by 4 load-only
+ * waves; other values are refused); option 2 = workgroups
  * per split-K V A product of the norm lower bound (default 1024); option 3 = MFMA steps per load batch of the V A
  * kernels (2, 4 or 8; default 4; the column-block kernel takes 2 or 4); option 4 = the V A kernel of full-storage
  * norm bounds (-1 by shape: 3 for bf16 launches of at least 16 matrices and 512 workgroups, else 2; 0 split-K products plus a reduce kernel, 1 one workgroup
@@ -344,9 +345,10 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * 0: never; not with a forced tile configuration, option 1); option 11 = of those, a launch with fewer 64 x 64 tiles
  * than this takes the tiny-product kernel (32 x 32 tiles whose four waves split k; results rounded in another
  * order than the other kernels' k-order sums; default 64, 0: never); option 12 = whether launches given 256 x 256
- * tiles by size take the configuration with load-only waves (option 1 value 3) rather than 0, except the Q-update
- * epilogues that read two more operands (1, default; 0: never). On gfx950 configurations 0 and 3 round the same
- * sums (their k steps of 32 and 16 accumulate in one order: bitwise-equal products). */
+ * or 128 x 128 tiles by size take the configurations with load-only waves (option 1 values 3 and 4) rather than 0
+ * and 1, except the Q-update epilogues that read two more operands (1, default; 0: never). On gfx950
+ * configurations 0, 1, 3 and 4 round the same sums (their k steps of 32 and 16 accumulate in one order:
+ * bitwise-equal products). */
 int psgdk_set_option(int option, int value);
 /* The calling thread's value of a psgdk_set_option switch. */
 int psgdk_get_option(int option, int* value);
