@@ -346,7 +346,7 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * than this takes the tiny-product kernel (32 x 32 tiles whose four waves split k; results rounded in another
  * order than the other kernels' k-order sums; default 64, 0: never); option 12 = whether launches given 256 x 256
  * or 128 x 128 tiles by size take the configurations with load-only waves (option 1 values 3 and 4) rather than 0
- * and 1, except the Q-update epilogues that read two more operands (1, default; 0: never). On gfx950
+ * and 1, except the Q-update epilogues that read two more operands and the r2 trace SYRK (1, default; 0: never). On gfx950
  * configurations 0, 1, 3 and 4 round the same sums (their k steps of 32 and 16 accumulate in one order:
  * bitwise-equal products). */
 int psgdk_set_option(int option, int value);

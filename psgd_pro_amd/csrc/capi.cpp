@@ -299,7 +299,8 @@ int batch_events(SideStreams* ss, size_t n) {
 // on 128 x 128 tiles (cfg 4) under the same rule (16 SYRKs of 768 x 3072: 67.9 -> 58.5 us).
 int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   if (g_force_cfg >= 0) return g_force_cfg;
-  const bool ws = g_ws && epi != EPI_FACTOR && epi != EPI_PROCB;  // the load-only-wave configurations 3 and 4
+  // the load-only-wave configurations 3 and 4, not for the epilogues that spill at their three waves per SIMD
+  const bool ws = g_ws && epi != EPI_FACTOR && epi != EPI_PROCB && epi != EPI_STRACE && epi != EPI_PROC;
   const int64_t t0 = gemm_bf16_tiles(M, N, tri, 0) * nb;
   if (!(t0 >= 160 || (t0 >= 128 && K >= 4096))) return ws ? 4 : 1;
   // a SYRK of at most nine 256-tile rows: a fifth or more of its 256-tiles straddle the diagonal and compute a whole
