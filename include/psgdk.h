@@ -303,8 +303,10 @@ int psgdk_fill_normal(void* out, int64_t n, int dtype, uint64_t seed, uint64_t s
  * bracketed by a pair of HIP events on its stream. psgdk_profile_stop ends the recording and, with out non-NULL,
  * waits for the recorded events and fills one record per launch: the kernel instantiation id
  * (general engine: cfg * 1000 + prec * 100 + a_dtype * 10 + b_dtype, cfg 0 = 128 x 128 tiles, 1 = 32 x 128;
- * bf16 engine: 5000 + cfg * 10 + epilogue, cfg 0 = 256 x 256 tiles on 8 waves, 1 = 128 x 128 on 4, 2 = 256 x 256
- * on 4; its fp32 twin: 6000 + cfg * 10 + epilogue; the small-problem kernels: 7000 / 7001 on 64 x 64 tiles, 7002 / 7003
+ * bf16 engine: 5000 + cfg * 10 + epilogue, cfg as option 1 below, epilogue 0 = store, 1 = factor update, 2 = Procrustes
+ * step, 3 = scale, 4 = R Q with its trace partials, 5 = store with sums of squares, 6 = the r2 trace SYRK's scale
+ * applied twice, 7 = Procrustes step reading (R Q)^T in bf16;
+ * its fp32 twin: 6000 + cfg * 10 + epilogue; the small-problem kernels: 7000 / 7001 on 64 x 64 tiles, 7002 / 7003
  * the tiny-product kernel, bf16 / fp32 operands), whether it was a
  * SYRK (triangular grid), the problems in the launch, its device time, its algorithmic flop count (SYRK n(n+1)k,
  * TRMM n(n+1)p, GEMM 2mnk, per problem) and its algorithmic bytes (operands read once, outputs written once). With out NULL only *n_records is set (records kept). */
@@ -346,7 +348,9 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
  * than this takes the tiny-product kernel (32 x 32 tiles whose four waves split k; results rounded in another
  * order than the other kernels' k-order sums; default 64, 0: never); option 12 = whether launches given 256 x 256
  * or 128 x 128 tiles by size take the configurations with load-only waves (option 1 values 3 and 4) rather than 0
- * and 1, except the Q-update epilogues that read two more operands and the r2 trace SYRK (1, default; 0: never). On gfx950
+ * and 1, except launches with epilogues 1, 2, 6 and 7 of the profiling ids above (the factor update, both Procrustes
+ * steps and the r2 trace SYRK), whose registers spill in configuration 3 (three waves per SIMD) and in configuration 4
+ * exceed the 128 of two workgroups per CU (1, default; 0: never). On gfx950
  * configurations 0, 1, 3 and 4 round the same sums (their k steps of 32 and 16 accumulate in one order:
  * bitwise-equal products). */
 int psgdk_set_option(int option, int value);
