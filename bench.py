@@ -208,7 +208,8 @@ def aggregate(recs, peak):
     """Per kernel instantiation: launches, total ms, algorithmic flops and bytes, roofline-model ms; plus the SYRK
     subset."""
     agg, syrk = {}, {}
-    for kid, tri, nb, ms, fl, by in recs:
+    for r in recs:
+        kid, tri, ms, fl, by = r.kernel_id, r.tri, r.ms, r.flops, r.bytes
         for d in (agg, syrk) if tri else (agg,):
             a = d.setdefault(kid, [0, 0.0, 0.0, 0.0, 0.0])
             a[0] += 1
@@ -220,26 +221,32 @@ def aggregate(recs, peak):
 
 
 def launch_classes(recs, steps, peak, top=12):
-    """The most expensive (kernel, problems, flops per launch) classes of MFMA launches, per step, each against its
-    own roof: its arithmetic intensity (algorithmic flops / algorithmic bytes) against the ridge (MFMA peak / HBM
-    peak) says whether the MFMA peak or the HBM peak bounds it, and roof_frac is the roofline model's time over the
-    measured time."""
+    """The most expensive (kernel, problems, shape) classes of MFMA launches, per step, each against its own roof:
+    its arithmetic intensity (algorithmic flops / algorithmic bytes) against the ridge (MFMA peak / HBM peak) says
+    whether the MFMA peak or the HBM peak bounds it, and roof_frac is the roofline model's time over the measured
+    time. shape is [problems, m, n, k] (k: the largest problem's); rounds is the launch's workgroups over the ones
+    the GPU holds at once (CUs x per_cu, the kernel's occupancy), so 1.27 means a full round and a 27% tail."""
+    import torch
+    from psgd_pro_amd import _lib as L
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
     agg = {}
-    for kid, tri, nb, ms, fl, by in recs:
-        a = agg.setdefault((kid, tri, nb, round(fl), round(by)), [0, 0.0])
+    for r in recs:
+        key = (r.kernel_id, r.tri, r.nb, r.m, r.n, r.k, round(r.flops), round(r.bytes), r.workgroups, r.per_cu)
+        a = agg.setdefault(key, [0, 0.0])
         a[0] += 1
-        a[1] += ms
+        a[1] += r.ms
     rows = sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]
     out = []
-    for k, v in rows:
+    for (kid, tri, nb, m, n, k, fl, by, wgs, per_cu), v in rows:
         us = v[1] * 1e3 / v[0]
-        ai = k[3] / k[4]
-        out.append({"kernel": k[0], "syrk": bool(k[1]), "nb": k[2], "gflop": round(k[3] / 1e9, 2),
-                    "gbyte": round(k[4] / 1e9, 3), "flop_per_byte": round(ai, 1),
+        ai = fl / by
+        out.append({"kernel": kid, "name": L.kernel_name(kid), "syrk": bool(tri), "shape": [nb, m, n, k],
+                    "gflop": round(fl / 1e9, 2), "gbyte": round(by / 1e9, 3), "flop_per_byte": round(ai, 1),
                     "bound": "mfma" if ai >= peak / PEAK_HBM else "hbm",
                     "launches_per_step": v[0] / steps, "us": round(us, 1),
-                    "tflops": round(k[3] / (us * 1e-6) / 1e12, 1), "tbps": round(k[4] / (us * 1e-6) / 1e12, 2),
-                    "roof_frac": round(roof_ms(k[3], k[4], peak) * 1e3 / us, 3)})
+                    "tflops": round(fl / (us * 1e-6) / 1e12, 1), "tbps": round(by / (us * 1e-6) / 1e12, 2),
+                    "roof_frac": round(roof_ms(fl, by, peak) * 1e3 / us, 3), "workgroups": wgs, "per_cu": per_cu,
+                    "rounds": round(wgs / (cus * per_cu), 2) if per_cu else None})
     return out
 
 

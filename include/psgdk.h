@@ -27,7 +27,7 @@ extern "C" {
 typedef struct ihipStream_t* psgdk_stream_t; /* hipStream_t */
 typedef struct ihipEvent_t* psgdk_event_t;   /* hipEvent_t */
 
-#define PSGDK_VERSION 3
+#define PSGDK_VERSION 4
 #define PSGDK_MAXB 16 /* problems per grouped call */
 #define PSGDK_MAX_GROUPS 64 /* groups per psgdk_kron2d_update_groups call */
 #define PSGDK_NLB_K 32 /* rows of the random start of the norm lower bounds */
@@ -317,6 +317,9 @@ typedef struct psgdk_prof_record {
   float ms;
   double flops;
   double bytes; /* algorithmic HBM bytes: each operand read once, each output written once, epilogue reads */
+  int64_t m, n, k;    /* each problem's output rows and columns (a SYRK: n = m) and k extent (the largest one) */
+  int32_t workgroups; /* workgroups launched */
+  int32_t per_cu;     /* workgroups of this kernel that one CU holds at once (HIP's occupancy query; 0 unknown) */
 } psgdk_prof_record_t;
 int psgdk_profile_start(void);
 int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records);

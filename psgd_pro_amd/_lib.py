@@ -3,6 +3,7 @@
 The library is loaded after torch, so that it binds to the HIP runtime torch already loaded (same soname) and works
 on torch's streams and allocations. There is no fallback: when the library is missing, `lib()` raises.
 """
+import collections
 import ctypes as C
 import os
 
@@ -54,7 +55,11 @@ class Draws(C.Structure):
 
 class ProfRecord(C.Structure):
     _fields_ = [("kernel_id", C.c_int32), ("tri", C.c_int32), ("nb", C.c_int32), ("ms", C.c_float),
-                ("flops", C.c_double), ("bytes", C.c_double)]
+                ("flops", C.c_double), ("bytes", C.c_double), ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
+                ("workgroups", C.c_int32), ("per_cu", C.c_int32)]
+
+
+Launch = collections.namedtuple("Launch", [f for f, _ in ProfRecord._fields_])
 
 
 _SIGS = {
@@ -191,12 +196,13 @@ def profile_start():
 
 
 def profile_stop():
-    """List of (kernel_id, tri, nb, ms, flops, bytes) for the launches since profile_start()."""
+    """A Launch (kernel_id, tri, nb, ms, flops, bytes, m, n, k, workgroups, per_cu) per launch since
+    profile_start()."""
     n = C.c_int(0)
     check(lib().psgdk_profile_stop(None, 0, C.byref(n)))
     arr = (ProfRecord * max(1, n.value))()
     check(lib().psgdk_profile_stop(arr, n.value, C.byref(n)))
-    return [(r.kernel_id, r.tri, r.nb, r.ms, r.flops, r.bytes) for r in arr[:n.value]]
+    return [Launch(*(getattr(r, f) for f in Launch._fields)) for r in arr[:n.value]]
 
 
 def call_ws(fn, *args, ws, device, stream):

@@ -83,7 +83,8 @@ def build(jobs=None, verbose=False, asan=False):
         if err.strip() and verbose:
             print(err, file=sys.stderr)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *[o for o, _ in results]]
+    # --no-undefined: a symbol that no object defines fails the link, not the first dlopen
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-Wl,--no-undefined", "-o", tmp, *[o for o, _ in results]]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")

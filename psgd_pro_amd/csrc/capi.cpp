@@ -111,6 +111,8 @@ int check_dims(int64_t v, const char* name) {
 struct ProfRec {
   int kernel_id, tri, nb;
   double flops, bytes;
+  int64_t m = 0, n = 0, k = 0;
+  LaunchShape shape;
   hipEvent_t a, b;
 };
 struct Prof {  // one per host thread: a thread's records cover its own launches
@@ -125,6 +127,7 @@ struct Prof {  // one per host thread: a thread's records cover its own launches
   }
 };
 thread_local Prof g_prof;
+thread_local LaunchShape g_last_launch;  // set by psgdk::note_launch (end of this file)
 
 // Instantiation id of gemm_kernel<PREC, TA, TB, tile config>: cfg * 1000 + prec * 100 + adt * 10 + bdt.
 int kernel_id(int prec, int adt, int bdt, int cfg) { return cfg * 1000 + prec * 100 + adt * 10 + bdt; }
@@ -202,9 +205,14 @@ int run_gemm_general(int prec, int nb, int64_t M, int64_t N, int64_t K, const Op
   r.a = g_prof.ev();
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
+  g_last_launch = LaunchShape();
   PSGDK_HIP(hipEventRecord(r.a, st), "profiling event");
   PSGDK_TRY(hip_check(gemm_launch(a, prec, A.dt, B.dt, cfg, st), "gemm launch"));
   PSGDK_HIP(hipEventRecord(r.b, st), "profiling event");
+  r.m = M;
+  r.n = tri ? M : N;
+  r.k = K;
+  r.shape = last_launch();
   g_prof.recs.push_back(r);
   return PSGDK_OK;
 }
@@ -410,9 +418,16 @@ int run_b16(int nb, int64_t M, int64_t N, int64_t K, const void* const* A, int64
   r.a = g_prof.ev();
   r.b = g_prof.ev();
   if (!r.a || !r.b) return fail(PSGDK_EHIP, "profiling: hipEventCreate failed");
+  g_last_launch = LaunchShape();
   PSGDK_HIP(hipEventRecord(r.a, st), "profiling event");
   PSGDK_TRY(hip_check(launch(), "k-contiguous gemm launch"));
   PSGDK_HIP(hipEventRecord(r.b, st), "profiling event");
+  r.m = M;
+  r.n = tri ? M : N;
+  r.k = kper ? 0 : K;  // with k per problem: the largest
+  if (kper)
+    for (int b = 0; b < nb; ++b) r.k = kper[b] > r.k ? kper[b] : r.k;
+  r.shape = last_launch();
   g_prof.recs.push_back(r);
   return PSGDK_OK;
 }
@@ -1646,6 +1661,19 @@ int procrustes_run(int prec, int nb, int64_t d, const float* const* Q, float* co
 
 }  // namespace
 
+// The launchers in the kernel source files report each launch here (declared in common.h).
+void psgdk::note_launch(const void* fn, long long workgroups, int threads, int lds_bytes) {
+  if (!g_prof.on) return;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds_bytes) != hipSuccess) {
+    per_cu = 0;
+    (void)hipGetLastError();  // the query's error is not the launch's
+  }
+  g_last_launch.workgroups = (int)workgroups;
+  g_last_launch.per_cu = per_cu;
+}
+psgdk::LaunchShape psgdk::last_launch() { return g_last_launch; }
+
 int psgdk::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 // ==============================================================================================================
@@ -2420,6 +2448,11 @@ int psgdk_profile_stop(psgdk_prof_record_t* out, int max_records, int* n_records
     out[i].ms = ms;
     out[i].flops = r.flops;
     out[i].bytes = r.bytes;
+    out[i].m = r.m;
+    out[i].n = r.n;
+    out[i].k = r.k;
+    out[i].workgroups = r.shape.workgroups;
+    out[i].per_cu = r.shape.per_cu;
   }
   return PSGDK_OK;
 }

@@ -12,6 +12,16 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr float kSmallestNormal = 1.17549435e-38f;  // torch.finfo(torch.float32).smallest_normal
 
+// The calling thread's last MFMA-engine launch, for the launch profiler: the workgroups it launched and how many of
+// its kernel's workgroups one CU holds at once (the runtime's occupancy query for its block and LDS size; 0 when
+// that query fails). The launchers call note_launch after their hipGetLastError, and it does nothing unless the
+// calling thread is profiling.
+struct LaunchShape {
+  int workgroups = 0, per_cu = 0;
+};
+void note_launch(const void* fn, long long workgroups, int threads, int lds_bytes);
+LaunchShape last_launch();
+
 // Operand element addressing of a GEMM operand viewed as X[mn][k]:
 //   KC  : X[mn][k] at mn * ld + k   (k contiguous: A row-major M x K, or B given as N x K)
 //   MC  : X[mn][k] at k * ld + mn   (mn contiguous: A given as K x M, or B row-major K x N)

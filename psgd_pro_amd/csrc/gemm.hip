@@ -451,15 +451,15 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BK = Prec<PREC>::BK, CE = Prec<PREC>::CE, ESZ = Prec<PREC>::ESZ, KP = BK + CE;
   constexpr int smem = 2 * (BM + BN) * KP * ESZ;
   auto fn = gemm_kernel<PREC, TA, TB, BM, BN, WM, WN>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  // once per instantiation (a function-local static is initialised once, also under concurrent first calls)
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (attr != hipSuccess) return attr;
   const int G = a.ntiles * a.nb * a.splitk;
   hipLaunchKernelGGL(fn, dim3(G), dim3(WM * WN * 64), smem, st, a);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  note_launch(reinterpret_cast<const void*>(fn), G, WM * WN * 64, smem);
+  return e;
 }
 
 template <int PREC, typename TA, typename TB>

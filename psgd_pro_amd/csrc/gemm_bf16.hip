@@ -871,7 +871,9 @@ static hipError_t launch_b16(GB16Args& a, hipStream_t st) {
   a.tiles_n = (a.N + BN - 1) / BN;
   a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;
   hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(64 * (NW + PW)), smem, st, a);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  note_launch(reinterpret_cast<const void*>(fn), (long long)a.ntiles * a.nb, 64 * (NW + PW), smem);
+  return e;
 }
 
 template <typename T, int BM, int BN, int WGM, int WGN, int LAY = 0, int PW = 0>

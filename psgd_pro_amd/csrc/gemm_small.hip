@@ -392,6 +392,7 @@ hipError_t gemm_tiny_launch(const GB16Args& a, int esz, hipStream_t st) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  note_launch(reinterpret_cast<const void*>(fn), (long long)t.ntiles * a.nb, 256, 0);
   return hipSuccess;
 }
 
@@ -416,7 +417,9 @@ hipError_t gemm_small_launch(GB16Args& a, int esz, hipStream_t st) {
   a.tiles_n = (a.N + SM_T - 1) / SM_T;
   a.ntiles = a.tri ? a.tiles_m * (a.tiles_m + 1) / 2 : a.tiles_m * a.tiles_n;
   hipLaunchKernelGGL(fn, dim3(a.ntiles * a.nb), dim3(256), smem, st, a);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  note_launch(reinterpret_cast<const void*>(fn), (long long)a.ntiles * a.nb, 256, smem);
+  return e;
 }
 
 }  // namespace psgdk

@@ -589,6 +589,39 @@ def test_load_only_waves_give_the_same_sums(hip, kind, nb, m, n, k):
     check_gemm_bound(out[3][0].cpu(), X, Y.T)
 
 
+def test_launch_records_name_shape_and_occupancy(hip):
+    """The launch profiler's records carry each launch's problem shape, its workgroup count (tiles x problems) and
+    the occupancy the runtime reports for its kernel: one 256-tile workgroup per CU for configurations 0 and 3, two
+    128-tile workgroups of eight waves per CU for configuration 4 (the load-only-wave loop is built for that)."""
+    nb, m, n, k = 2, 520, 264, 1040
+    A = [rnd(m, k, seed=30 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
+    B = [rnd(n, k, seed=40 + i).to(torch.bfloat16).to(DEV) for i in range(nb)]
+    C = [torch.empty(m, m, device=DEV) for _ in range(nb)]
+    st = L.stream_of(A[0])
+    recs = {}
+    try:
+        for c in (0, 1, 3, 4):
+            L.check(hip.psgdk_set_option(1, c))
+            L.profile_start()
+            L.check(hip.psgdk_gemm(1, 0, 1, m, n, k, 1.0, 1, 1, nb, L.ptrs(A), k, L.ptrs(B), k, 0.0, L.ptrs(C), n,
+                                   st))
+            L.check(hip.psgdk_syrk(1, 0, L.OUT_MIRROR, m, k, 1, nb, L.ptrs(A), k, L.ptrs(C), m, st))
+            recs[c] = L.profile_stop()
+    finally:
+        L.check(hip.psgdk_set_option(1, -1))
+    for c, (g, s) in recs.items():
+        t = 128 if c in (1, 4) else 256
+        tm, tn = -(-m // t), -(-n // t)
+        assert (g.kernel_id, g.tri, g.nb, g.m, g.n, g.k) == (5000 + 10 * c, 0, nb, m, n, k), g
+        assert (s.kernel_id, s.tri, s.nb, s.m, s.n, s.k) == (5000 + 10 * c, 1, nb, m, m, k), s
+        assert g.workgroups == tm * tn * nb and s.workgroups == tm * (tm + 1) // 2 * nb, (g, s)
+        assert g.per_cu == s.per_cu >= 1, (g, s)
+        if c in (0, 3):
+            assert g.per_cu == 1, g
+        if c == 4:
+            assert g.per_cu == 2, g
+
+
 @pytest.mark.parametrize("nb,n,k", [(1, 768, 2304), (1, 3072, 768), (16, 1024, 256), (1, 200, 72)])
 def test_syrk_bf16_k_contiguous(hip, b16cfg, nb, n, k):
     As = [rnd(n, k, seed=i).to(torch.bfloat16).to(DEV) for i in range(nb)]

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     lib = L.lib()
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.psgdk_version() == 3
+    assert lib.psgdk_version() == 4
 
 
 def test_nm_exports():
