@@ -128,8 +128,10 @@ int psgdk_norm_lower_bound_full_noalloc(int64_t n, int sign, int nb, const void*
 
 /* norm_lower_bound_spd (psgd_pro.py:19-41) of P P^T (d x d) given P (d x k bf16, rows k-contiguous) and Pt = P^T
  * (k x d bf16), without forming P P^T: the squared row norms come from P (P^T P), the diagonal from the rows of P,
- * row j from P P_j^T, and each product V (P P^T) as (V P) P^T. The bound the bf16 update takes for term1 = Pg Pg^T
- * or Pg^T Pg when the other side k is under half of d. d and k multiples of 8, 16-byte aligned operands. */
+ * row j from P P_j^T. The subspace iteration runs in k-space: with X = V P, the product V (P P^T) is (X H) P^T for
+ * H = P^T P (k x k), and row r of V has squared norm X_r H X_r^T. So the start V0 is multiplied by P once and the
+ * four products are k x k products with H. The bound the bf16 update takes for term1 = Pg Pg^T or Pg^T Pg when the
+ * other side k is under half of d. d and k multiples of 8, 16-byte aligned operands. */
 int psgdk_norm_lower_bound_gram(int64_t d, int64_t k, int nb, const void* const* P, const void* const* Pt,
                                 const float* const* V, float* const* out, void* ws, size_t* ws_bytes,
                                 psgdk_stream_t stream);

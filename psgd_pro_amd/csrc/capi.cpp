@@ -620,10 +620,14 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
 }
 
 // The SPD bound of term1 = Pc Pc^T (d x d) from its factor Pc (d x k bf16 rows; Pr = Pc^T, k x d rows), without
-// forming term1: the same bound (psgd_pro.py:19-41) on the same matrix, the products associated the other way.
+// forming term1: the same bound (psgd_pro.py:19-41) on the same matrix, its products carried out in k-space.
 //   H = Pr Pr^T = Pc^T Pc (k x k, SYRK) -> Hb; W = Pc H -> Wb (d x k); row statistics of term1 (squared row norms
-//   rowsum(W * Pc), diagonal rowsum(Pc * Pc)); argmax j; row j of term1 = Pc Pc_j^T; V0 from it;
-//   4 x { U = V Pc (32 x k), V <- U Pc^T / nf (normalized every second time) }; bound and the consumer's scalars.
+//   rowsum(W * Pc), diagonal rowsum(Pc * Pc)); argmax j; row j of term1 = Pc Pc_j^T; V0 from it; U0 = V0 Pc.
+//   The bound's iterate V (32 x d) is X Pc^T with X = V Pc (32 x k): V term1 / nf = (X H / nf) Pc^T, and row r of
+//   V has squared norm X_r H X_r^T. So its four products V <- s (V term1 / nf) (s: the row normalization, every
+//   second product) are X <- s (X H / nf) on the k x k matrix H, starting from U0, with the row dots X H X^T in
+//   place of the sums of squares (the V A kernels' dot epilogue); the bound nf max_r ||V_r|| reads the last ones.
+//   One d x k read of Pc and four of the k x k H, against eight of Pc with the products through Pc and Pc^T.
 // Needs k, d multiples of 8 and 16-byte aligned operands (the bf16 update's Pg route: k < d / 2).
 int run_nlb_gram(int64_t d, int64_t k, int nb, const bf16_t* const* Pc, const bf16_t* const* Pr, bf16_t* const* Hb,
                  bf16_t* const* Wb, const float* const* V, const NlbFinal& fin, const NlbWs& w, hipStream_t st) {
@@ -656,26 +660,31 @@ int run_nlb_gram(int64_t d, int64_t k, int nb, const bf16_t* const* Pc, const bf
   a.vmm_cols = g_vmm_cols == 1 ? 1 : 2; a.ssc = 64; a.vmm_u = g_vmm_u == 2 ? 2 : 4;
   for (int b = 0; b < nb; ++b) { a.Vin[b] = V[b]; a.Vout[b] = w.vb0[b]; }
   PSGDK_HIP(nlb_full_launch(a, 1, 1, 0, st), "nlb init");
+  {
+    NlbArgs h1 = a;  // U0 = V0 Pc: A = Pr (k rows of d), 32 x k, no scale
+    h1.n = (int)k; h1.kdim = (int)d; h1.lda = d; h1.plain = 1;
+    for (int b = 0; b < nb; ++b) { h1.A[b] = reinterpret_cast<const float*>(Pr[b]); h1.Vin[b] = w.vb0[b]; h1.Vout[b] = w.part[b]; }
+    PSGDK_HIP(nlb_full_launch(h1, 2, 1, 0, st), "V Pc");
+  }
+  NlbArgs hx = a;  // X <- s (X H / nf): A = Hb (k x k, both triangles), row dots for the norms
+  hx.n = (int)k; hx.lda = k; hx.dot = 1;
   float* const* vb[2] = {w.vb0, w.vb1};
   float* const* ss[2] = {w.ss0, w.ss1};
   int cur = 0;
   for (int it = 0; it < 4; ++it) {
     const int normalize = it & 1;
-    NlbArgs h1 = a;  // U = V Pc: A = Pr (k rows of d), 32 x k, no scale
-    h1.n = (int)k; h1.kdim = (int)d; h1.lda = d; h1.plain = 1;
-    for (int b = 0; b < nb; ++b) { h1.A[b] = reinterpret_cast<const float*>(Pr[b]); h1.Vin[b] = vb[cur][b]; h1.Vout[b] = w.part[b]; }
-    PSGDK_HIP(nlb_full_launch(h1, 2, 1, 0, st), "V Pc");
-    NlbArgs h2 = a;  // V' = U Pc^T / nf: A = Pc (d rows of k)
-    h2.n = (int)d; h2.kdim = (int)k; h2.lda = k;
     for (int b = 0; b < nb; ++b) {
-      h2.A[b] = reinterpret_cast<const float*>(Pc[b]); h2.Vin[b] = w.part[b]; h2.Vout[b] = vb[cur ^ 1][b];
-      h2.ssin[b] = ss[0][b]; h2.ssout[b] = ss[normalize][b];
+      hx.A[b] = reinterpret_cast<const float*>(Hb[b]);
+      hx.Vin[b] = it == 0 ? w.part[b] : vb[cur][b];
+      hx.Vout[b] = vb[cur ^ 1][b];
+      hx.ssin[b] = ss[0][b];
+      hx.ssout[b] = ss[normalize][b];
     }
-    PSGDK_HIP(nlb_full_launch(h2, 2, 1, normalize, st), "U Pc^T");
+    PSGDK_HIP(nlb_full_launch(hx, 2, 1, normalize, st), "X H");
     cur ^= 1;
   }
-  for (int b = 0; b < nb; ++b) a.ssin[b] = ss[1][b];
-  PSGDK_HIP(nlb_final_launch(a, fin, st), "nlb_final");
+  for (int b = 0; b < nb; ++b) hx.ssin[b] = ss[1][b];  // k-space partials: ceil(k / 64) per row
+  PSGDK_HIP(nlb_final_launch(hx, fin, st), "nlb_final");
   return PSGDK_OK;
 }
 

@@ -23,6 +23,10 @@ struct NlbArgs {
                             // (ssc = 128)
   int kdim;                 // column kernel: k extent of a rectangular product (0: n)
   int plain;                // column kernel: no row scale and no sums of squares
+  int dot;                  // column and row kernels (square: kdim 0): the per-(row, column block) partials are
+                            // sum_c W[r][c] * s_r Vin[r][c] (s_r the row scale) instead of sum_c W[r][c]^2: with A
+                            // the Gram matrix H = P^T P of a factor P and X = s Vin, row r of X P^T has squared
+                            // norm X_r H X_r^T = sum_c (X H)_rc X_rc
   long long lda;
   const float* A[MAXB];     // n x n, upper triangle read
   const float* Vin[MAXB];   // init: the random start (32 x n)

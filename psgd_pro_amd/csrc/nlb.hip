@@ -807,11 +807,16 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
     w[4 * h + 3] = ((x0.w + x1.w) + x2.w) + x3.w;
   }
   const float sc = rs[row];
+  float x[8];  // dot: the scaled input row at these columns (square products: V is 32 x n)
+  if (p.dot) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = col + e < n ? sc * to_f32(V[(long long)row * n + col + e]) : 0.f;
+  }
   float sq = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     w[e] *= sc;
-    if (col + e < n) sq += w[e] * w[e];
+    if (col + e < n) sq += w[e] * (p.dot ? x[e] : w[e]);
   }
   T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
   if (col + 8 <= n) {
@@ -956,11 +961,16 @@ __global__ void __launch_bounds__(256) vmm_rows_kernel(const NlbArgs p, int norm
     float w[4] = {((x0.x + x1.x) + x2.x) + x3.x, ((x0.y + x1.y) + x2.y) + x3.y, ((x0.z + x1.z) + x2.z) + x3.z,
                   ((x0.w + x1.w) + x2.w) + x3.w};
     const float sc = rsl[row];
+    float x[4];  // dot: the scaled input row at these columns (square products: V is 32 x n)
+    if (p.dot) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = col + e < n ? sc * to_f32(V[(long long)row * n + col + e]) : 0.f;
+    }
     float sq = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       w[e] *= sc;
-      if (col + e < n) sq += w[e] * w[e];
+      if (col + e < n) sq += w[e] * (p.dot ? x[e] : w[e]);
     }
     T* __restrict__ W = reinterpret_cast<T*>(p.Vout[b]) + (long long)row * n + col;
     if (col + 4 <= n) {
