@@ -103,6 +103,32 @@ def test_nlb_uses_max_diag_for_spd_and_max_abs_for_skew():
     assert float(O.norm_lower_bound(Z, torch.randn(32, 5, dtype=torch.float64), skew=True)) == 0.0
 
 
+@pytest.mark.parametrize("d,k,seed", [(40, 8, 0), (96, 24, 1), (200, 48, 2)])
+def test_nlb_spd_of_a_gram_product_in_k_space(d, k, seed):
+    """The library's bound of A = P P^T (psgdk_norm_lower_bound_gram) never forms A. Its iterate V (32 x d) is kept as
+    X = V P (32 x k), each product V A / nf as X <- s (X H / nf) with H = P^T P, and each squared row norm of V as the
+    row dot of X H with X. In float64 that sequence gives the oracle's bound of P P^T to rounding."""
+    g = torch.Generator().manual_seed(seed)
+    P = torch.randn(d, k, generator=g, dtype=torch.float64) * torch.linspace(0.2, 2.0, k, dtype=torch.float64)
+    V = torch.randn(32, d, generator=g, dtype=torch.float64)
+    sn = O.smallest_normal(torch.float64)
+    H = P.T @ P
+    nf = (P * P).sum(dim=1).amax() + sn          # the diagonal of P P^T
+    j = int(torch.argmax(((P @ H) * P).sum(dim=1)))  # its squared row norms, rowsum((P H) * P)
+    row = (P @ P[j]) / nf                        # row j of P P^T / nf
+    V0 = row + torch.sgn((row * V).sum(dim=1, keepdim=True)) * V
+    Y = V0 @ P                                   # U0; the first product scales by 1 / nf
+    scale = torch.full((32, 1), 1 / float(nf), dtype=torch.float64)
+    for it in range(4):
+        X = scale * Y
+        Y = X @ H
+        dots = (Y * X).sum(dim=1, keepdim=True)  # squared row norms of the d-space iterate
+        scale = (1 / (dots.sqrt() + sn) if it % 2 == 0 else torch.ones_like(dots)) / nf
+    got = float(nf * dots.amax().sqrt())
+    want = float(O.norm_lower_bound(P @ P.T, V, skew=False))
+    assert got == pytest.approx(want, rel=1e-10)
+
+
 # --------------------------------------------------------------------------- Procrustes (psgd_pro.py:71-94)
 def test_procrustes_fixed_point_for_symmetric_q():
     A = spd(20, 5) / 20 + torch.eye(20, dtype=torch.float64)
