@@ -843,8 +843,8 @@ __global__ void __launch_bounds__(256) vmm_cols_kernel(const NlbArgs p, int norm
 // element s of every lane's piece at k = kk + 4 g + s for both operands); the next chunk's A and V loads are in
 // flight while a chunk is multiplied. The four waves' partial blocks are summed through LDS in the fixed order
 // w = 0..3, 16 rows of W at a time, and each row is scaled, stored and its sum of squares (of this column block)
-// written. The 32 KB of LDS (the staging buffer, which the epilogue reuses) let five workgroups share a CU, so the
-// 1152 workgroups of 24 matrices of 3072 columns run in one round.
+// written. The 32 KB of LDS (the staging buffer, which the epilogue reuses) would let five workgroups share a CU;
+// the 136 registers of the bf16 instantiation (three waves per SIMD) let three.
 // grid: nb * ceil(n / 64).
 constexpr int VR_ROWB = 512;                   // bytes of one row per chunk
 constexpr int VR_SMEM = VMC * VR_ROWB;         // the staging buffer: 64 rows x 512 bytes
