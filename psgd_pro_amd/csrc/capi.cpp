@@ -300,11 +300,13 @@ int batch_events(SideStreams* ss, size_t n) {
 
 // The 256-tile configuration needs most of the 256 CUs busy; with K >= 4096 its faster main loop pays for a
 // half-empty chip down to 128 tiles (one 4096 x 4096 SYRK, 136 tiles: 117 us against 133 us on 528 128-tiles).
-// Its warp-specialized main loop (cfg 3, option 12) gives the same sums; it is taken except for the two epilogues
-// that read two more operands per element (EPI_FACTOR, EPI_PROCB): with three waves per SIMD those spill registers
-// and run at half the epilogue's load depth, and lose more than the main loop gains (measured on the ViT-B step:
-// the d = 3072 SYRKs 907 -> 840 us, the PROCB products 1676 -> 1759 us). The 128-tile launches take the same loop
-// on 128 x 128 tiles (cfg 4) under the same rule (16 SYRKs of 768 x 3072: 67.9 -> 58.5 us).
+// Its warp-specialized main loop (cfg 3, option 12) gives the same sums; it is taken except for four epilogues:
+// the factor update (EPI_FACTOR, reading X1), both Procrustes steps (EPI_PROC, EPI_PROCB, reading X1 and X2) and
+// the r2 trace SYRK (EPI_STRACE). At three waves per SIMD their registers spill (11 to 118 registers per lane in
+// the code objects' metadata), they run at half the epilogue's load depth, and they lose more than the main loop
+// gains (measured on the ViT-B step: the d = 3072 SYRKs 907 -> 840 us, the PROCB products 1676 -> 1759 us). The
+// 128-tile launches take the same loop on 128 x 128 tiles (cfg 4) under the same rule (16 SYRKs of 768 x 3072:
+// 67.9 -> 58.5 us); there those four epilogues would exceed the 128 registers of two workgroups per CU.
 int b16_cfg(int64_t M, int64_t N, int64_t K, int tri, int nb, int epi) {
   if (g_force_cfg >= 0) return g_force_cfg;
   // the load-only-wave configurations 3 and 4, not for the epilogues that spill at their three waves per SIMD
