@@ -596,6 +596,7 @@ int run_nlb_full(int64_t n, int sign, int nb, const void* const* A, int64_t lda,
   // workgroups; smaller sets ran faster on the row kernel (measured crossovers), and option 4 = 3 forces it.
   const bool tri_ok = a.vmm_cols == 2 && a_bf16 && n % 128 == 0;
   if (tri_ok && (g_vmm_cols == 3 || (g_vmm_cols == -1 && nb >= 16 && (int64_t)nb * (n / 64) >= 512))) a.vmm_cols = 3;
+  a.vblk = a.vmm_cols == 3;  // the upper-tile kernel's V layout, from the init kernel on
   a.ssc = a.vmm_cols ? 64 : 128;
   if (a.vmm_cols && a.vmm_u == 8) a.vmm_u = 4;
   if (stats_in_part) PSGDK_HIP(nlb_full_launch(a, 3, a_bf16, 0, st), "row norms from partials");

@@ -22,6 +22,9 @@ struct NlbArgs {
                             // tournament-paired rounds (ssc = 64); 0 = split-K products plus a reduce kernel
                             // (ssc = 128)
   int kdim;                 // column kernel: k extent of a rectangular product (0: n)
+  int vblk;                 // init and upper-tile kernels: V (32 x n) stored in 16-column blocks, element (r, c)
+                            // at ((c / 16) 32 + r) 16 + c % 16, so that a wave's MFMA fragment of 32 rows x 16 k
+                            // is one contiguous 1 KB (n a multiple of 16)
   int plain;                // column kernel: no row scale and no sums of squares
   int dot;                  // column and row kernels (square: kdim 0): the per-(row, column block) partials are
                             // sum_c W[r][c] * s_r Vin[r][c] (s_r the row scale) instead of sum_c W[r][c]^2: with A

@@ -420,7 +420,9 @@ __global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
   const int j = sj;
   const float nf = snf;
   const float* __restrict__ vr = p.Vin[b] + (long long)r * n;
-  T* __restrict__ v0 = reinterpret_cast<T*>(p.Vout[b]) + (long long)r * n;
+  T* __restrict__ v0 = reinterpret_cast<T*>(p.Vout[b]);
+  // element k of row r of V0: row-major, or in 16-column blocks (vblk)
+  auto vat = [&](int k) { return p.vblk ? ((long long)(k >> 4) * NLB_K + r) * 16 + (k & 15) : (long long)r * n + k; };
   const bool vec = (n & 7) == 0 && (p.lda * (long long)sizeof(T)) % 16 == 0 &&
                    (reinterpret_cast<uintptr_t>(p.A[b]) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.Vin[b]) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(p.Vout[b]) & 15) == 0;
@@ -448,10 +450,10 @@ __global__ void __launch_bounds__(256) nlb_init_full_kernel(const NlbArgs p) {
       load8(vr + 8 * c, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = aval(a[e], 8 * c + e) + sg * v[e];
-      store8(v0 + 8 * c, a);
+      store8(v0 + vat(8 * c), a);  // 8 columns inside one 16-column block
     }
   } else {
-    for (int k = tid; k < n; k += 256) v0[k] = from_f32<T>(aval(to_f32<T>(arow[k]), k) + sg * vr[k]);
+    for (int k = tid; k < n; k += 256) v0[vat(k)] = from_f32<T>(aval(to_f32<T>(arow[k]), k) + sg * vr[k]);
   }
 }
 
@@ -1088,7 +1090,8 @@ hipError_t gram_launch(const GramArgs& a, int stage, hipStream_t st) {
 // b % 8), so the second read of a tile is an L2 hit. A loads-only probe of 24 matrices of 3072^2 read this way took
 // 34.5 us against 74.3 us for their full rows. A round stages the tile in LDS as stored (16-byte writes), then wave w
 // multiplies its k quarter of it with one v_mfma_f32_32x32x16_bf16 per 32-column half (V's 32 rows are one M tile;
-// V fragments straight from global memory): a tile (J, s) is [column][k] and its B fragments are 16-byte reads, a
+// V fragments straight from global memory, where V is kept in 16-column blocks (NlbArgs::vblk) so that a wave's
+// fragment is one contiguous 1 KB read): a tile (J, s) is [column][k] and its B fragments are 16-byte reads, a
 // tile (s, J) is [k][column] and its fragments come from gfx950's transposing LDS reads (ds_read_b64_tr_b16), the
 // sign folded in. VT_D rounds' loads are in flight, issued unconditionally (loads
 // past the last round re-read it) so that the compiler can count them; one barrier per round (two LDS buffers). The
@@ -1135,7 +1138,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
     const bf16_t* const t = A + (long long)(lo * VMC + (tid >> 3)) * lda + hi * VMC + (tid & 7) * 8;
     x.t0 = *reinterpret_cast<const u32x4*>(t);
     x.t1 = *reinterpret_cast<const u32x4*>(t + 32 * lda);  // v = tid + 256: 32 rows further
-    x.v = *reinterpret_cast<const u32x4*>(V + (long long)c * n + s * VMC + 16 * w + 8 * h);
+    // V in 16-column blocks: this wave's fragment (rows 0..31, k = 64 s + 16 w ..) is one contiguous 1 KB
+    x.v = *reinterpret_cast<const u32x4*>(V + ((long long)(4 * s + w) * NLB_K + c) * 16 + 8 * h);
   };
   f32x16_t acc[2];
 #pragma unroll
@@ -1217,7 +1221,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) v
       wv[e] *= sc;
       sq += wv[e] * wv[e];
     }
-    store4(reinterpret_cast<bf16_t*>(p.Vout[b]) + (long long)row * n + col, wv);
+    // W in 16-column blocks, as this kernel reads its V (4 columns inside one block)
+    store4(reinterpret_cast<bf16_t*>(p.Vout[b]) + ((long long)(col >> 4) * NLB_K + row) * 16 + (col & 15), wv);
     sq += __shfl_xor(sq, 1, 64);
     sq += __shfl_xor(sq, 2, 64);
     sq += __shfl_xor(sq, 4, 64);
