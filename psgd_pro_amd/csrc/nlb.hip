@@ -710,9 +710,9 @@ __global__ void __launch_bounds__(256) vmm_reduce_kernel(const NlbArgs p, int no
 // Operands come from 16-byte buffer loads straight into MFMA fragments, U steps issued together (the 16-byte layout
 // is required: n and the row stride multiples of 16 bytes, aligned bases, each matrix < 2 GiB; the host checks).
 // Epilogue: thread t owns row t / 8 and 8 consecutive columns: W in T (one 16- or 32-byte store) and
-// ssout[r][cb] = sum over the block's columns of W[r][c]^2, reduced over the row's 8 lanes in a fixed tree.
-// Rectangular products (kdim > 0): V is 32 x kdim, A is n x kdim, W is 32 x n; plain: no row scale and no sums of
-// squares (the first half of a product through a factor, V Pcol then (V Pcol) Pcol^T).
+// ssout[r][cb] = sum over the block's columns of W[r][c]^2 (dot: of W[r][c] times the scaled input), reduced over
+// the row's 8 lanes in a fixed tree. Rectangular products (kdim > 0): V is 32 x kdim, A is n x kdim, W is 32 x n;
+// plain: no row scale and no sums of squares (the Gram route's start U0 = V0 Pc).
 // grid: nb * ceil(n / 64).
 constexpr int VMC = 64;     // output columns per workgroup
 constexpr int VMC_LD = 68;  // LDS row stride (floats) of the partial blocks
