@@ -110,6 +110,7 @@ _SIGS = {
 }
 
 EXPORTED = tuple(_SIGS)
+ABI_VERSION = 4  # PSGDK_VERSION of include/psgdk.h that these signatures and structures follow
 
 _lib = None
 
@@ -126,6 +127,9 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        if L.psgdk_version() != ABI_VERSION:  # a stale build: its structures may not match these bindings
+            raise RuntimeError(f"psgd_pro_amd: {LIB_PATH} has ABI version {L.psgdk_version()}, the bindings expect "
+                               f"{ABI_VERSION}; rebuild it with `python -m psgd_pro_amd.build`")
         _lib = L
     return _lib
 

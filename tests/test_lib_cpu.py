@@ -27,7 +27,8 @@ def test_library_exports_every_declared_symbol():
     lib = L.lib()
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.psgdk_version() == 4
+    assert lib.psgdk_version() == L.ABI_VERSION
+    assert re.search(r"#define PSGDK_VERSION (\d+)", open(HEADER).read()).group(1) == str(L.ABI_VERSION)
 
 
 def test_nm_exports():
